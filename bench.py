@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Q8_0 path on the BASELINE workload (one JSON line).
+
+Metric: "Q8_0 Linear decode GB/s (% HBM peak); prefill TFLOP/s (% MFMA)
+@M=512".
+
+Workload of one step (the Llama-7B-shaped decode set): for each
+M in {1, 4, 8}, the five Q8_0 Linears [4096->12288] QKV, [4096->4096] o_proj,
+[4096->11008] gate, [4096->11008] up and [11008->4096] down, each a separate launch
+(15 launches), FP32 activations ~N(0,1), synthetic Q8_0 weights (int8 uniform in
+[-127,127], fp16 scales |N(0,1)|*0.02/127), no bias.  Inputs are resident in HBM before
+timing.  Weights rotate over R copies of the set (R * 215 MB >= 1 GiB) so that no
+launch finds its weights in the 256 MB Infinity Cache.
+
+value = algorithmic bytes of all launches / wall time of the timed steps (GB/s), with
+algorithmic bytes per launch = N*(K/32)*34 + 4*M*K + 4*M*N.
+
+Also reported: per-launch kernel durations (HIP events on the launch stream, >= 100
+launches each), the roofline of the dominant launch, the prefill GEMM of configs[2]
+(M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding gather of configs[4], and the
+reference's own CPU kernels timed on this host (cpu_baseline).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, 8 TB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, 2.5 PFLOP/s
+ROTATE_BYTES = 1 << 30          # >= 4x the 256 MB Infinity Cache
+
+LLAMA_SET = [("qkv", 12288, 4096), ("o_proj", 4096, 4096), ("gate", 11008, 4096),
+             ("up", 11008, 4096), ("down", 4096, 11008)]
+MS = (1, 4, 8)
+SEED_W = {"qkv": 21, "o_proj": 22, "gate": 23, "up": 24, "down": 25}
+
+
+def gemv_bytes(M, N, K):
+    return N * (K // 32) * 34 + 4 * M * K + 4 * M * N
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--launch-iters", type=int, default=120,
+                   help="launches per shape for the per-launch kernel timings")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true",
+                   help="skip the prefill and embedding figures")
+    return p.parse_args()
+
+
+def cpu_baseline(weights_host, xs_host):
+    """Time the reference's CPU kernels (oracle/_ref, else the C restatement) on the
+    M=1 and M=4 launches of one step (10 of the 15 launches, every row)."""
+    import oracle
+    if oracle.reference_available():
+        lib, kind = oracle.reference(), "reference"
+    else:
+        lib, kind = oracle.oracle(), "port"
+    total_bytes, t0 = 0, time.perf_counter()
+    for M in (1, 4):
+        for name, N, K in LLAMA_SET:
+            lib.sgemm_nt(xs_host[(M, K)], weights_host[name], M, N, K)
+            total_bytes += gemv_bytes(M, N, K)
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(total_bytes / dt / 1e9, 4), "unit": "GB/s",
+            "cores": min(4, threads), "kind": kind,
+            "sample": (f"M=1 and M=4 launches of one step (10 Q8_0 Linears, all rows) in "
+                       f"{dt:.1f} s; the reference parallelises over M only, so M=1 ran on 1 "
+                       f"thread and M=4 on 4 (OMP_NUM_THREADS={threads})")}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
+              "supported (no multi-GPU path exists in this round)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from llmengine_amd import capi
+    from llmengine_amd import synthetic as S
+
+    dev = torch.device("cuda:0")
+    capi.load()
+    stream = torch.cuda.current_stream()
+
+    # ---- inputs, resident in HBM before timing
+    set_bytes = sum(S.weight_bytes(N, K) for _, N, K in LLAMA_SET)
+    R = max(2, -(-ROTATE_BYTES // set_bytes) + 1)
+    weights_host, wdev = {}, {}
+    for name, N, K in LLAMA_SET:
+        w, _, _ = S.q8_0_weight(SEED_W[name], N, K)
+        weights_host[name] = w
+        base = torch.from_numpy(w).to(dev)
+        wdev[name] = [base] + [base.clone() for _ in range(R - 1)]
+    xs_host, xdev, ydev = {}, {}, {}
+    for M in MS:
+        for K in (4096, 11008):
+            xs_host[(M, K)] = S.activations(1000 + M, (M, K))
+            xdev[(M, K)] = torch.from_numpy(xs_host[(M, K)]).to(dev)
+        for name, N, K in LLAMA_SET:
+            ydev[(M, name)] = torch.empty((M, N), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    step_bytes = sum(gemv_bytes(M, N, K) for M in MS for _, N, K in LLAMA_SET)
+
+    def step(i):
+        for mi, M in enumerate(MS):
+            c = (i * len(MS) + mi) % R
+            for name, N, K in LLAMA_SET:
+                capi.linear(xdev[(M, K)], wdev[name][c], None, ydev[(M, name)], M, N, K,
+                            stream=stream)
+
+    # ---- timed steps
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    elapsed = max(wall, gpu_ms / 1e3)
+    value = step_bytes * args.steps / elapsed / 1e9
+
+    # ---- per-launch kernel durations (events around back-to-back launches)
+    per_launch = []
+    for M in MS:
+        for name, N, K in LLAMA_SET:
+            for j in range(3):  # warm
+                capi.linear(xdev[(M, K)], wdev[name][j % R], None, ydev[(M, name)], M, N, K,
+                            stream=stream)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for j in range(args.launch_iters):
+                capi.linear(xdev[(M, K)], wdev[name][j % R], None, ydev[(M, name)], M, N, K,
+                            stream=stream)
+            b.record(stream)
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / args.launch_iters
+            nbytes = gemv_bytes(M, N, K)
+            per_launch.append({"M": M, "op": name, "N": N, "K": K, "us": round(us, 3),
+                               "GBps": round(nbytes / us / 1e3, 1),
+                               "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+    dom = max(per_launch, key=lambda r: r["us"])
+    dom_bytes = gemv_bytes(dom["M"], dom["N"], dom["K"])
+    achieved = dom_bytes / dom["us"] / 1e3
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"gemv_q8_0 M={dom['M']} {dom['op']} [{dom['N']}x{dom['K']}]",
+                "bytes_per_launch": dom_bytes, "us_per_launch": dom["us"]}
+
+    extras = {}
+    if not args.no_extras:
+        # ---- prefill GEMM, configs[2]: M=512 on the bf16 MFMA path
+        pre = []
+        for name, N, K in (("gate", 11008, 4096), ("down", 4096, 11008)):
+            M = 512
+            x = torch.from_numpy(S.activations(2000 + K, (M, K))).to(dev)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            for j in range(3):
+                capi.linear(x, wdev[name][j % R], None, y, M, N, K, stream=stream)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            iters = 40
+            a.record(stream)
+            for j in range(iters):
+                capi.linear(x, wdev[name][j % R], None, y, M, N, K, stream=stream)
+            b.record(stream)
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / iters
+            tflops = 2.0 * M * N * K / us / 1e6
+            pre.append({"M": M, "N": N, "K": K, "us": round(us, 2),
+                        "TFLOPs": round(tflops, 1),
+                        "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)})
+        extras["prefill"] = pre
+        # ---- embedding gather, configs[4]
+        V, H, T = 151936, 896, 8 * 512
+        tbl = torch.from_numpy(S.q8_0_weight(5, V, H)[0]).to(dev)
+        Re = max(2, -(-ROTATE_BYTES // tbl.numel()) + 1)
+        tbls = [tbl] + [tbl.clone() for _ in range(Re - 1)]
+        ids = torch.from_numpy(S.token_ids(5, T, V)).to(dev)
+        out = torch.empty((T, H), dtype=torch.float32, device=dev)
+        for j in range(3):
+            capi.embedding(tbls[j % Re], ids, out, T, V, H, stream=stream)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        iters = 100
+        a.record(stream)
+        for j in range(iters):
+            capi.embedding(tbls[j % Re], ids, out, T, V, H, stream=stream)
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / iters
+        eb = T * (H // 32) * 34 + 4 * T + 4 * T * H
+        extras["embedding"] = {"T": T, "vocab": V, "hidden": H, "us": round(us, 2),
+                               "GBps": round(eb / us / 1e3, 1),
+                               "frac_hbm": round(eb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del tbls
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(weights_host, xs_host)
+
+    line = {
+        "metric": "Q8_0 Linear decode GB/s (% HBM peak); prefill TFLOP/s (% MFMA) @M=512",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (seeded BASELINE distributions; random Q8_0 weights)",
+        "config": {"workload": "configs[1]: Llama-7B decode Q8_0 Linear set, M in {1,4,8} x "
+                               "{QKV 4096->12288, o_proj 4096->4096, gate/up 4096->11008, "
+                               "down 11008->4096}, 15 launches per step",
+                   "rotated_weight_copies": R, "bytes_per_step": step_bytes,
+                   "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_launch": per_launch,
+    }
+    line.update(extras)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

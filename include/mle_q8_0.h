@@ -1,0 +1,129 @@
+/*
+ * mle_q8_0.h -- C ABI of the MI355X (gfx950) Q8_0 weight-only Linear / MatMul /
+ * Embedding kernels: the drop-in boundary for MiniLLMEngine's Q8_0 path.
+ *
+ * Library: llmengine_amd/libmle_q8_0.so (hand-written HIP kernels for gfx950).
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are DEVICE pointers (HIP device memory).  Q8_0 data is
+ *     the raw GGUF block_q8_0 stream: per 34-byte block a little-endian binary16
+ *     scale d followed by 32 int8 quants q; value = d * q.
+ *   - Work is enqueued on `stream` (NULL = the default stream) and is
+ *     asynchronous; the caller synchronises.  Nothing is allocated and nothing
+ *     is freed.  Entry points are re-entrant; calls writing the same output
+ *     buffer on different streams race, as with any kernel.
+ *   - Return value: 0 on success, else a value of the reference's ErrorCode
+ *     enum (include/minillm/core/status.h:20-32): 1 InvalidArgument,
+ *     2 OutOfRange, 3 ShapeMismatch, 4 Unsupported, 6 RuntimeError.  The
+ *     message of the last failure on the calling thread is mle_last_error().
+ *   - Alignment: fp32 activation/output buffers must be 16-byte aligned (any
+ *     hipMalloc'd buffer is), Q8_0 buffers 2-byte aligned, ids 4-byte aligned.
+ */
+#ifndef MLE_Q8_0_H
+#define MLE_Q8_0_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLE_OK 0
+#define MLE_INVALID_ARGUMENT 1
+#define MLE_OUT_OF_RANGE 2
+#define MLE_SHAPE_MISMATCH 3
+#define MLE_UNSUPPORTED 4
+#define MLE_RUNTIME_ERROR 6
+
+/* ABI revision of this header; bumped on any signature change. */
+int mle_q8_0_abi_version(void);
+
+/*
+ * Q8_0 Linear: y[M,N] = x[M,K] . W^T (+ bias[N]), W = [N,K] Q8_0 (blocks along K,
+ * row n starts at byte n*(K/32)*34).  FP32 activations, FP32 accumulation.
+ *
+ * Replaces minillm::cuda::sgemm_nt(const float* A, const uint8_t* B_q8_0,
+ * float* C, int M, int N, int K)  (reference include/minillm/runtime/kernels/
+ * cuda_kernels.h:16, src/runtime/kernels/cuda_kernels.cu:918-936) followed by
+ * minillm::cuda::add_bias(float*, const float*, int, int) (cuda_kernels.h:22),
+ * which this entry point fuses when `bias` is non-NULL (NULL = no bias).
+ *
+ * Paths: M <= 8 runs the FP32 decode GEMV; 8 < M < 64 runs the GEMV in chunks
+ * of 8 tokens; M >= 64 runs the bf16-MFMA prefill GEMM (relative L2 error vs
+ * FP32 about 2e-3).
+ * Errors: NULL x/w/y -> InvalidArgument; M, N or K <= 0 -> InvalidArgument;
+ * K % 32 != 0 -> Unsupported ("... requires K to be a multiple of 32").
+ */
+int mle_q8_0_linear(const float* x, const uint8_t* w_q8_0, const float* bias,
+                    float* y, int M, int N, int K, hipStream_t stream);
+
+/*
+ * Q8_0 MatMul: c[M,N] = a[M,K] . B[K,N], B = [K,N] Q8_0 stored row-major, so
+ * element (k,n) is flat index k*N+n and blocks run along N.
+ *
+ * Replaces minillm::cuda::sgemm(const float* A, const uint8_t* B_q8_0, float* C,
+ * int M, int N, int K)  (reference cuda_kernels.h:13, cuda_kernels.cu:852-868).
+ * Result is bit-identical to the reference CPU kernel cpu::sgemm(q8_0)
+ * (src/runtime/kernels/cpu_kernels.cpp:116-130).
+ * Errors: NULL pointers, non-positive sizes -> InvalidArgument;
+ * K % 32 != 0 or N % 32 != 0 -> Unsupported.
+ */
+int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M,
+                    int N, int K, hipStream_t stream);
+
+/*
+ * Q8_0 Embedding: out[s,h] = d*q of element h of table row ids[s]
+ * (table = [vocab, hidden] Q8_0, blocks along hidden).  Bit-identical to the
+ * reference CPU kernel cpu::embedding(q8_0) (cpu_kernels.cpp:286-295) for ids
+ * in [0, vocab); an id outside that range gives a row of +0.0f, as the
+ * reference device kernel does (cuda_kernels.cu:410-415).
+ *
+ * Replaces minillm::cuda::embedding(const uint8_t* weight_q8_0, const int* ids,
+ * float* out, int seq_len, int vocab_size, int hidden)  (reference
+ * cuda_kernels.h:37-38, cuda_kernels.cu:1054-1073).
+ * Errors: NULL pointers, seq_len < 0, vocab or hidden <= 0 -> InvalidArgument;
+ * hidden % 32 != 0 -> Unsupported.  seq_len == 0 is a no-op (as on the CPU path).
+ */
+int mle_q8_0_embedding(const uint8_t* table_q8_0, const int32_t* ids, float* out,
+                       int seq_len, int vocab, int hidden, hipStream_t stream);
+
+/*
+ * Message of the last failed call on this thread ("" if none).  Stands in for
+ * the message of the reference's Status return (status.h:34-59).  The pointer
+ * stays valid until the next call on the same thread.
+ */
+const char* mle_last_error(void);
+
+/*
+ * Raw Q8_0 byte size of a tensor with `numel` elements: ceil(numel/32)*34.
+ * Same rule as the reference's q8_required_bytes (src/runtime/kernels/
+ * cuda_kernel_adapter.cpp:86-97) and GGUFTensorInfo::bytes()
+ * (src/io/gguf_parser.cpp:226-243).  Returns 0 on overflow or numel < 0.
+ */
+size_t mle_q8_0_bytes(int64_t numel);
+
+/*
+ * Test / tuning hooks (no counterpart in the reference).
+ *
+ * mle_q8_0_f16_decode: out[i] = the scale value the kernels use for the
+ *   binary16 pattern bits[i] (exact; NaN canonicalised as the reference CPU
+ *   decode does, cpu_kernels.cpp:21-37).  Used for the exhaustive decode check.
+ * mle_q8_0_linear_ex: mle_q8_0_linear with the path forced (path 1 = FP32 GEMV
+ *   for any M, path 2 = bf16-MFMA GEMM for any M, 0 = automatic) and, for the
+ *   GEMV, an optional launch shape (mt in {1,2,4,8} >= min(M,8), lpr in
+ *   {16,32,64}, rw in {1,2,4,8}; all three 0 = automatic).
+ */
+int mle_q8_0_f16_decode(const uint16_t* bits, float* out, int64_t n,
+                        hipStream_t stream);
+int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
+                       float* y, int M, int N, int K, int path, int mt, int lpr,
+                       int rw, hipStream_t stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* MLE_Q8_0_H */

@@ -1,0 +1,143 @@
+"""ctypes binding of the C ABI in ``include/mle_q8_0.h`` (``libmle_q8_0.so``).
+
+This is plumbing for Python callers (tests, bench): device buffers come from PyTorch-ROCm
+tensors, the work runs in the HIP kernels of ``libmle_q8_0.so``.  There is no fallback:
+if the library is missing, every call raises.
+
+Each wrapper accepts torch tensors (or raw integer device addresses) and the HIP stream
+to launch on (default: torch's current stream).  Failures raise :class:`Q8_0Error`
+carrying the reference ``ErrorCode`` value and message; the ``*_status`` variants return
+``(code, message)`` instead, for error-path tests.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmle_q8_0.so")
+
+ERROR_NAMES = {0: "Ok", 1: "InvalidArgument", 2: "OutOfRange", 3: "ShapeMismatch",
+               4: "Unsupported", 5: "NotImplemented", 6: "RuntimeError"}
+
+EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
+            "mle_q8_0_matmul", "mle_q8_0_embedding", "mle_last_error", "mle_q8_0_bytes",
+            "mle_q8_0_f16_decode")
+
+
+class Q8_0Error(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERROR_NAMES.get(code, code)}: {message}")
+        self.code = code
+        self.message = message
+
+
+_lib = None
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+
+
+def load() -> ctypes.CDLL:
+    """Load libmle_q8_0.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m llmengine_amd.build` "
+            "(there is no CPU fallback for the Q8_0 path)")
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.mle_q8_0_abi_version.restype = _i
+    lib.mle_q8_0_abi_version.argtypes = []
+    lib.mle_q8_0_linear.restype = _i
+    lib.mle_q8_0_linear.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_q8_0_linear_ex.restype = _i
+    lib.mle_q8_0_linear_ex.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]
+    lib.mle_q8_0_matmul.restype = _i
+    lib.mle_q8_0_matmul.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_q8_0_embedding.restype = _i
+    lib.mle_q8_0_embedding.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_last_error.restype = ctypes.c_char_p
+    lib.mle_last_error.argtypes = []
+    lib.mle_q8_0_bytes.restype = ctypes.c_size_t
+    lib.mle_q8_0_bytes.argtypes = [ctypes.c_int64]
+    lib.mle_q8_0_f16_decode.restype = _i
+    lib.mle_q8_0_f16_decode.argtypes = [_vp, _vp, ctypes.c_int64, _vp]
+    _lib = lib
+    return lib
+
+
+def _addr(t) -> int | None:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def last_error() -> str:
+    return load().mle_last_error().decode()
+
+
+def _status(rc: int):
+    return rc, (last_error() if rc else "")
+
+
+def _raise(rc: int):
+    if rc != 0:
+        raise Q8_0Error(rc, last_error())
+
+
+def linear_status(x, w, bias, y, M, N, K, stream=None):
+    rc = load().mle_q8_0_linear(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K,
+                                _stream(stream))
+    return _status(rc)
+
+
+def linear(x, w, bias, y, M, N, K, stream=None) -> None:
+    """y[M,N] = x[M,K] . W^T (+ bias); W raw Q8_0 [N,K]."""
+    _raise(linear_status(x, w, bias, y, M, N, K, stream)[0])
+
+
+def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, stream=None) -> None:
+    rc = load().mle_q8_0_linear_ex(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K,
+                                   path, mt, lpr, rw, _stream(stream))
+    _raise(rc)
+
+
+def matmul_status(a, b, c, M, N, K, stream=None):
+    rc = load().mle_q8_0_matmul(_addr(a), _addr(b), _addr(c), M, N, K, _stream(stream))
+    return _status(rc)
+
+
+def matmul(a, b, c, M, N, K, stream=None) -> None:
+    """c[M,N] = a[M,K] . B[K,N]; B raw Q8_0 [K,N] with blocks along N."""
+    _raise(matmul_status(a, b, c, M, N, K, stream)[0])
+
+
+def embedding_status(w, ids, out, seq_len, vocab, hidden, stream=None):
+    rc = load().mle_q8_0_embedding(_addr(w), _addr(ids), _addr(out), seq_len, vocab,
+                                   hidden, _stream(stream))
+    return _status(rc)
+
+
+def embedding(w, ids, out, seq_len, vocab, hidden, stream=None) -> None:
+    """out[s,h] = dequantised row ids[s] of a raw Q8_0 [vocab, hidden] table."""
+    _raise(embedding_status(w, ids, out, seq_len, vocab, hidden, stream)[0])
+
+
+def f16_decode(bits, out, n, stream=None) -> None:
+    _raise(load().mle_q8_0_f16_decode(_addr(bits), _addr(out), n, _stream(stream)))
+
+
+def q8_0_bytes(numel: int) -> int:
+    return load().mle_q8_0_bytes(numel)

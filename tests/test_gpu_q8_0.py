@@ -1,0 +1,306 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars (stated per test): Embedding and MatMul bit-exact; Linear on the FP32 GEMV path
+(M <= 63) relative L2 <= 1e-5; Linear on the bf16-MFMA path (M >= 64) relative L2
+<= 1e-2.  Full BASELINE sizes are covered either directly against the oracle (where it
+finishes in seconds) or through size-independent properties (agreement of the two
+Linear paths, determinism, linearity).
+"""
+import functools
+
+import numpy as np
+import pytest
+
+from helpers import (assert_bitexact, bits, empty_f32, note, rel_l2, sha, to_dev,
+                     to_host)
+from llmengine_amd import capi
+from llmengine_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-5
+MFMA_TOL = 1e-2
+
+
+@functools.lru_cache(maxsize=None)
+def weight(seed, rows, cols):
+    w, _, _ = S.q8_0_weight(seed, rows, cols)
+    return w
+
+
+@functools.lru_cache(maxsize=None)
+def acts(seed, rows, cols, tag=S.TAG_X):
+    return S.activations(seed, (rows, cols), tag=tag)
+
+
+def run_linear(dev, x, w, bias, M, N, K, path=0, mt=0, lpr=0, rw=0):
+    dx, dw = to_dev(x, dev), to_dev(w, dev)
+    db = to_dev(bias, dev) if bias is not None else None
+    dy = empty_f32((M, N), dev)
+    if path == 0 and mt == 0:
+        capi.linear(dx, dw, db, dy, M, N, K)
+    else:
+        capi.linear_ex(dx, dw, db, dy, M, N, K, path=path, mt=mt, lpr=lpr, rw=rw)
+    return to_host(dy)
+
+
+# ----------------------------------------------------------------------------- decode
+
+def test_f16_scale_decode_exhaustive(dev, orc):
+    import torch
+    note("f16 decode, all 65536 patterns")
+    pat = torch.arange(65536, dtype=torch.int32, device=dev).to(torch.int16).view(torch.uint16)
+    out = empty_f32((65536,), dev)
+    capi.f16_decode(pat, out, 65536)
+    got = to_host(out)
+    want = orc.f16_table()
+    assert np.array_equal(bits(got), bits(want))  # NaNs canonicalised like the reference
+
+
+# ----------------------------------------------------------------------------- embedding
+
+def test_embedding_known_answers(dev, orc, golden):
+    for c in golden["cases"]:
+        if not (c.get("known_answer") and c["op"] == "embedding"):
+            continue
+        note(c["name"])
+        Q = np.array(c["quants"], np.int8)
+        table = S.pack_q8_0_const_scale(Q, c["scale_bits"])
+        ids = np.array(c["ids"], np.int32)
+        out = empty_f32((ids.size, c["hidden"]), dev)
+        capi.embedding(to_dev(table, dev), to_dev(ids, dev), out, ids.size, c["vocab"], c["hidden"])
+        got = to_host(out)
+        assert sha(got) == c["sha256"]
+
+
+def test_embedding_c5_full_bitexact(dev, orc, golden):
+    """Config 5: table [151936, 896], 8 x 512 ids; every output bit checked."""
+    c = next(c for c in golden["cases"] if c["name"] == "embedding_c5_151936x896_4096")
+    note("embedding C5 full")
+    w = weight(c["seed"], c["vocab"], c["hidden"])
+    ids = S.token_ids(c["seed"], c["n_ids"], c["vocab"])
+    out = empty_f32((ids.size, c["hidden"]), dev)
+    capi.embedding(to_dev(w, dev), to_dev(ids, dev), out, ids.size, c["vocab"], c["hidden"])
+    got = to_host(out)
+    assert_bitexact(got, orc.embedding(w, ids, c["hidden"]), "C5")
+    assert sha(got) == c["sha256"]
+
+
+@pytest.mark.parametrize("vocab,hidden,n", [(1, 32, 1), (3, 32, 7), (257, 64, 100),
+                                            (1000, 896, 513), (77, 4096, 33)])
+def test_embedding_ragged_bitexact(dev, orc, vocab, hidden, n):
+    note(f"embedding vocab={vocab} hidden={hidden} n={n}")
+    w = weight(50 + vocab, vocab, hidden)
+    ids = S.token_ids(51 + n, n, vocab)
+    ids[-1] = vocab - 1  # always touch the last row, the last bytes of the table
+    out = empty_f32((n, hidden), dev)
+    capi.embedding(to_dev(w, dev), to_dev(ids, dev), out, n, vocab, hidden)
+    assert_bitexact(to_host(out), orc.embedding(w, ids, hidden))
+
+
+def test_embedding_out_of_range_ids_give_zero_rows(dev, orc):
+    vocab, hidden = 40, 64
+    w = weight(52, vocab, hidden)
+    ids = np.array([3, -1, 39, 40, 7, 2 ** 31 - 1, -2 ** 31, 0], np.int32)
+    note("embedding invalid ids")
+    out = empty_f32((ids.size, hidden), dev)
+    capi.embedding(to_dev(w, dev), to_dev(ids, dev), out, ids.size, vocab, hidden)
+    assert_bitexact(to_host(out), orc.embedding_zero_fill(w, ids, vocab, hidden))
+
+
+def test_embedding_special_scales(dev, orc):
+    """Every binary16 class as a scale, with signed zeros: bit-exact except that
+    NaN outputs are compared by position (x86 and AMD differ on the sign of the
+    NaN produced by Inf * 0)."""
+    specials = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x0400, 0x3C00, 0x7BFF,
+                         0xFBFF, 0x7C00, 0xFC00, 0x7E00, 0x7C01, 0xFE00, 0x13FF, 0x8200],
+                        np.uint16)
+    q = S.quants(53, specials.size * 32)
+    q[::7] = 0
+    table = S.pack_q8_0(q, specials.view(np.float16))
+    ids = np.arange(specials.size, dtype=np.int32)[::-1].copy()
+    note("embedding special scales")
+    out = empty_f32((ids.size, 32), dev)
+    capi.embedding(to_dev(table, dev), to_dev(ids, dev), out, ids.size, specials.size, 32)
+    assert_bitexact(to_host(out), orc.embedding(table, ids, 32))
+
+
+def test_embedding_empty_is_noop(dev):
+    w = to_dev(weight(54, 4, 32), dev)
+    ids = to_dev(np.zeros(1, np.int32), dev)
+    out = empty_f32((1, 32), dev)
+    capi.embedding(w, ids, out, 0, 4, 32)
+    assert np.all(np.isnan(to_host(out)))
+
+
+# ----------------------------------------------------------------------------- linear GEMV
+
+def test_linear_known_answers_exact(dev, golden):
+    """Integer quants x dyadic activations: every partial sum is exact, so the GPU
+    must reproduce the reference's bits whatever its summation order."""
+    for c in golden["cases"]:
+        if not (c.get("known_answer") and c["op"] == "linear"):
+            continue
+        note(c["name"])
+        Q = np.array(c["quants"], np.int8)
+        w = S.pack_q8_0_const_scale(Q, c["scale_bits"])
+        x = np.array(c["activations"], np.float32).reshape(c["M"], c["K"])
+        for path in (1, 2):
+            got = run_linear(dev, x, w, None, c["M"], c["N"], c["K"], path=path)
+            if path == 1:
+                assert sha(got) == c["sha256"], (c["name"], path)
+            else:  # bf16 MFMA: dyadic inputs with <= 8 significant bits stay exact
+                assert sha(got) == c["sha256"], (c["name"], path)
+
+
+def test_linear_c1_full(dev, orc):
+    M, N, K = 1, 4096, 4096
+    note("linear C1 1x4096x4096")
+    w, x = weight(1, N, K), acts(1, M, K)
+    got = run_linear(dev, x, w, None, M, N, K)
+    assert rel_l2(got, orc.sgemm_nt(x, w, M, N, K)) <= GEMV_TOL
+
+
+C2_SHAPES = [(12288, 4096), (4096, 4096), (11008, 4096), (4096, 11008)]
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+@pytest.mark.parametrize("N,K", C2_SHAPES)
+def test_linear_c2_llama_decode(dev, orc, M, N, K):
+    note(f"linear C2 M={M} N={N} K={K}")
+    w, x = weight(2, N, K), acts(2 + M, M, K)
+    got = run_linear(dev, x, w, None, M, N, K)
+    err = rel_l2(got, orc.sgemm_nt(x, w, M, N, K))
+    assert err <= GEMV_TOL, err
+
+
+@pytest.mark.parametrize("N,K,M", [(1152, 896, 1), (4864, 896, 1), (896, 4864, 1),
+                                   (151936, 896, 1), (151936, 896, 8)])
+def test_linear_c4_qwen_decode(dev, orc, N, K, M):
+    note(f"linear C4 M={M} N={N} K={K}")
+    w, x = weight(4, N, K), acts(4 + M, M, K)
+    got = run_linear(dev, x, w, None, M, N, K)
+    err = rel_l2(got, orc.sgemm_nt(x, w, M, N, K))
+    assert err <= GEMV_TOL, err
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 32), (2, 3, 64), (3, 7, 96), (5, 33, 992),
+                                   (8, 1000, 512), (6, 129, 2080), (1, 515, 11008),
+                                   (9, 40, 256), (17, 65, 1024), (63, 100, 320)])
+def test_linear_ragged_with_bias(dev, orc, M, N, K):
+    note(f"linear ragged M={M} N={N} K={K}")
+    w, x = weight(60 + N, N, K), acts(61 + K, M, K)
+    bias = S.activations(62, (N,), tag=S.TAG_BIAS)
+    got = run_linear(dev, x, w, bias, M, N, K)
+    err = rel_l2(got, orc.linear(x, w, bias, M, N, K))
+    assert err <= GEMV_TOL, err
+
+
+def test_linear_every_gemv_launch_shape(dev, orc):
+    """All (mt, lpr, rw) instantiations on a ragged shape, M from 1 to mt."""
+    N, K = 77, 1312
+    w = weight(70, N, K)
+    for mt in (1, 2, 4, 8):
+        M = max(1, mt - 1) if mt > 1 else 1
+        x = acts(71 + M, M, K)
+        want = orc.sgemm_nt(x, w, M, N, K)
+        for lpr in (16, 32, 64):
+            for rw in (1, 2, 4, 8):
+                note(f"gemv shape mt={mt} lpr={lpr} rw={rw} M={M}")
+                got = run_linear(dev, x, w, None, M, N, K, path=1, mt=mt, lpr=lpr, rw=rw)
+                assert rel_l2(got, want) <= GEMV_TOL, (mt, lpr, rw)
+
+
+def test_linear_gemv_deterministic_and_linear(dev):
+    """lm_head [151936, 896] at M=8: bitwise repeatable, and linear in x."""
+    import torch
+    N, K, M = 151936, 896, 8
+    note("gemv determinism/linearity lm_head")
+    dw = to_dev(weight(4, N, K), dev)
+    x1, x2 = acts(80, M, K), acts(81, M, K)
+    d1, d2, d12 = to_dev(x1, dev), to_dev(x2, dev), to_dev(x1 + x2, dev)
+    y1a, y1b, y2, y12 = (empty_f32((M, N), dev) for _ in range(4))
+    capi.linear(d1, dw, None, y1a, M, N, K)
+    capi.linear(d1, dw, None, y1b, M, N, K)
+    capi.linear(d2, dw, None, y2, M, N, K)
+    capi.linear(d12, dw, None, y12, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(y1a, y1b)
+    assert rel_l2(to_host(y12), to_host(y1a) + to_host(y2)) <= GEMV_TOL
+
+
+# ----------------------------------------------------------------------------- linear MFMA
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (65, 130, 96), (128, 128, 128),
+                                   (200, 333, 512), (64, 1, 32), (300, 257, 4096)])
+def test_linear_mfma_ragged_with_bias(dev, orc, M, N, K):
+    note(f"mfma ragged M={M} N={N} K={K}")
+    w, x = weight(90 + N, N, K), acts(91 + K, M, K)
+    bias = S.activations(92, (N,), tag=S.TAG_BIAS)
+    got = run_linear(dev, x, w, bias, M, N, K)
+    err = rel_l2(got, orc.linear(x, w, bias, M, N, K))
+    assert err <= MFMA_TOL, err
+
+
+@pytest.mark.parametrize("N,K", [(11008, 4096), (4096, 11008)])
+def test_linear_c3_prefill_full(dev, orc, N, K):
+    """Config 3 at full size (M=512): sampled rows against the oracle, the whole
+    output against the FP32 GEMV path (itself pinned to the oracle at 1e-5)."""
+    import torch
+    M = 512
+    note(f"mfma C3 M={M} N={N} K={K}")
+    w, x = weight(3, N, K), acts(3, M, K)
+    dx, dw = to_dev(x, dev), to_dev(w, dev)
+    y_mfma, y_fp32 = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    capi.linear(dx, dw, None, y_mfma, M, N, K)
+    capi.linear_ex(dx, dw, None, y_fp32, M, N, K, path=1)
+    torch.cuda.synchronize()
+    got, fp32 = to_host(y_mfma), to_host(y_fp32)
+    rows = np.array([0, 1, 255, 511])
+    want_rows = orc.sgemm_nt(x[rows], w, rows.size, N, K)
+    assert rel_l2(fp32[rows], want_rows) <= GEMV_TOL
+    assert rel_l2(got[rows], want_rows) <= MFMA_TOL
+    assert rel_l2(got, fp32) <= MFMA_TOL
+    y_again = empty_f32((M, N), dev)
+    capi.linear(dx, dw, None, y_again, M, N, K)
+    assert torch.equal(y_again, y_mfma)
+
+
+# ----------------------------------------------------------------------------- matmul
+
+def test_matmul_known_answers(dev, golden):
+    for c in golden["cases"]:
+        if not (c.get("known_answer") and c["op"] == "matmul"):
+            continue
+        if c["K"] % 32:
+            continue  # the device path requires K % 32 == 0 (cuda_kernels.cu:856-858)
+        note(c["name"])
+        Q = np.array(c["quants"], np.int8)
+        b = S.pack_q8_0_const_scale(Q, c["scale_bits"])
+        a = np.array(c["activations"], np.float32).reshape(c["M"], c["K"])
+        out = empty_f32((c["M"], c["N"]), dev)
+        capi.matmul(to_dev(a, dev), to_dev(b, dev), out, c["M"], c["N"], c["K"])
+        assert sha(to_host(out)) == c["sha256"]
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 32, 32), (3, 64, 160), (5, 256, 512), (1, 32, 4096),
+                                   (8, 1024, 96), (33, 96, 64)])
+def test_matmul_bitexact(dev, orc, M, N, K):
+    note(f"matmul M={M} N={N} K={K}")
+    b, a = weight(100 + N, K, N), acts(101 + K, M, K)
+    out = empty_f32((M, N), dev)
+    capi.matmul(to_dev(a, dev), to_dev(b, dev), out, M, N, K)
+    assert_bitexact(to_host(out), orc.sgemm(a, b, M, N, K), f"matmul {M}x{N}x{K}")
+
+
+# ----------------------------------------------------------------------------- errors
+
+def test_device_error_paths(dev):
+    x = to_dev(acts(110, 1, 64), dev)
+    w = to_dev(weight(110, 2, 64), dev)
+    y = empty_f32((1, 2), dev)
+    code, msg = capi.linear_status(x, w, None, y, 1, 2, 31)
+    assert code == 4 and "Q8_0" in msg and "32" in msg
+    with pytest.raises(capi.Q8_0Error) as e:
+        capi.matmul(x, w, y, 1, 2, 64)
+    assert e.value.code == 4
