@@ -25,16 +25,86 @@
 namespace mle {
 namespace {
 
+constexpr int kXPad = 36;  // floats per staged 32-activation block (144 B: conflict-free)
+
+template <int RW>
+__device__ __forceinline__ void load_rows(Block (&blk)[RW], const uint8_t* __restrict__ w,
+                                          const int64_t (&row_off)[RW], int b) {
+#pragma unroll
+  for (int r = 0; r < RW; ++r) blk[r] = load_block(w + row_off[r] + (int64_t)b * kBlockBytes);
+}
+
+// One lane's contribution of block `blk[r]` (activations from LDS) to acc[m][r].
+template <int MT, int RW>
+__device__ __forceinline__ void consume(float (&acc)[MT][RW], const Block (&blk)[RW],
+                                        const float* __restrict__ xb, int xm_stride) {
+  float part[MT][RW];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) part[m][r] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    f32x4 xv[MT][2];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const f32x4* xp = reinterpret_cast<const f32x4*>(xb + m * xm_stride + 8 * c);
+      xv[m][0] = xp[0];
+      xv[m][1] = xp[1];
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const uint32_t q0 = blk[r].q[2 * c];
+      const uint32_t q1 = blk[r].q[2 * c + 1];
+      float qf[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qf[j] = q_at(q0, j);
+        qf[4 + j] = q_at(q1, j);
+      }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float s = part[m][r];
+        s = __builtin_fmaf(xv[m][0].x, qf[0], s);
+        s = __builtin_fmaf(xv[m][0].y, qf[1], s);
+        s = __builtin_fmaf(xv[m][0].z, qf[2], s);
+        s = __builtin_fmaf(xv[m][0].w, qf[3], s);
+        s = __builtin_fmaf(xv[m][1].x, qf[4], s);
+        s = __builtin_fmaf(xv[m][1].y, qf[5], s);
+        s = __builtin_fmaf(xv[m][1].z, qf[6], s);
+        s = __builtin_fmaf(xv[m][1].w, qf[7], s);
+        part[m][r] = s;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const float d = scale_to_f32_fast(blk[r].scale_bits);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m][r] = __builtin_fmaf(d, part[m][r], acc[m][r]);
+  }
+}
+
+// Activations are staged in LDS one K-chunk of `ckb` blocks at a time, as
+// [token][block][kXPad] floats; rows of weights stream straight from HBM.
 template <int MT, int LPR, int RW>
 __global__ __launch_bounds__(256) void gemv_q8_0_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w,
-    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K) {
+    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int ckb) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];
   constexpr int G = 256 / LPR;  // lane groups per workgroup
   const int li = threadIdx.x % LPR;
   const int grp = threadIdx.x / LPR;
   const int64_t row0 = ((int64_t)blockIdx.x * G + grp) * RW;
   const int KB = K / kBlockElems;
   const int64_t row_bytes = (int64_t)KB * kBlockBytes;
+  const int xm_stride = ckb * kXPad;
+
+  // Rows past N are clamped to row N-1 so that every weight load is
+  // unconditional (loads issue back to back); their results are dropped.
+  int64_t row_off[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) row_off[r] = (row0 + r < N ? row0 + r : (int64_t)N - 1) * row_bytes;
 
   float acc[MT][RW];
 #pragma unroll
@@ -42,74 +112,34 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(
 #pragma unroll
     for (int r = 0; r < RW; ++r) acc[m][r] = 0.0f;
 
-  bool row_ok[RW];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) row_ok[r] = (row0 + r) < N;
+  for (int c0 = 0; c0 < KB; c0 += ckb) {
+    const int cend = c0 + ckb < KB ? c0 + ckb : KB;
+    // Issue this lane's first weight loads before waiting on the barrier.
+    int b = c0 + li;
+    Block cur[RW];
+    if (b < cend) load_rows<RW>(cur, w, row_off, b);
 
-  for (int b = li; b < KB; b += LPR) {
-    Block blk[RW];
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      if (row_ok[r]) {
-        blk[r] = load_block(w + (row0 + r) * row_bytes + (int64_t)b * kBlockBytes);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) blk[r].q[i] = 0u;
-        blk[r].scale_bits = 0u;
+    __syncthreads();  // the previous chunk's readers are done with xs
+    {
+      const int nquads = (cend - c0) * 8;  // float4s per token in this chunk
+      for (int i = threadIdx.x; i < M * nquads; i += 256) {
+        const int m = i / nquads;
+        const int qd = i - m * nquads;
+        const int bb = qd >> 3, j = qd & 7;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(
+            x + (int64_t)m * K + (int64_t)(c0 + bb) * kBlockElems + 4 * j);
+        *reinterpret_cast<f32x4*>(xs + m * xm_stride + bb * kXPad + 4 * j) = v;
       }
     }
-    float part[MT][RW];
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int r = 0; r < RW; ++r) part[m][r] = 0.0f;
+    __syncthreads();
 
-    // Activations in quarters of a block (8 values per token) to bound VGPRs.
+    for (; b < cend; b += LPR) {
+      Block nxt[RW];
+      const int bn = b + LPR;
+      if (bn < cend) load_rows<RW>(nxt, w, row_off, bn);
+      consume<MT, RW>(acc, cur, xs + (b - c0) * kXPad, xm_stride);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      f32x4 xv[MT][2];
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m < M) {
-          const f32x4* xp = reinterpret_cast<const f32x4*>(
-              x + (int64_t)m * K + (int64_t)b * kBlockElems + 8 * c);
-          xv[m][0] = xp[0];
-          xv[m][1] = xp[1];
-        } else {
-          xv[m][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-          xv[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        const uint32_t q0 = blk[r].q[2 * c];
-        const uint32_t q1 = blk[r].q[2 * c + 1];
-        float qf[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          qf[j] = q_at(q0, j);
-          qf[4 + j] = q_at(q1, j);
-        }
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          float s = part[m][r];
-          s = __builtin_fmaf(xv[m][0].x, qf[0], s);
-          s = __builtin_fmaf(xv[m][0].y, qf[1], s);
-          s = __builtin_fmaf(xv[m][0].z, qf[2], s);
-          s = __builtin_fmaf(xv[m][0].w, qf[3], s);
-          s = __builtin_fmaf(xv[m][1].x, qf[4], s);
-          s = __builtin_fmaf(xv[m][1].y, qf[5], s);
-          s = __builtin_fmaf(xv[m][1].z, qf[6], s);
-          s = __builtin_fmaf(xv[m][1].w, qf[7], s);
-          part[m][r] = s;
-        }
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const float d = scale_to_f32_fast(blk[r].scale_bits);
-#pragma unroll
-      for (int m = 0; m < MT; ++m) acc[m][r] = __builtin_fmaf(d, part[m][r], acc[m][r]);
+      for (int r = 0; r < RW; ++r) cur[r] = nxt[r];
     }
   }
 
@@ -125,7 +155,7 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(
   if (li == 0) {
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-      if (!row_ok[r]) continue;
+      if (row0 + r >= N) continue;
       const float bv = bias ? bias[row0 + r] : 0.0f;
 #pragma unroll
       for (int m = 0; m < MT; ++m)
@@ -134,13 +164,25 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(
   }
 }
 
+constexpr int kXLdsBudget = 48 * 1024;  // bytes of staged activations per workgroup
+
 template <int MT, int LPR, int RW>
 hipError_t launch_one(const float* x, const uint8_t* w, const float* bias, float* y,
                       int M, int N, int K, hipStream_t stream) {
   constexpr int rows_per_wg = (256 / LPR) * RW;
   const int64_t grid = ((int64_t)N + rows_per_wg - 1) / rows_per_wg;
+  const int KB = K / kBlockElems;
+  // Chunk of blocks staged per pass: whole K if it fits, else a multiple of LPR.
+  int ckb = kXLdsBudget / (MT * kXPad * 4);
+  if (ckb >= KB) {
+    ckb = KB;
+  } else {
+    ckb = ckb / LPR * LPR;
+    if (ckb < LPR) ckb = LPR;
+  }
+  const size_t lds = (size_t)MT * ckb * kXPad * sizeof(float);
   hipLaunchKernelGGL((gemv_q8_0_kernel<MT, LPR, RW>), dim3((unsigned)grid), dim3(256),
-                     0, stream, x, w, bias, y, M, N, K);
+                     lds, stream, x, w, bias, y, M, N, K, ckb);
   return hipGetLastError();
 }
 
@@ -178,30 +220,15 @@ bool gemv_config_valid(const GemvConfig& c) {
 }
 
 GemvConfig gemv_pick_config(int M, int N, int K) {
+  (void)N;
   GemvConfig c;
   c.mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  // Launch shapes measured best on MI355X (about 8-16 rows per workgroup):
+  // narrow lane groups for short rows, wide ones for long rows.
   const int kb = K / kBlockElems;
-  // Lanes per row: the width that leaves the fewest idle lanes on the last
-  // block step, preferring wider groups on ties.
-  int best = 64;
-  int64_t best_waste = -1;
-  for (int lpr : {64, 32, 16}) {
-    const int64_t steps = (kb + lpr - 1) / lpr;
-    const int64_t waste = steps * lpr - kb;
-    if (best_waste < 0 || waste < best_waste) {
-      best = lpr;
-      best_waste = waste;
-    }
-  }
-  c.lpr = best;
-  // Rows per group: reuse activations across rows, but keep >= 1024
-  // workgroups in flight when the matrix is large enough.
-  c.rw = c.mt >= 4 ? 2 : 4;
-  while (c.rw > 1) {
-    const int64_t rows_per_wg = (int64_t)(256 / c.lpr) * c.rw;
-    if ((N + rows_per_wg - 1) / rows_per_wg >= 1024) break;
-    c.rw /= 2;
-  }
+  c.lpr = kb < 64 ? 16 : kb <= 160 ? 32 : 64;
+  const bool two = c.mt == 8 || (c.lpr == 64 && c.mt == 1) || (c.lpr == 32 && c.mt >= 4);
+  c.rw = two ? 2 : 1;
   return c;
 }
 
