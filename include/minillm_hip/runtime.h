@@ -1,0 +1,136 @@
+// runtime.h -- kernel registry, backends, runtime context and executors of the
+// MiniLLMEngine host API, with the HIP backend and executor.
+//
+// Same plugin contract as the reference runtime:
+//   KernelFn = Status(*)(const Node&, RuntimeContext&)    (kernel_registry.h:18)
+//   KernelRegistry::register_kernel/find/has              (kernel_registry.h:20-35)
+//   Backend(DeviceType, name)::supports(OpType)           (backend.h:10-21, backend.cpp:9-30)
+//   Executor::compile(const Graph&) / run(RuntimeContext&) (executor.h:16-51,
+//                                                           executor.cpp:86-142)
+//   RuntimeContext::bind/emplace/get/allocate_intermediates (runtime_context.h:19-97)
+// HipBackend and HipExecutor stand where CudaBackend and CudaExecutor stand.
+// The executor enqueues every kernel on its HIP stream (carried to the kernels
+// through RuntimeContext::hip_stream()) and never synchronises: as with the
+// reference device executor, the caller synchronises before reading outputs.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <map>
+#include <memory>
+#include <string_view>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+#include "minillm_hip/core.h"
+#include "minillm_hip/graph.h"
+
+namespace minillm {
+
+class RuntimeContext;
+
+using KernelFn = Status (*)(const Node&, RuntimeContext&);
+
+class KernelRegistry {
+ public:
+  void register_kernel(DeviceType device, OpType op, KernelFn fn);
+  expected<KernelFn, Status> find(DeviceType device, OpType op) const;
+  bool has(DeviceType device, OpType op) const;
+
+ private:
+  std::map<std::pair<int, int>, KernelFn> kernels_;
+};
+
+class Backend {
+ public:
+  Backend(DeviceType dt, std::string_view n);
+  virtual ~Backend() = default;
+  DeviceType device_type() const;
+  // Ops the backend can run (graph plumbing ops included).
+  virtual bool supports(OpType op) const;
+  std::string_view name() const;
+
+ private:
+  DeviceType device_type_;
+  std::string_view name_;
+};
+
+// MI355X backend: the ops of the Q8_0 path (Embedding, MatMul, Linear) plus
+// Output.  Graphs using other ops are rejected by HipExecutor::compile.
+class HipBackend final : public Backend {
+ public:
+  HipBackend() : Backend(DeviceType::HIP, "HipBackend") {}
+  bool supports(OpType op) const override;
+};
+
+// ValueId -> Tensor* binding for one execution.
+class RuntimeContext {
+ public:
+  RuntimeContext() = default;
+  ~RuntimeContext();
+  RuntimeContext(const RuntimeContext&) = delete;
+  RuntimeContext& operator=(const RuntimeContext&) = delete;
+
+  Status bind(ValueId id, Tensor* tensor);
+  Status emplace(ValueId id, std::unique_ptr<Tensor> tensor);
+  Tensor* get(ValueId id) const;
+  // Allocates every non-Input, non-Constant value that has no binding yet, on
+  // the value's device (HIP values: hipMalloc'd device storage).
+  Status allocate_intermediates(const Graph& graph);
+  // No KV cache on this path; kept for executor parity (reference
+  // runtime_context.cpp:222-243).
+  Status advance_kv_cache_step();
+
+  hipStream_t hip_stream() const { return hip_stream_; }
+  void set_hip_stream(hipStream_t s) { hip_stream_ = s; }
+
+ private:
+  std::unordered_map<size_t, Tensor*> bindings_;
+  std::vector<std::unique_ptr<Tensor>> owned_;
+  hipStream_t hip_stream_{nullptr};
+};
+
+class Executor {
+ public:
+  virtual ~Executor() = default;
+  virtual Status compile(const Graph& graph) = 0;
+  virtual Status run(RuntimeContext& ctx) = 0;
+};
+
+class HipExecutor final : public Executor {
+ public:
+  // `stream` = the HIP stream every kernel is enqueued on (nullptr = default stream).
+  HipExecutor(std::shared_ptr<Backend> backend, KernelRegistry& registry,
+              hipStream_t stream = nullptr);
+
+  Status compile(const Graph& graph) override;
+  Status run(RuntimeContext& ctx) override;
+  hipStream_t stream() const { return stream_; }
+
+ private:
+  const Graph* graph_{nullptr};
+  std::shared_ptr<Backend> backend_;
+  KernelRegistry& registry_;
+  std::vector<NodeId> execution_order_;
+  hipStream_t stream_;
+};
+
+// Registers the HIP Q8_0 kernels (Embedding, Linear, MatMul) under
+// DeviceType::HIP; stands where register_cuda_kernels stands
+// (reference src/runtime/kernels/cuda_kernel_adapter.cpp:700-715).
+void register_hip_kernels(KernelRegistry& registry);
+
+// Low-level launchers (device pointers, async on `stream`), the counterparts of
+// minillm::cuda::sgemm_nt / sgemm / embedding for Q8_0 weights
+// (reference include/minillm/runtime/kernels/cuda_kernels.h:13,16,37-38).
+namespace hip {
+Status sgemm_nt(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
+                const float* bias = nullptr, hipStream_t stream = nullptr);
+Status sgemm(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
+             hipStream_t stream = nullptr);
+Status embedding(const uint8_t* weight_q8_0, const int* ids, float* out, int seq_len,
+                 int vocab_size, int hidden, hipStream_t stream = nullptr);
+}  // namespace hip
+
+}  // namespace minillm

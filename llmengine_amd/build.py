@@ -29,7 +29,6 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-HOST_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__"]
 
 KERNEL_LIB = os.path.join(PKG, "libmle_q8_0.so")
 HOST_LIB = os.path.join(PKG, "libminillm_hip.so")
@@ -90,7 +89,7 @@ def build_cpp_tests(jobs: int = 8) -> list[str]:
         tmp = exe + ".tmp"
         _run([HIPCC, *HIP_FLAGS, "-UNDEBUG", *inc, "-x", "hip", src, "-o", tmp,
               "-L", PKG, "-lminillm_hip", "-lmle_q8_0",
-              f"-Wl,-rpath,{PKG}"])
+              "-Wl,-rpath,$ORIGIN/../../../llmengine_amd"])
         os.replace(tmp, exe)
         return exe
 

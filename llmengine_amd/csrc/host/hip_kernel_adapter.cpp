@@ -1,0 +1,260 @@
+// hip_kernel_adapter.cpp -- Node -> kernel glue of the HIP backend.
+//
+// Embedding / Linear / MatMul adapters registered by register_hip_kernels().
+// Validation order, error codes and message substrings follow the reference
+// device adapters (src/runtime/kernels/cuda_kernel_adapter.cpp:33-108 helpers,
+// :110-156 embedding, :158-220 linear, :222-268 matmul); the work runs in the
+// gfx950 kernels behind the C ABI of include/mle_q8_0.h.  In addition, every
+// buffer's byte size is checked against what the launch will touch, so no
+// kernel can read or write outside a bound tensor.
+#include <limits>
+#include <string>
+#include <string_view>
+
+#include "mle_q8_0.h"
+#include "minillm_hip/runtime.h"
+
+namespace minillm {
+
+namespace {
+
+Status from_capi(int rc) {
+  if (rc == MLE_OK) return Status::make_ok();
+  const std::string msg = mle_last_error();
+  switch (rc) {
+    case MLE_INVALID_ARGUMENT: return Status::invalid_argument(msg);
+    case MLE_OUT_OF_RANGE: return Status::out_of_range(msg);
+    case MLE_SHAPE_MISMATCH: return Status::shape_mismatch(msg);
+    case MLE_UNSUPPORTED: return Status::unsupported(msg);
+    default: return Status::runtime_error(msg);
+  }
+}
+
+expected<Tensor*, Status> get_tensor(ValueId id, RuntimeContext& ctx, std::string_view role) {
+  Tensor* t = ctx.get(id);
+  if (!t)
+    return unexpected(Status::runtime_error(std::string(role) + " tensor not found for ValueId %" +
+                                            std::to_string(id.value)));
+  return t;
+}
+
+Status check_allocated(const Tensor* t, std::string_view name) {
+  if (!t->is_allocated()) return Status::runtime_error(std::string(name) + " tensor not allocated");
+  return Status::make_ok();
+}
+
+Status check_hip_device(const Tensor* t, std::string_view name) {
+  if (t->device().type != DeviceType::HIP)
+    return Status::unsupported(std::string(name) + " must be a HIP tensor, got " +
+                               t->device().to_string());
+  return Status::make_ok();
+}
+
+Status check_hip_float(const Tensor* t, std::string_view name) {
+  TRY(check_allocated(t, name));
+  TRY(check_hip_device(t, name));
+  if (t->dtype() != DType::Float32)
+    return Status::unsupported(std::string(name) + " only supports Float32, got " +
+                               std::string(dtype_name(t->dtype())));
+  return Status::make_ok();
+}
+
+// The HIP backend implements the Q8_0 weight path only.
+Status check_hip_q8_weight(const Tensor* t, std::string_view name) {
+  TRY(check_allocated(t, name));
+  TRY(check_hip_device(t, name));
+  if (t->dtype() != DType::Q8_0)
+    return Status::unsupported(std::string(name) +
+                               " supports Q8_0 weights on the HIP backend, got " +
+                               std::string(dtype_name(t->dtype())));
+  return Status::make_ok();
+}
+
+Status check_q8_block_aligned(int64_t block_dim, std::string_view op) {
+  if (block_dim % static_cast<int64_t>(kQ8_0BlockElems) == 0) return Status::make_ok();
+  return Status::unsupported(std::string(op) +
+                             " Q8_0 weights require the packed dimension to be a multiple of 32, got " +
+                             std::to_string(block_dim));
+}
+
+Status check_q8_storage_bytes(const Tensor* t, std::string_view name) {
+  auto n = t->numel();
+  if (!n) return n.error();
+  const size_t need = q8_0_bytes(*n);
+  if (t->allocated_bytes() < need)
+    return Status::out_of_range(std::string(name) + " Q8_0 raw storage is too small: need " +
+                                std::to_string(need) + " bytes, got " +
+                                std::to_string(t->allocated_bytes()));
+  return Status::make_ok();
+}
+
+Status check_storage_bytes(const Tensor* t, size_t need, std::string_view name) {
+  if (t->allocated_bytes() < need)
+    return Status::out_of_range(std::string(name) + " storage is too small: need " +
+                                std::to_string(need) + " bytes, got " +
+                                std::to_string(t->allocated_bytes()));
+  return Status::make_ok();
+}
+
+expected<int, Status> checked_dim(int64_t v, std::string_view role) {
+  if (v < 0 || v > std::numeric_limits<int>::max())
+    return unexpected(Status::unsupported(std::string(role) + " dimension is outside int range"));
+  return static_cast<int>(v);
+}
+
+expected<int, Status> checked_count(size_t v, std::string_view role) {
+  if (v > static_cast<size_t>(std::numeric_limits<int>::max()))
+    return unexpected(Status::unsupported(std::string(role) + " is too large for int indexing"));
+  return static_cast<int>(v);
+}
+
+Status kernel_embedding(const Node& node, RuntimeContext& ctx) {
+  if (node.inputs().size() < 2 || node.outputs().empty())
+    return Status::invalid_argument("Embedding expects inputs [input_ids, weight] and one output");
+  auto ids = get_tensor(node.inputs()[0], ctx, "input_ids");
+  if (!ids) return ids.error();
+  auto wt = get_tensor(node.inputs()[1], ctx, "weight");
+  if (!wt) return wt.error();
+  auto ot = get_tensor(node.outputs()[0], ctx, "output");
+  if (!ot) return ot.error();
+
+  TRY(check_allocated(*ids, "input_ids"));
+  TRY(check_hip_device(*ids, "input_ids"));
+  if ((*ids)->dtype() != DType::Int32)
+    return Status::unsupported("input_ids only supports Int32, got " +
+                               std::string(dtype_name((*ids)->dtype())));
+  TRY(check_hip_q8_weight(*wt, "weight"));
+  TRY(check_hip_float(*ot, "output"));
+  if ((*wt)->shape().rank() != 2) return Status::shape_mismatch("Embedding weight must be rank 2");
+
+  auto n_ids = (*ids)->numel();
+  if (!n_ids) return n_ids.error();
+  auto seq_len = checked_count(*n_ids, "embedding input_ids");
+  if (!seq_len) return seq_len.error();
+  auto vocab = checked_dim((*wt)->shape().dim(0), "embedding vocab");
+  if (!vocab) return vocab.error();
+  auto hidden = checked_dim((*wt)->shape().dim(1), "embedding hidden");
+  if (!hidden) return hidden.error();
+  TRY(check_q8_block_aligned(*hidden, "embedding"));
+  TRY(check_q8_storage_bytes(*wt, "embedding weight"));
+  TRY(check_storage_bytes(*ids, static_cast<size_t>(*seq_len) * 4, "input_ids"));
+  TRY(check_storage_bytes(*ot, static_cast<size_t>(*seq_len) * static_cast<size_t>(*hidden) * 4,
+                          "output"));
+  return hip::embedding(static_cast<const uint8_t*>((*wt)->data()),
+                        static_cast<const int*>((*ids)->data()),
+                        static_cast<float*>((*ot)->data()), *seq_len, *vocab, *hidden,
+                        ctx.hip_stream());
+}
+
+Status kernel_linear(const Node& node, RuntimeContext& ctx) {
+  if (node.inputs().size() < 2 || node.outputs().empty())
+    return Status::invalid_argument("Linear expects inputs [x, weight, (bias)] and one output");
+  auto xt = get_tensor(node.inputs()[0], ctx, "x");
+  if (!xt) return xt.error();
+  auto wt = get_tensor(node.inputs()[1], ctx, "weight");
+  if (!wt) return wt.error();
+  auto ot = get_tensor(node.outputs()[0], ctx, "output");
+  if (!ot) return ot.error();
+
+  TRY(check_hip_float(*xt, "x"));
+  TRY(check_hip_q8_weight(*wt, "weight"));
+  TRY(check_hip_float(*ot, "output"));
+  if ((*wt)->shape().rank() != 2) return Status::shape_mismatch("Linear weight must be rank 2");
+  if ((*xt)->shape().rank() == 0) return Status::shape_mismatch("linear x expects rank >= 1");
+
+  size_t rows = 1;
+  for (size_t i = 0; i + 1 < (*xt)->shape().rank(); ++i)
+    rows *= static_cast<size_t>((*xt)->shape().dim(i));
+  auto M = checked_count(rows, "linear x");
+  if (!M) return M.error();
+  auto K = checked_dim((*xt)->shape().dim((*xt)->shape().rank() - 1), "linear x");
+  if (!K) return K.error();
+  auto N = checked_dim((*wt)->shape().dim(0), "linear output");
+  if (!N) return N.error();
+  auto wk = checked_dim((*wt)->shape().dim(1), "linear weight input");
+  if (!wk) return wk.error();
+  if (*wk != *K)
+    return Status::shape_mismatch("Linear x last dimension must match weight input dimension");
+
+  const float* bias = nullptr;
+  if (node.inputs().size() >= 3) {
+    auto bt = get_tensor(node.inputs()[2], ctx, "bias");
+    if (!bt) return bt.error();
+    TRY(check_hip_float(*bt, "bias"));
+    if ((*bt)->shape().rank() != 1 || (*bt)->shape().dim(0) != *N)
+      return Status::shape_mismatch("Linear bias shape must match output features");
+    TRY(check_storage_bytes(*bt, static_cast<size_t>(*N) * 4, "bias"));
+    bias = static_cast<const float*>((*bt)->data());
+  }
+  TRY(check_q8_block_aligned(*K, "linear"));
+  TRY(check_q8_storage_bytes(*wt, "linear weight"));
+  TRY(check_storage_bytes(*xt, static_cast<size_t>(*M) * static_cast<size_t>(*K) * 4, "x"));
+  TRY(check_storage_bytes(*ot, static_cast<size_t>(*M) * static_cast<size_t>(*N) * 4, "output"));
+  return hip::sgemm_nt(static_cast<const float*>((*xt)->data()),
+                       static_cast<const uint8_t*>((*wt)->data()),
+                       static_cast<float*>((*ot)->data()), *M, *N, *K, bias, ctx.hip_stream());
+}
+
+Status kernel_matmul(const Node& node, RuntimeContext& ctx) {
+  if (node.inputs().size() < 2 || node.outputs().empty())
+    return Status::invalid_argument("MatMul expects inputs [a, b] and one output");
+  auto at = get_tensor(node.inputs()[0], ctx, "a");
+  if (!at) return at.error();
+  auto bt = get_tensor(node.inputs()[1], ctx, "b");
+  if (!bt) return bt.error();
+  auto ot = get_tensor(node.outputs()[0], ctx, "output");
+  if (!ot) return ot.error();
+
+  TRY(check_hip_float(*at, "a"));
+  TRY(check_hip_q8_weight(*bt, "b"));
+  TRY(check_hip_float(*ot, "output"));
+  if ((*at)->shape().rank() != 2 || (*bt)->shape().rank() != 2)
+    return Status::shape_mismatch("HIP MatMul currently expects rank-2 tensors");
+  auto M = checked_dim((*at)->shape().dim(0), "matmul M");
+  if (!M) return M.error();
+  auto K = checked_dim((*at)->shape().dim(1), "matmul K");
+  if (!K) return K.error();
+  auto bk = checked_dim((*bt)->shape().dim(0), "matmul B K");
+  if (!bk) return bk.error();
+  auto N = checked_dim((*bt)->shape().dim(1), "matmul N");
+  if (!N) return N.error();
+  if (*bk != *K) return Status::shape_mismatch("MatMul inner dimensions differ");
+  TRY(check_q8_block_aligned(*K, "matmul reduction dimension"));
+  TRY(check_q8_block_aligned(*N, "matmul output dimension"));
+  TRY(check_q8_storage_bytes(*bt, "matmul b"));
+  TRY(check_storage_bytes(*at, static_cast<size_t>(*M) * static_cast<size_t>(*K) * 4, "a"));
+  TRY(check_storage_bytes(*ot, static_cast<size_t>(*M) * static_cast<size_t>(*N) * 4, "output"));
+  return hip::sgemm(static_cast<const float*>((*at)->data()),
+                    static_cast<const uint8_t*>((*bt)->data()),
+                    static_cast<float*>((*ot)->data()), *M, *N, *K, ctx.hip_stream());
+}
+
+}  // namespace
+
+namespace hip {
+
+Status sgemm_nt(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
+                const float* bias, hipStream_t stream) {
+  return from_capi(mle_q8_0_linear(A, B_q8_0, bias, C, M, N, K, stream));
+}
+
+Status sgemm(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
+             hipStream_t stream) {
+  return from_capi(mle_q8_0_matmul(A, B_q8_0, C, M, N, K, stream));
+}
+
+Status embedding(const uint8_t* weight_q8_0, const int* ids, float* out, int seq_len,
+                 int vocab_size, int hidden, hipStream_t stream) {
+  return from_capi(mle_q8_0_embedding(weight_q8_0, reinterpret_cast<const int32_t*>(ids), out,
+                                      seq_len, vocab_size, hidden, stream));
+}
+
+}  // namespace hip
+
+void register_hip_kernels(KernelRegistry& registry) {
+  registry.register_kernel(DeviceType::HIP, OpType::Embedding, kernel_embedding);
+  registry.register_kernel(DeviceType::HIP, OpType::Linear, kernel_linear);
+  registry.register_kernel(DeviceType::HIP, OpType::MatMul, kernel_matmul);
+}
+
+}  // namespace minillm

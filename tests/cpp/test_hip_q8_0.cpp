@@ -1,0 +1,455 @@
+// test_hip_q8_0.cpp -- the HIP backend end to end on an MI355X.
+//
+// Mirrors the reference's device tests of the Q8_0 path with the HIP names:
+//   tests/test_cuda_kernels.cpp:409-529   low-level sgemm_nt / sgemm / embedding
+//   tests/test_cuda_kernels.cpp:953-1061  executor Linear + MatMul on Q8_0 weights
+//   tests/test_cuda_kernels.cpp:1063-1123 rejects K % 32 != 0 and short storage
+//   tests/test_runtime.cpp:561-626        Linear with bias through the executor
+// plus embedding through the executor (device semantics for bad ids), a
+// caller-owned stream, and a prefill-sized Linear (bf16 MFMA path).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "minillm_hip/runtime.h"
+
+using namespace minillm;
+
+#define CHECK(cond)                                                              \
+  do {                                                                           \
+    if (!(cond)) {                                                               \
+      std::fprintf(stderr, "CHECK failed at %s:%d: %s\n", __FILE__, __LINE__, #cond); \
+      std::abort();                                                              \
+    }                                                                            \
+  } while (0)
+
+static void check_hip(hipError_t e) {
+  if (e != hipSuccess) {
+    std::fprintf(stderr, "HIP error: %s\n", hipGetErrorString(e));
+    std::abort();
+  }
+}
+
+static void check_status(const Status& st) {
+  if (!st.ok()) {
+    std::fprintf(stderr, "%s\n", st.to_string().c_str());
+    std::abort();
+  }
+}
+
+static void near(float got, float want, float tol) {
+  if (!(std::fabs(got - want) <= tol)) {
+    std::fprintf(stderr, "got %.9g want %.9g (tol %g)\n", got, want, tol);
+    std::abort();
+  }
+}
+
+// Packs int8 values into Q8_0 blocks with one fp16 scale (reference test helper
+// semantics, tests/test_cuda_kernels.cpp:51-65).
+static std::vector<uint8_t> pack_q8_0(const std::vector<int8_t>& v, uint16_t scale_bits) {
+  const size_t blocks = (v.size() + 31) / 32;
+  std::vector<uint8_t> out(blocks * 34, 0);
+  for (size_t b = 0; b < blocks; ++b) {
+    out[b * 34] = static_cast<uint8_t>(scale_bits & 0xff);
+    out[b * 34 + 1] = static_cast<uint8_t>(scale_bits >> 8);
+    for (size_t i = 0; i < 32 && b * 32 + i < v.size(); ++i)
+      out[b * 34 + 2 + i] = static_cast<uint8_t>(v[b * 32 + i]);
+  }
+  return out;
+}
+
+template <typename T>
+struct DevBuf {
+  T* p = nullptr;
+  size_t n = 0;
+  explicit DevBuf(size_t count) : n(count) { check_hip(hipMalloc(&p, n * sizeof(T) + 1)); }
+  ~DevBuf() { (void)hipFree(p); }
+  void put(const std::vector<T>& h) { check_hip(hipMemcpy(p, h.data(), n * sizeof(T), hipMemcpyHostToDevice)); }
+  std::vector<T> get() const {
+    std::vector<T> h(n);
+    check_hip(hipMemcpy(h.data(), p, n * sizeof(T), hipMemcpyDeviceToHost));
+    return h;
+  }
+};
+
+static void upload(Tensor& t, const void* host, size_t bytes) {
+  check_hip(hipMemcpy(t.data(), host, bytes, hipMemcpyHostToDevice));
+}
+
+static std::vector<float> download(const Tensor* t, size_t count) {
+  std::vector<float> h(count);
+  check_hip(hipMemcpy(h.data(), t->data(), count * 4, hipMemcpyDeviceToHost));
+  return h;
+}
+
+static void test_low_level_kernels() {
+  {  // Linear M=1 N=2 K=32, scale 1.0
+    const int M = 1, N = 2, K = 32;
+    std::vector<float> A(M * K);
+    std::vector<int8_t> B(N * K);
+    for (int i = 0; i < M * K; ++i) A[i] = float((i % 7) - 3) * 0.25f;
+    for (int i = 0; i < N * K; ++i) B[i] = int8_t((i * 5) % 17 - 8);
+    auto packed = pack_q8_0(B, 0x3c00);
+    DevBuf<float> dA(A.size()), dC(M * N);
+    DevBuf<uint8_t> dB(packed.size());
+    dA.put(A);
+    dB.put(packed);
+    check_status(hip::sgemm_nt(dA.p, dB.p, dC.p, M, N, K));
+    check_hip(hipDeviceSynchronize());
+    auto C = dC.get();
+    for (int n = 0; n < N; ++n) {
+      float e = 0.f;
+      for (int k = 0; k < K; ++k) e += A[k] * float(B[n * K + k]);
+      near(C[n], e, 1e-5f);
+    }
+  }
+  {  // Linear M=2 N=3 K=64, scale 0.5
+    const int M = 2, N = 3, K = 64;
+    std::vector<float> A(M * K);
+    std::vector<int8_t> B(N * K);
+    for (int i = 0; i < M * K; ++i) A[i] = float((i % 11) - 5) * 0.125f;
+    for (int i = 0; i < N * K; ++i) B[i] = int8_t((i * 7) % 23 - 11);
+    auto packed = pack_q8_0(B, 0x3800);
+    DevBuf<float> dA(A.size()), dC(M * N);
+    DevBuf<uint8_t> dB(packed.size());
+    dA.put(A);
+    dB.put(packed);
+    check_status(hip::sgemm_nt(dA.p, dB.p, dC.p, M, N, K));
+    check_hip(hipDeviceSynchronize());
+    auto C = dC.get();
+    for (int m = 0; m < M; ++m)
+      for (int n = 0; n < N; ++n) {
+        float e = 0.f;
+        for (int k = 0; k < K; ++k) e += A[m * K + k] * float(B[n * K + k]) * 0.5f;
+        near(C[m * N + n], e, 1e-4f);
+      }
+  }
+  {  // MatMul M=2 N=64 K=32, scale 0.5 (blocks along N)
+    const int M = 2, N = 64, K = 32;
+    std::vector<float> A(M * K);
+    std::vector<int8_t> B(K * N);
+    for (int i = 0; i < M * K; ++i) A[i] = float((i % 13) - 6) * 0.125f;
+    for (int i = 0; i < K * N; ++i) B[i] = int8_t((i * 3) % 29 - 14);
+    auto packed = pack_q8_0(B, 0x3800);
+    DevBuf<float> dA(A.size()), dC(M * N);
+    DevBuf<uint8_t> dB(packed.size());
+    dA.put(A);
+    dB.put(packed);
+    check_status(hip::sgemm(dA.p, dB.p, dC.p, M, N, K));
+    check_hip(hipDeviceSynchronize());
+    auto C = dC.get();
+    for (int m = 0; m < M; ++m)
+      for (int n = 0; n < N; ++n) {
+        float e = 0.f;
+        for (int k = 0; k < K; ++k) e += A[m * K + k] * float(B[k * N + n]) * 0.5f;
+        near(C[m * N + n], e, 1e-4f);
+      }
+  }
+  {  // Embedding vocab 3, hidden 64, ids {2, 0, 1}, scale 0.5
+    const int vocab = 3, hidden = 64;
+    std::vector<int8_t> W(vocab * hidden);
+    for (int i = 0; i < vocab * hidden; ++i) W[i] = int8_t((i * 5) % 31 - 15);
+    auto packed = pack_q8_0(W, 0x3800);
+    const std::vector<int> ids{2, 0, 1};
+    DevBuf<uint8_t> dW(packed.size());
+    DevBuf<int> dids(ids.size());
+    DevBuf<float> dout(ids.size() * hidden);
+    dW.put(packed);
+    dids.put(ids);
+    check_status(hip::embedding(dW.p, dids.p, dout.p, int(ids.size()), vocab, hidden));
+    check_hip(hipDeviceSynchronize());
+    auto out = dout.get();
+    for (size_t s = 0; s < ids.size(); ++s)
+      for (int h = 0; h < hidden; ++h)
+        CHECK(out[s * hidden + h] == float(W[ids[s] * hidden + h]) * 0.5f);  // exact
+  }
+  {  // low-level error path: K not a multiple of 32
+    const Status st = hip::sgemm_nt(reinterpret_cast<const float*>(16),
+                                    reinterpret_cast<const uint8_t*>(16),
+                                    reinterpret_cast<float*>(16), 1, 2, 31);
+    CHECK(st.code() == ErrorCode::Unsupported);
+    CHECK(std::string(st.message()).find("multiple of 32") != std::string::npos);
+  }
+  std::printf("  PASS test_low_level_kernels\n");
+}
+
+static void test_executor_linear_and_matmul() {
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  {
+    Graph graph;
+    GraphBuilder gb(graph);
+    auto x = gb.input("x", Shape({2, 32}), DType::Float32, Device::hip(0));
+    auto w = gb.constant("w", Shape({3, 32}), DType::Float32, Device::hip(0));
+    auto y = gb.linear(*x, *w, std::nullopt, "linear_q8");
+    CHECK(x && w && y && gb.output(*y, "out"));
+    Tensor tx("x", Shape({2, 32}), DType::Float32, Device::hip(0));
+    Tensor tw("w", Shape({3, 32}), DType::Q8_0, Device::hip(0));
+    check_status(tx.allocate_hip());
+    std::vector<float> hx(64);
+    for (int i = 0; i < 64; ++i) hx[i] = float((i % 11) - 5) * 0.125f;
+    std::vector<int8_t> hw(96);
+    for (int i = 0; i < 96; ++i) hw[i] = int8_t((i * 7) % 19 - 9);
+    auto packed = pack_q8_0(hw, 0x3c00);
+    check_status(tw.allocate_hip_bytes(packed.size()));
+    upload(tx, hx.data(), hx.size() * 4);
+    upload(tw, packed.data(), packed.size());
+    RuntimeContext ctx;
+    check_status(ctx.bind(*x, &tx));
+    check_status(ctx.bind(*w, &tw));
+    check_status(ctx.allocate_intermediates(graph));
+    HipExecutor ex(std::make_shared<HipBackend>(), registry);
+    check_status(ex.compile(graph));
+    check_status(ex.run(ctx));
+    check_hip(hipDeviceSynchronize());
+    Tensor* yt = ctx.get(*y);
+    CHECK(yt && yt->device().type == DeviceType::HIP && yt->dtype() == DType::Float32);
+    auto got = download(yt, 6);
+    for (int m = 0; m < 2; ++m)
+      for (int n = 0; n < 3; ++n) {
+        float e = 0.f;
+        for (int k = 0; k < 32; ++k) e += hx[m * 32 + k] * float(hw[n * 32 + k]);
+        near(got[m * 3 + n], e, 1e-4f);
+      }
+  }
+  {
+    Graph graph;
+    GraphBuilder gb(graph);
+    auto a = gb.input("a", Shape({2, 32}), DType::Float32, Device::hip(0));
+    auto b = gb.constant("b", Shape({32, 32}), DType::Float32, Device::hip(0));
+    auto y = gb.matmul(*a, *b, "matmul_q8");
+    CHECK(a && b && y);
+    Tensor ta("a", Shape({2, 32}), DType::Float32, Device::hip(0));
+    Tensor tb("b", Shape({32, 32}), DType::Q8_0, Device::hip(0));
+    check_status(ta.allocate_hip());
+    std::vector<float> ha(64);
+    for (int i = 0; i < 64; ++i) ha[i] = float((i % 13) - 6) * 0.125f;
+    std::vector<int8_t> hb(1024);
+    for (int i = 0; i < 1024; ++i) hb[i] = int8_t((i * 5) % 17 - 8);
+    auto packed = pack_q8_0(hb, 0x3c00);
+    check_status(tb.allocate_hip_bytes(packed.size()));
+    upload(ta, ha.data(), ha.size() * 4);
+    upload(tb, packed.data(), packed.size());
+    RuntimeContext ctx;
+    check_status(ctx.bind(*a, &ta));
+    check_status(ctx.bind(*b, &tb));
+    check_status(ctx.allocate_intermediates(graph));
+    HipExecutor ex(std::make_shared<HipBackend>(), registry);
+    check_status(ex.compile(graph));
+    check_status(ex.run(ctx));
+    check_hip(hipDeviceSynchronize());
+    auto got = download(ctx.get(*y), 64);
+    for (int m = 0; m < 2; ++m)
+      for (int n = 0; n < 32; ++n) {
+        float e = 0.f;
+        for (int k = 0; k < 32; ++k) e += ha[m * 32 + k] * float(hb[k * 32 + n]);
+        CHECK(got[m * 32 + n] == e);  // exact: integer quants x dyadic activations
+      }
+  }
+  std::printf("  PASS test_executor_linear_and_matmul\n");
+}
+
+static void test_executor_linear_bias_rank3() {
+  // x [1,2,32], w [3,32] Q8_0 scale 1, bias [3]  (tests/test_runtime.cpp:561-626)
+  Graph g;
+  GraphBuilder gb(g);
+  auto x = gb.input("x", Shape({1, 2, 32}), DType::Float32, Device::hip(0));
+  auto w = gb.constant("w", Shape({3, 32}), DType::Float32, Device::hip(0));
+  auto b = gb.constant("b", Shape({3}), DType::Float32, Device::hip(0));
+  auto y = gb.linear(*x, *w, *b, "linear_q8");
+  CHECK(y && gb.output(*y, "out"));
+  Tensor tx("x", Shape({1, 2, 32}), DType::Float32, Device::hip(0));
+  Tensor tw("w", Shape({3, 32}), DType::Q8_0, Device::hip(0));
+  Tensor tb("b", Shape({3}), DType::Float32, Device::hip(0));
+  check_status(tx.allocate_hip());
+  check_status(tb.allocate_hip());
+  std::vector<float> hx(64), hb{0.5f, -1.0f, 1.5f};
+  for (int i = 0; i < 64; ++i) hx[i] = float((i % 11) - 5) * 0.125f;
+  std::vector<int8_t> hw(96);
+  for (int i = 0; i < 96; ++i) hw[i] = int8_t((i * 7) % 19 - 9);
+  auto packed = pack_q8_0(hw, 0x3c00);
+  check_status(tw.allocate_hip_bytes(packed.size()));
+  upload(tx, hx.data(), 256);
+  upload(tb, hb.data(), 12);
+  upload(tw, packed.data(), packed.size());
+  RuntimeContext ctx;
+  check_status(ctx.bind(*x, &tx));
+  check_status(ctx.bind(*w, &tw));
+  check_status(ctx.bind(*b, &tb));
+  check_status(ctx.allocate_intermediates(g));
+  KernelRegistry reg;
+  register_hip_kernels(reg);
+  HipExecutor ex(std::make_shared<HipBackend>(), reg);
+  check_status(ex.compile(g));
+  check_status(ex.run(ctx));
+  check_hip(hipDeviceSynchronize());
+  CHECK(ctx.get(*y)->shape() == Shape({1, 2, 3}));
+  auto got = download(ctx.get(*y), 6);
+  for (int t = 0; t < 2; ++t)
+    for (int o = 0; o < 3; ++o) {
+      float e = hb[o];
+      for (int k = 0; k < 32; ++k) e += hx[t * 32 + k] * float(hw[o * 32 + k]);
+      near(got[t * 3 + o], e, 1e-5f);
+    }
+  std::printf("  PASS test_executor_linear_bias_rank3\n");
+}
+
+static void test_executor_embedding_and_stream() {
+  // ids [2,3] (rank 2) -> out [2,3,64]; id 7 is outside vocab 5 -> zero row.
+  hipStream_t stream;
+  check_hip(hipStreamCreate(&stream));
+  Graph g;
+  GraphBuilder gb(g);
+  auto ids = gb.input("ids", Shape({2, 3}), DType::Int32, Device::hip(0));
+  auto w = gb.constant("emb", Shape({5, 64}), DType::Float32, Device::hip(0));
+  auto y = gb.embedding(*ids, *w, "embed");
+  CHECK(y && gb.output(*y, "out"));
+  Tensor tids("ids", Shape({2, 3}), DType::Int32, Device::hip(0));
+  Tensor tw("emb", Shape({5, 64}), DType::Q8_0, Device::hip(0));
+  check_status(tids.allocate_hip());
+  check_status(tw.allocate_hip());
+  CHECK(tw.allocated_bytes() == q8_0_bytes(320));
+  std::vector<int8_t> hw(320);
+  for (int i = 0; i < 320; ++i) hw[i] = int8_t((i * 13) % 255 - 127);
+  auto packed = pack_q8_0(hw, 0x1401);  // a non-trivial scale (~0.00101)
+  std::vector<int> hids{4, 0, 7, 2, 2, 1};
+  upload(tids, hids.data(), 24);
+  upload(tw, packed.data(), packed.size());
+  RuntimeContext ctx;
+  check_status(ctx.bind(*ids, &tids));
+  check_status(ctx.bind(*w, &tw));
+  check_status(ctx.allocate_intermediates(g));
+  KernelRegistry reg;
+  register_hip_kernels(reg);
+  HipExecutor ex(std::make_shared<HipBackend>(), reg, stream);
+  CHECK(ex.stream() == stream);
+  check_status(ex.compile(g));
+  check_status(ex.run(ctx));
+  check_hip(hipStreamSynchronize(stream));
+  CHECK(ctx.get(*y)->shape() == Shape({2, 3, 64}));
+  auto got = download(ctx.get(*y), 6 * 64);
+  const float d = std::ldexp(1025.0f, -20);  // fp16 0x1401 = (1 + 1/1024) * 2^-10
+  for (int s = 0; s < 6; ++s)
+    for (int h = 0; h < 64; ++h) {
+      const float want = (hids[s] < 0 || hids[s] >= 5) ? 0.0f : d * float(hw[hids[s] * 64 + h]);
+      CHECK(got[s * 64 + h] == want);
+    }
+  check_hip(hipStreamDestroy(stream));
+  std::printf("  PASS test_executor_embedding_and_stream\n");
+}
+
+static void test_executor_rejects_invalid_inputs() {
+  KernelRegistry reg;
+  register_hip_kernels(reg);
+  {  // K = 31
+    Graph g;
+    GraphBuilder gb(g);
+    auto x = gb.input("x", Shape({1, 31}), DType::Float32, Device::hip(0));
+    auto w = gb.constant("w", Shape({2, 31}), DType::Float32, Device::hip(0));
+    auto y = gb.linear(*x, *w, std::nullopt, "linear_q8_bad_k");
+    CHECK(y);
+    Tensor tx("x", Shape({1, 31}), DType::Float32, Device::hip(0));
+    Tensor tw("w", Shape({2, 31}), DType::Q8_0, Device::hip(0));
+    check_status(tx.allocate_hip());
+    check_status(tw.allocate_hip_bytes(q8_0_bytes(62)));
+    RuntimeContext ctx;
+    check_status(ctx.bind(*x, &tx));
+    check_status(ctx.bind(*w, &tw));
+    check_status(ctx.allocate_intermediates(g));
+    HipExecutor ex(std::make_shared<HipBackend>(), reg);
+    check_status(ex.compile(g));
+    const Status st = ex.run(ctx);
+    CHECK(!st.ok() && std::string(st.message()).find("Q8_0") != std::string::npos);
+  }
+  {  // raw storage too small
+    Graph g;
+    GraphBuilder gb(g);
+    auto x = gb.input("x", Shape({1, 32}), DType::Float32, Device::hip(0));
+    auto w = gb.constant("w", Shape({1, 32}), DType::Float32, Device::hip(0));
+    auto y = gb.linear(*x, *w, std::nullopt, "linear_q8_short_storage");
+    CHECK(y);
+    Tensor tx("x", Shape({1, 32}), DType::Float32, Device::hip(0));
+    Tensor tw("w", Shape({1, 32}), DType::Q8_0, Device::hip(0));
+    check_status(tx.allocate_hip());
+    check_status(tw.allocate_hip_bytes(1));
+    RuntimeContext ctx;
+    check_status(ctx.bind(*x, &tx));
+    check_status(ctx.bind(*w, &tw));
+    check_status(ctx.allocate_intermediates(g));
+    HipExecutor ex(std::make_shared<HipBackend>(), reg);
+    check_status(ex.compile(g));
+    const Status st = ex.run(ctx);
+    CHECK(!st.ok() && std::string(st.message()).find("too small") != std::string::npos);
+  }
+  std::printf("  PASS test_executor_rejects_invalid_inputs\n");
+}
+
+static void test_executor_prefill_linear() {
+  // x [2,64,256] -> M = 128 tokens: the bf16 MFMA path; checked in FP64.
+  const int M = 128, N = 160, K = 256;
+  Graph g;
+  GraphBuilder gb(g);
+  auto x = gb.input("x", Shape({2, 64, K}), DType::Float32, Device::hip(0));
+  auto w = gb.constant("w", Shape({N, K}), DType::Float32, Device::hip(0));
+  auto y = gb.linear(*x, *w, std::nullopt, "prefill");
+  CHECK(y);
+  std::vector<float> hx(size_t(M) * K);
+  uint32_t s = 12345;
+  auto rnd = [&]() { s = s * 1664525u + 1013904223u; return s; };
+  for (auto& v : hx) v = float(int(rnd() >> 16) % 2001 - 1000) / 500.0f;
+  std::vector<int8_t> hq(size_t(N) * K);
+  for (auto& q : hq) q = int8_t(int(rnd() >> 20) % 255 - 127);
+  auto packed = pack_q8_0(hq, 0x2200);  // scale 2^-7 * 1.5
+  Tensor tx("x", Shape({2, 64, K}), DType::Float32, Device::hip(0));
+  Tensor tw("w", Shape({N, K}), DType::Q8_0, Device::hip(0));
+  check_status(tx.allocate_hip());
+  check_status(tw.allocate_hip());
+  upload(tx, hx.data(), hx.size() * 4);
+  upload(tw, packed.data(), packed.size());
+  RuntimeContext ctx;
+  check_status(ctx.bind(*x, &tx));
+  check_status(ctx.bind(*w, &tw));
+  check_status(ctx.allocate_intermediates(g));
+  KernelRegistry reg;
+  register_hip_kernels(reg);
+  HipExecutor ex(std::make_shared<HipBackend>(), reg);
+  check_status(ex.compile(g));
+  check_status(ex.run(ctx));
+  check_hip(hipDeviceSynchronize());
+  auto got = download(ctx.get(*y), size_t(M) * N);
+  const double d = 1.5 / 128.0;
+  double num = 0, den = 0;
+  for (int m = 0; m < M; ++m)
+    for (int n = 0; n < N; ++n) {
+      double e = 0;
+      for (int k = 0; k < K; ++k) e += double(hx[size_t(m) * K + k]) * d * hq[size_t(n) * K + k];
+      num += (got[size_t(m) * N + n] - e) * (got[size_t(m) * N + n] - e);
+      den += e * e;
+    }
+  const double rel = std::sqrt(num / den);
+  std::printf("    prefill rel_l2 = %.3e\n", rel);
+  CHECK(rel <= 1e-2);
+  std::printf("  PASS test_executor_prefill_linear\n");
+}
+
+int main() {
+  int count = 0;
+  check_hip(hipGetDeviceCount(&count));
+  CHECK(count > 0);
+  check_hip(hipSetDevice(0));
+  std::printf("test_hip_q8_0:\n");
+  test_low_level_kernels();
+  test_executor_linear_and_matmul();
+  test_executor_linear_bias_rank3();
+  test_executor_embedding_and_stream();
+  test_executor_rejects_invalid_inputs();
+  test_executor_prefill_linear();
+  std::printf("test_hip_q8_0: all passed\n");
+  return 0;
+}
