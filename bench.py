@@ -57,7 +57,37 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true",
                    help="skip the prefill and embedding figures")
+    p.add_argument("--profile-kernel", default=None, metavar="M,N,K",
+                   help="counter-collection mode: run only the decode Linear of this shape "
+                        "200 times (rotating weight copies) and a 256 MiB device copy used "
+                        "to calibrate FETCH_SIZE / WRITE_SIZE, then exit")
     return p.parse_args()
+
+
+def profile_kernel(spec):
+    """Launches for `rocprofv3 --pmc`: one decode Linear shape, then a calibration copy."""
+    import torch
+    from llmengine_amd import capi
+    from llmengine_amd import synthetic as S
+    M, N, K = (int(v) for v in spec.split(","))
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    w = torch.from_numpy(S.q8_0_weight(7, N, K)[0]).to(dev)
+    R = max(2, -(-ROTATE_BYTES // w.numel()) + 1)
+    ws = [w] + [w.clone() for _ in range(R - 1)]
+    x = torch.from_numpy(S.activations(8, (M, K))).to(dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    for j in range(200):
+        capi.linear(x, ws[j % R], None, y, M, N, K, stream=stream)
+    torch.cuda.synchronize()
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profiled": {"M": M, "N": N, "K": K, "launches": 200,
+                                   "bytes_per_launch": gemv_bytes(M, N, K),
+                                   "calibration_copy_bytes": src.numel() * 4}}), flush=True)
 
 
 def cpu_baseline(weights_host, xs_host):
@@ -84,6 +114,9 @@ def cpu_baseline(weights_host, xs_host):
 
 def main():
     args = parse()
+    if args.profile_kernel:
+        profile_kernel(args.profile_kernel)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
               "supported (no multi-GPU path exists in this round)", file=sys.stderr)
