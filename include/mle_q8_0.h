@@ -112,15 +112,20 @@ size_t mle_q8_0_bytes(int64_t numel);
  *   binary16 pattern bits[i] (exact; NaN canonicalised as the reference CPU
  *   decode does, cpu_kernels.cpp:21-37).  Used for the exhaustive decode check.
  * mle_q8_0_linear_ex: mle_q8_0_linear with the path forced (path 1 = FP32 GEMV
- *   for any M, path 2 = bf16-MFMA GEMM for any M, 0 = automatic) and, for the
- *   GEMV, an optional launch shape (mt in {1,2,4,8} >= min(M,8), lpr in
- *   {16,32,64}, rw in {1,2,4,8}; all three 0 = automatic).
+ *   for any M, path 2 = bf16-MFMA GEMM for any M, path 3 = MFMA decode with
+ *   FP32-exact activations for any M, 0 = automatic) and an optional launch
+ *   shape t0..t3 (all four 0 = automatic):
+ *     path 1: t0 = token tile mt in {1,2,4,8} >= min(M,8), t1 = lanes per row
+ *             in {16,32,64}, t2 = rows per lane group in {1,2,4,8}, t3 = 0;
+ *     path 3: t0 = token tile in {1,2,4,5,8,16} >= min(M,16), t1 = waves per
+ *             workgroup, t2 = K blocks per chunk ((4,8), (4,16), (2,8), (8,8)),
+ *             t3 = K splits in [0, 64] (0 or 1 = no split).
  */
 int mle_q8_0_f16_decode(const uint16_t* bits, float* out, int64_t n,
                         hipStream_t stream);
 int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
-                       float* y, int M, int N, int K, int path, int mt, int lpr,
-                       int rw, hipStream_t stream);
+                       float* y, int M, int N, int K, int path, int t0, int t1,
+                       int t2, int t3, hipStream_t stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

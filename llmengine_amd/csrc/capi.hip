@@ -8,9 +8,13 @@
 // the HIP error string.  Codes are the reference's ErrorCode values.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "../../include/mle_q8_0.h"
 #include "launch.hpp"
@@ -84,16 +88,93 @@ int validate_linear(const float* x, const uint8_t* w, const float* bias, float* 
   return MLE_OK;
 }
 
+// Split-K workspace of the MFMA decode path, one per (device, stream): calls on
+// one stream run in order, so its partial sums and tile counters are never used
+// by two launches at once.  Allocated on the first call that needs it (and grown
+// when a larger shape comes), kept until the process ends.
+struct StreamWorkspace {
+  float* partials = nullptr;
+  size_t partial_cap = 0;
+  uint32_t* counters = nullptr;
+  size_t counter_cap = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, StreamWorkspace> g_ws;
+
+int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWorkspace* out) {
+  *out = mle::SplitKWorkspace{};
+  if (need.partial_floats == 0) return MLE_OK;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 workspace");
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  StreamWorkspace& e = g_ws[{dev, stream}];
+  if (e.partial_cap < need.partial_floats || e.counter_cap < need.counters) {
+    if (e.partials != nullptr || e.counters != nullptr) {
+      // Earlier launches on this stream may still read the old buffers.
+      err = hipStreamSynchronize(stream);
+      if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 workspace");
+      (void)hipFree(e.partials);
+      (void)hipFree(e.counters);
+      e = StreamWorkspace{};
+    }
+    const size_t pc = std::max<size_t>(need.partial_floats, size_t(1) << 20);
+    const size_t cc = std::max<size_t>(need.counters, 4096);
+    err = hipMalloc(&e.partials, pc * sizeof(float));
+    if (err == hipSuccess) err = hipMalloc(&e.counters, cc * sizeof(uint32_t));
+    if (err == hipSuccess) err = hipMemsetAsync(e.counters, 0, cc * sizeof(uint32_t), stream);
+    if (err != hipSuccess) {
+      (void)hipFree(e.partials);
+      (void)hipFree(e.counters);
+      e = StreamWorkspace{};
+      return check_launch(err, "hip sgemm_nt Q8_0 workspace allocation failed");
+    }
+    e.partial_cap = pc;
+    e.counter_cap = cc;
+  }
+  out->partials = e.partials;
+  out->counters = e.counters;
+  return MLE_OK;
+}
+
+// Linear path numbers (mle_q8_0_linear_ex): 1 FP32 GEMV, 2 bf16-MFMA prefill GEMM,
+// 3 MFMA decode with FP32-exact activations.
+int pick_path(int M) { return M >= 64 ? 2 : M == 1 ? 1 : 3; }
+
+struct Tune {
+  mle::GemvConfig gemv{0, 0, 0};
+  mle::DecodeMfmaConfig dec{0, 0, 0, 0};
+};
+
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
-               int N, int K, int path, mle::GemvConfig cfg, hipStream_t stream) {
-  if (path == 0) path = M >= 64 ? 2 : 1;
+               int N, int K, int path, const Tune& tune, hipStream_t stream) {
+  if (path == 0) path = pick_path(M);
   if (path == 2)
     return check_launch(mle::launch_gemm_mfma(x, w, bias, y, M, N, K, stream),
                         "hip sgemm_nt Q8_0 launch failed");
+  if (path == 3) {
+    // MFMA decode in chunks of at most 16 tokens.
+    for (int m0 = 0; m0 < M; m0 += 16) {
+      const int mc = M - m0 < 16 ? M - m0 : 16;
+      mle::DecodeMfmaConfig c = tune.dec;
+      if (c.mt == 0) {
+        c = mle::decode_mfma_pick(mc, N, K);
+      } else if (c.mt < mc) {
+        return fail(MLE_INVALID_ARGUMENT, "hip sgemm_nt_q8_0_weight: MFMA token tile " +
+                                              std::to_string(c.mt) + " is smaller than M");
+      }
+      mle::SplitKWorkspace ws;
+      MLE_TRY(get_workspace(mle::decode_mfma_workspace(c, N, K), stream, &ws));
+      const hipError_t err = mle::launch_gemv_mfma(c, x + (int64_t)m0 * K, w, bias,
+                                                   y + (int64_t)m0 * N, mc, N, K, ws, stream);
+      if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 launch failed");
+    }
+    return ok();
+  }
   // FP32 GEMV in chunks of at most 8 tokens.
   for (int m0 = 0; m0 < M; m0 += 8) {
     const int mc = M - m0 < 8 ? M - m0 : 8;
-    mle::GemvConfig c = cfg;
+    mle::GemvConfig c = tune.gemv;
     if (c.mt == 0) {
       c = mle::gemv_pick_config(mc, N, K);
     } else if (c.mt < mc) {
@@ -111,7 +192,7 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
 
 extern "C" {
 
-int mle_q8_0_abi_version(void) { return 1; }
+int mle_q8_0_abi_version(void) { return 2; }
 
 const char* mle_last_error(void) { return g_last_error.c_str(); }
 
@@ -125,24 +206,39 @@ size_t mle_q8_0_bytes(int64_t numel) {
 int mle_q8_0_linear(const float* x, const uint8_t* w_q8_0, const float* bias, float* y,
                     int M, int N, int K, hipStream_t stream) {
   MLE_TRY(validate_linear(x, w_q8_0, bias, y, M, N, K));
-  return run_linear(x, w_q8_0, bias, y, M, N, K, 0, mle::GemvConfig{0, 0, 0}, stream);
+  return run_linear(x, w_q8_0, bias, y, M, N, K, 0, Tune{}, stream);
 }
 
 int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
-                       float* y, int M, int N, int K, int path, int mt, int lpr, int rw,
-                       hipStream_t stream) {
+                       float* y, int M, int N, int K, int path, int t0, int t1, int t2,
+                       int t3, hipStream_t stream) {
   MLE_TRY(validate_linear(x, w_q8_0, bias, y, M, N, K));
-  if (path < 0 || path > 2)
-    return fail(MLE_INVALID_ARGUMENT, "hip sgemm_nt_q8_0_weight: path must be 0, 1 or 2");
-  mle::GemvConfig cfg{mt, lpr, rw};
-  const bool all_zero = mt == 0 && lpr == 0 && rw == 0;
-  if (!all_zero && !mle::gemv_config_valid(cfg))
+  if (path < 0 || path > 3)
     return fail(MLE_INVALID_ARGUMENT,
-                "hip sgemm_nt_q8_0_weight: invalid GEMV launch shape (mt " +
-                    std::to_string(mt) + ", lpr " + std::to_string(lpr) + ", rw " +
-                    std::to_string(rw) + ")");
-  if (all_zero) cfg = mle::GemvConfig{0, 0, 0};
-  return run_linear(x, w_q8_0, bias, y, M, N, K, path, cfg, stream);
+                "hip sgemm_nt_q8_0_weight: path must be 0, 1, 2 or 3");
+  Tune tune;
+  const bool all_zero = t0 == 0 && t1 == 0 && t2 == 0 && t3 == 0;
+  if (!all_zero) {
+    if (path == 1) {
+      tune.gemv = mle::GemvConfig{t0, t1, t2};
+      if (t3 != 0 || !mle::gemv_config_valid(tune.gemv))
+        return fail(MLE_INVALID_ARGUMENT,
+                    "hip sgemm_nt_q8_0_weight: invalid GEMV launch shape (mt " +
+                        std::to_string(t0) + ", lpr " + std::to_string(t1) + ", rw " +
+                        std::to_string(t2) + ")");
+    } else if (path == 3) {
+      tune.dec = mle::DecodeMfmaConfig{t0, t1, t2, t3};
+      if (!mle::decode_mfma_config_valid(tune.dec))
+        return fail(MLE_INVALID_ARGUMENT,
+                    "hip sgemm_nt_q8_0_weight: invalid MFMA decode shape (mt " +
+                        std::to_string(t0) + ", waves " + std::to_string(t1) + ", ks " +
+                        std::to_string(t2) + ", splits " + std::to_string(t3) + ")");
+    } else {
+      return fail(MLE_INVALID_ARGUMENT,
+                  "hip sgemm_nt_q8_0_weight: a launch shape needs path 1 or 3");
+    }
+  }
+  return run_linear(x, w_q8_0, bias, y, M, N, K, path, tune, stream);
 }
 
 int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M, int N, int K,

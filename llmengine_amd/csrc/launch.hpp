@@ -21,6 +21,33 @@ hipError_t launch_gemv(const GemvConfig& cfg, const float* x, const uint8_t* w,
                        const float* bias, float* y, int M, int N, int K,
                        hipStream_t stream);
 
+// Linear decode on bf16 MFMA with FP32-exact activations (1 <= M <= 16 per
+// launch; larger M in chunks).  A workgroup of `waves` waves owns 16*waves output
+// rows and walks K in chunks of `ks` blocks (software-pipelined); K chunks are
+// split over `splits` workgroups whose partial sums meet in a workspace.
+struct DecodeMfmaConfig {
+  int mt;      // token tile: 1, 2, 4, 5, 8 or 16 (>= M)
+  int waves;   // waves per workgroup: 2, 4 or 8
+  int ks;      // K blocks per chunk: 8 or 16 (valid pairs: see config_valid)
+  int splits;  // workgroups along K (clamped to the number of chunks)
+};
+struct SplitKNeed {
+  int splits;             // workgroups along K
+  size_t partial_floats;  // workspace floats (0 when splits == 1)
+  size_t counters;        // per-tile arrival counters (0 when splits == 1)
+};
+struct SplitKWorkspace {
+  float* partials = nullptr;     // [splits][mt][N]
+  uint32_t* counters = nullptr;  // zero between launches (the kernel resets them)
+};
+int decode_mfma_tile(int M);
+DecodeMfmaConfig decode_mfma_pick(int M, int N, int K);
+bool decode_mfma_config_valid(const DecodeMfmaConfig& c);
+SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K);
+hipError_t launch_gemv_mfma(const DecodeMfmaConfig& c, const float* x, const uint8_t* w,
+                            const float* bias, float* y, int M, int N, int K,
+                            const SplitKWorkspace& ws, hipStream_t stream);
+
 // Linear GEMM on bf16 MFMA (prefill): same contract as launch_gemv, any M.
 hipError_t launch_gemm_mfma(const float* x, const uint8_t* w, const float* bias,
                             float* y, int M, int N, int K, hipStream_t stream);

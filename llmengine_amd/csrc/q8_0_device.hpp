@@ -47,27 +47,46 @@ struct Block {
   uint32_t scale_bits;
 };
 
-// Loads the 34-byte block starting at `blk` (2-byte aligned).
+// The raw loads of one block, not yet realigned: keeping these in registers
+// (instead of a Block) lets a software pipeline carry loads in flight across a
+// loop iteration, since nothing touches them until the block is consumed.
+struct RawBlock {
+  u32x4_a4 v0, v1;  // 32 bytes from the 4-aligned address at or after the block
+  uint32_t u;       // the remaining u16 (q30, q31 in case A; the scale in case B)
+  uint32_t mis;     // 0 (case A) or 2 (case B)
+};
+
+// Issues the loads of the 34-byte block starting at `blk` (2-byte aligned).
 //
 // Case A (blk % 4 == 0): 8 dwords from blk (scale + q0..q29) and the u16 at
 //   blk + 32 (q30, q31); quants are realigned by 2 bytes.
 // Case B (blk % 4 == 2): 8 dwords from blk + 2 (exactly q0..q31) and the u16 at
 //   blk (the scale).
 // Both cases read exactly bytes [blk, blk + 34).
-__device__ __forceinline__ Block load_block(const uint8_t* __restrict__ blk) {
-  const uint32_t mis = (uint32_t)((uintptr_t)blk & 2u);  // 0 (case A) or 2 (case B)
-  const uint8_t* p8 = blk + mis;                          // 4-byte aligned
-  const uint8_t* p2 = blk + (mis ? 0 : 32);
-  const u32x4_a4 v0 = *reinterpret_cast<const u32x4_a4*>(p8);
-  const u32x4_a4 v1 = *reinterpret_cast<const u32x4_a4*>(p8 + 16);
-  const uint32_t u = *reinterpret_cast<const uint16_t*>(p2);
-  const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, u};
-  const uint32_t sh = mis ? 0u : 2u;
+__device__ __forceinline__ RawBlock load_block_raw(const uint8_t* __restrict__ blk) {
+  RawBlock r;
+  r.mis = (uint32_t)((uintptr_t)blk & 2u);
+  const uint8_t* p8 = blk + r.mis;  // 4-byte aligned
+  const uint8_t* p2 = blk + (r.mis ? 0 : 32);
+  r.v0 = *reinterpret_cast<const u32x4_a4*>(p8);
+  r.v1 = *reinterpret_cast<const u32x4_a4*>(p8 + 16);
+  r.u = *reinterpret_cast<const uint16_t*>(p2);
+  return r;
+}
+
+// Realigns raw loads into quants + scale.
+__device__ __forceinline__ Block finish_block(const RawBlock& r) {
+  const uint32_t w[9] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w, r.u};
+  const uint32_t sh = r.mis ? 0u : 2u;
   Block b;
 #pragma unroll
   for (int i = 0; i < 8; ++i) b.q[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
-  b.scale_bits = mis ? u : (w[0] & 0xffffu);
+  b.scale_bits = r.mis ? r.u : (w[0] & 0xffffu);
   return b;
+}
+
+__device__ __forceinline__ Block load_block(const uint8_t* __restrict__ blk) {
+  return finish_block(load_block_raw(blk));
 }
 
 // Signed int8 byte j of a dword, as float (one v_cvt_f32_i32 with SDWA sext).

@@ -25,7 +25,7 @@ def declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     lib = capi.load()
-    assert lib.mle_q8_0_abi_version() == 1
+    assert lib.mle_q8_0_abi_version() == 2
     out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH],
                          stdout=subprocess.PIPE, text=True, check=True).stdout
     exported = set(re.findall(r" T (mle_\w+)", out))
@@ -66,10 +66,16 @@ def test_linear_validation_errors():
 
 def test_linear_ex_rejects_bad_launch_shape():
     lib = capi.load()
-    rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 1, 3, 32, 1, None)
+    rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 1, 3, 32, 1, 0, None)
     assert rc == 1 and "launch shape" in capi.last_error()
-    rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 5, 0, 0, 0, None)
+    rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 5, 0, 0, 0, 0, None)
     assert rc == 1 and "path" in capi.last_error()
+    # MFMA decode: token tile 3 does not exist, 6 waves is not a shape, 65 splits too many
+    for t in [(3, 4, 8, 0), (4, 6, 8, 0), (4, 4, 8, 65), (4, 4, 12, 1)]:
+        rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 3, *t, None)
+        assert rc == 1 and "MFMA decode shape" in capi.last_error(), t
+    rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 2, 1, 0, 0, 0, None)
+    assert rc == 1 and "path 1 or 3" in capi.last_error()
 
 
 def test_matmul_validation_errors():

@@ -33,14 +33,14 @@ def acts(seed, rows, cols, tag=S.TAG_X):
     return S.activations(seed, (rows, cols), tag=tag)
 
 
-def run_linear(dev, x, w, bias, M, N, K, path=0, mt=0, lpr=0, rw=0):
+def run_linear(dev, x, w, bias, M, N, K, path=0, **shape):
     dx, dw = to_dev(x, dev), to_dev(w, dev)
     db = to_dev(bias, dev) if bias is not None else None
     dy = empty_f32((M, N), dev)
-    if path == 0 and mt == 0:
+    if path == 0 and not shape:
         capi.linear(dx, dw, db, dy, M, N, K)
     else:
-        capi.linear_ex(dx, dw, db, dy, M, N, K, path=path, mt=mt, lpr=lpr, rw=rw)
+        capi.linear_ex(dx, dw, db, dy, M, N, K, path=path, **shape)
     return to_host(dy)
 
 
@@ -145,12 +145,11 @@ def test_linear_known_answers_exact(dev, golden):
         Q = np.array(c["quants"], np.int8)
         w = S.pack_q8_0_const_scale(Q, c["scale_bits"])
         x = np.array(c["activations"], np.float32).reshape(c["M"], c["K"])
-        for path in (1, 2):
+        # path 1 FP32 GEMV, 3 MFMA decode (exact bf16 parts), 2 bf16 MFMA GEMM
+        # (dyadic inputs with <= 8 significant bits stay exact there too)
+        for path in (1, 2, 3):
             got = run_linear(dev, x, w, None, c["M"], c["N"], c["K"], path=path)
-            if path == 1:
-                assert sha(got) == c["sha256"], (c["name"], path)
-            else:  # bf16 MFMA: dyadic inputs with <= 8 significant bits stay exact
-                assert sha(got) == c["sha256"], (c["name"], path)
+            assert sha(got) == c["sha256"], (c["name"], path)
 
 
 def test_linear_c1_full(dev, orc):
@@ -227,6 +226,126 @@ def test_linear_gemv_deterministic_and_linear(dev):
     torch.cuda.synchronize()
     assert torch.equal(y1a, y1b)
     assert rel_l2(to_host(y12), to_host(y1a) + to_host(y2)) <= GEMV_TOL
+
+
+# ----------------------------------------------------------------------------- linear MFMA decode
+
+DECODE_SHAPES = [(4, 8), (4, 16), (2, 8), (8, 8)]
+
+
+def test_linear_every_decode_mfma_shape(dev, orc):
+    """All (mt, waves, ks) instantiations of the MFMA decode kernel, each with and
+    without K splits, on a ragged shape (N = 77 rows, K = 1312: 41 blocks, so the
+    last K chunk is partial), M from mt-1 to mt, with bias."""
+    N, K = 77, 1312
+    w = weight(72, N, K)
+    bias = S.activations(73, (N,), tag=S.TAG_BIAS)
+    for mt in (1, 2, 4, 5, 8, 16):
+        for M in sorted({max(1, mt - 1), mt}):
+            x = acts(74 + M, M, K)
+            want = orc.linear(x, w, bias, M, N, K)
+            for waves, ks in DECODE_SHAPES:
+                for splits in (1, 2, 5, 64):
+                    note(f"decode mfma mt={mt} waves={waves} ks={ks} splits={splits} M={M}")
+                    got = run_linear(dev, x, w, bias, M, N, K, path=3, mt=mt, waves=waves,
+                                     ks=ks, splits=splits)
+                    assert rel_l2(got, want) <= GEMV_TOL, (mt, waves, ks, splits, M)
+
+
+@pytest.mark.parametrize("M", [2, 3, 5, 7, 16, 17, 40])
+def test_linear_decode_mfma_sizes(dev, orc, M):
+    """Automatic launch shapes for token counts between the tiles (and chunks of 16)."""
+    N, K = 1000, 2080
+    note(f"decode mfma M={M}")
+    w, x = weight(75, N, K), acts(76 + M, M, K)
+    got = run_linear(dev, x, w, None, M, N, K, path=3)
+    err = rel_l2(got, orc.sgemm_nt(x, w, M, N, K))
+    assert err <= GEMV_TOL, err
+
+
+def test_linear_decode_mfma_exact_parts_wide_range(dev, orc):
+    """Activations spanning 2^-60 .. 2^60 and values with all 24 significand bits
+    set: the three bf16 parts carry every bit, so the error stays at fp32
+    accumulation level (checked per token against the oracle)."""
+    M, N, K = 4, 96, 512
+    w = weight(77, N, K)
+    rng = np.random.default_rng(7)
+    mant = (1.0 + rng.integers(0, 1 << 23, size=(M, K)) / float(1 << 23)).astype(np.float64)
+    expo = rng.integers(-60, 61, size=(M, K))
+    sign = np.where(rng.integers(0, 2, size=(M, K)) == 1, -1.0, 1.0)
+    x = (sign * mant * np.exp2(expo)).astype(np.float32)
+    x[1] = (x[1] / 1e30).astype(np.float32)  # one token entirely tiny
+    note("decode mfma wide-range activations")
+    got = run_linear(dev, x, w, None, M, N, K, path=3)
+    want = orc.sgemm_nt(x, w, M, N, K)
+    for m in range(M):
+        assert rel_l2(got[m], want[m]) <= GEMV_TOL, m
+
+
+def test_linear_decode_mfma_nonfinite_activations(dev, orc):
+    """+-Inf and NaN activations propagate as in the reference's FP32 FMA chain:
+    same NaN positions, same signed infinities, finite values within 1e-5."""
+    M, N, K = 4, 130, 256
+    w = weight(78, N, K)
+    x = acts(79, M, K).copy()
+    x[0, 5] = np.inf
+    x[1, 40] = -np.inf
+    x[2, 7] = np.nan
+    x[3, 100] = np.inf
+    x[3, 101] = -np.inf
+    note("decode mfma non-finite activations")
+    got = run_linear(dev, x, w, None, M, N, K, path=3)
+    want = orc.sgemm_nt(x, w, M, N, K)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+    fin = np.isfinite(want)
+    assert np.array_equal(np.sign(got[np.isinf(want)]), np.sign(want[np.isinf(want)]))
+    assert rel_l2(got[fin], want[fin]) <= GEMV_TOL
+
+
+def test_linear_decode_mfma_split_k_deterministic(dev):
+    """QKV [12288, 4096] at M=8 runs 8 K splits: repeated launches are bitwise
+    identical (partials are added in split order), and equal across streams."""
+    import torch
+    M, N, K = 8, 12288, 4096
+    note("decode mfma split-K determinism")
+    dw, dx = to_dev(weight(2, N, K), dev), to_dev(acts(2 + M, M, K), dev)
+    ya, yb = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    capi.linear(dx, dw, None, ya, M, N, K)
+    for _ in range(3):
+        capi.linear(dx, dw, None, yb, M, N, K)
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb)
+    s2 = torch.cuda.Stream()
+    yc = empty_f32((M, N), dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s2):
+        capi.linear(dx, dw, None, yc, M, N, K, stream=s2)
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yc)
+
+
+def test_linear_decode_mfma_two_streams_concurrently(dev, orc):
+    """Two streams, each with its own split-K workspace, interleaving launches of
+    different shapes; every result matches the oracle."""
+    import torch
+    note("decode mfma two streams")
+    shapes = [(8, 4096, 4096), (4, 1024, 11008)]
+    data = []
+    for i, (M, N, K) in enumerate(shapes):
+        w, x = weight(120 + i, N, K), acts(121 + i, M, K)
+        data.append((M, N, K, w, x, to_dev(w, dev), to_dev(x, dev),
+                     [empty_f32((M, N), dev) for _ in range(4)]))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for j in range(4):
+        for (M, N, K, _, _, dw, dx, ys), s in zip(data, streams):
+            capi.linear(dx, dw, None, ys[j], M, N, K, stream=s)
+    torch.cuda.synchronize()
+    for M, N, K, w, x, _, _, ys in data:
+        want = orc.sgemm_nt(x, w, M, N, K)
+        for y in ys:
+            assert rel_l2(to_host(y), want) <= GEMV_TOL
 
 
 # ----------------------------------------------------------------------------- linear MFMA
