@@ -118,8 +118,8 @@ size_t mle_q8_0_bytes(int64_t numel);
  *     path 1: t0 = token tile mt in {1,2,4,8} >= min(M,8), t1 = lanes per row
  *             in {16,32,64}, t2 = rows per lane group in {1,2,4,8}, t3 = 0;
  *     path 3: t0 = token tile in {1,2,4,5,8,16} >= min(M,16), t1 = waves per
- *             workgroup, t2 = K blocks per chunk ((4,8), (4,16), (2,8), (8,8)),
- *             t3 = K splits in [0, 64] (0 or 1 = no split).
+ *             workgroup in {2,4,8} (16 rows each), t2 = K blocks per
+ *             workgroup in {16, 32} (32 only for a token tile <= 8), t3 = 0.
  */
 int mle_q8_0_f16_decode(const uint16_t* bits, float* out, int64_t n,
                         hipStream_t stream);

@@ -109,14 +109,14 @@ def linear(x, w, bias, y, M, N, K, stream=None) -> None:
     _raise(linear_status(x, w, bias, y, M, N, K, stream)[0])
 
 
-def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, ks=0,
-              splits=0, stream=None) -> None:
+def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice=0,
+              stream=None) -> None:
     """Linear with a forced path and launch shape (test / tuning hook).
 
-    path 1 (FP32 GEMV) takes mt, lpr, rw; path 3 (MFMA decode) takes mt, waves, ks,
-    splits; all zero = automatic."""
+    path 1 (FP32 GEMV) takes mt, lpr, rw; path 3 (MFMA decode) takes mt, waves,
+    kslice; all zero = automatic."""
     if path == 3:
-        t = (mt, waves, ks, splits)
+        t = (mt, waves, kslice, 0)
     else:
         t = (mt, lpr, rw, 0)
     rc = load().mle_q8_0_linear_ex(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K,

@@ -143,12 +143,17 @@ int pick_path(int M) { return M >= 64 ? 2 : M == 1 ? 1 : 3; }
 
 struct Tune {
   mle::GemvConfig gemv{0, 0, 0};
-  mle::DecodeMfmaConfig dec{0, 0, 0, 0};
+  mle::DecodeMfmaConfig dec{0, 0, 0};
 };
 
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
                int N, int K, int path, const Tune& tune, hipStream_t stream) {
-  if (path == 0) path = pick_path(M);
+  if (path == 0) {
+    path = pick_path(M);
+    if (path == 3 && !mle::decode_mfma_fits(mle::decode_mfma_pick(M < 16 ? M : 16, N, K),
+                                            M < 16 ? M : 16, N, K))
+      path = 1;
+  }
   if (path == 2)
     return check_launch(mle::launch_gemm_mfma(x, w, bias, y, M, N, K, stream),
                         "hip sgemm_nt Q8_0 launch failed");
@@ -227,12 +232,12 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
                         std::to_string(t0) + ", lpr " + std::to_string(t1) + ", rw " +
                         std::to_string(t2) + ")");
     } else if (path == 3) {
-      tune.dec = mle::DecodeMfmaConfig{t0, t1, t2, t3};
-      if (!mle::decode_mfma_config_valid(tune.dec))
+      tune.dec = mle::DecodeMfmaConfig{t0, t1, t2};
+      if (t3 != 0 || !mle::decode_mfma_config_valid(tune.dec))
         return fail(MLE_INVALID_ARGUMENT,
                     "hip sgemm_nt_q8_0_weight: invalid MFMA decode shape (mt " +
-                        std::to_string(t0) + ", waves " + std::to_string(t1) + ", ks " +
-                        std::to_string(t2) + ", splits " + std::to_string(t3) + ")");
+                        std::to_string(t0) + ", waves " + std::to_string(t1) + ", kslice " +
+                        std::to_string(t2) + ")");
     } else {
       return fail(MLE_INVALID_ARGUMENT,
                   "hip sgemm_nt_q8_0_weight: a launch shape needs path 1 or 3");

@@ -27,15 +27,14 @@
 //
 // Work split.  A workgroup of W waves owns 16 W output rows (wave w: rows
 // 16w .. 16w+15, so no cross-wave reduction) and a range of K chunks of KS
-// blocks.  Lane l loads whole 34-byte blocks: row l % 16, blocks 4u + l / 16 of
-// the chunk (u = 0 .. KS/4-1), i.e. every row's blocks in 136-byte runs.  A 4 x 4
-// transpose of 8-byte quant chunks across the four 16-lane rows
-// (v_permlane32_swap then v_permlane16_swap, 8 instructions per 4 blocks) turns
-// those registers straight into MFMA A fragments, with no LDS round trip.
-// Software pipeline: the loads of chunk c+1 (weights and the activations of its K
-// slice) are in flight while chunk c is multiplied; the activation split of chunk
-// c+1 goes to the other half of a double-buffered LDS B-fragment area; one
-// barrier per chunk.
+// blocks.  Lane l loads whole 34-byte blocks through a buffer resource: row
+// l % 16, blocks 4u + l / 16 of the chunk (u = 0 .. KS/4-1).  A 4 x 4 transpose
+// of 8-byte quant chunks across the four 16-lane rows (v_permlane32_swap then
+// v_permlane16_swap, 8 instructions per 4 blocks) turns those registers straight
+// into MFMA A fragments, with no LDS round trip.  Software pipeline: the weight
+// loads of chunks c+1 and c+2 and the activation loads of chunk c+1 are in
+// flight while chunk c is multiplied; the activation split of chunk c+1 goes to
+// the other half of a double-buffered LDS B-fragment area; one barrier per chunk.
 //
 // Split K.  When there are too few row tiles to fill the GPU, the K chunks are
 // split over gridDim.y workgroups.  Each stores its 16 W x MT partial sums to its
@@ -60,19 +59,42 @@ __device__ __forceinline__ uint32_t top_halves(uint32_t lo_word, uint32_t hi_wor
   return __builtin_amdgcn_perm(hi_word, lo_word, 0x07060302u);
 }
 
-// Splits 8 activations into packed bf16 hi / mid / lo parts (4 dwords each).
-__device__ __forceinline__ void split3(const float (&v)[8], uint32_t (&hi)[4],
-                                       uint32_t (&mid)[4], uint32_t (&lo)[4]) {
+// Splits 8 activations into packed bf16 hi / mid / lo parts (4 dwords each):
+// hi = x with the low 16 bits cleared, r = x - hi (exact), mid = r with the low
+// 16 bits cleared, lo = r - mid (exact, <= 8 significant bits).  Finite x only.
+__device__ __forceinline__ void split3_finite(const float (&v)[8], uint32_t (&hi)[4],
+                                              uint32_t (&mid)[4], uint32_t (&lo)[4]) {
+  uint32_t hb[8], rb[8], lb[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v[j]);
+    const float r = v[j] - __builtin_bit_cast(float, b & 0xffff0000u);
+    const uint32_t r_bits = __builtin_bit_cast(uint32_t, r);
+    const float l = r - __builtin_bit_cast(float, r_bits & 0xffff0000u);
+    hb[j] = b;
+    rb[j] = r_bits;
+    lb[j] = __builtin_bit_cast(uint32_t, l);
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    hi[p] = top_halves(hb[2 * p], hb[2 * p + 1]);
+    mid[p] = top_halves(rb[2 * p], rb[2 * p + 1]);
+    lo[p] = top_halves(lb[2 * p], lb[2 * p + 1]);
+  }
+}
+
+// Same split for any x: +-Inf is carried whole in hi (mid = lo = 0; x - hi would
+// be NaN) and NaN stays NaN in every part.
+__device__ __forceinline__ void split3_any(const float (&v)[8], uint32_t (&hi)[4],
+                                           uint32_t (&mid)[4], uint32_t (&lo)[4]) {
   uint32_t hb[8], rb[8], lb[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t b = __builtin_bit_cast(uint32_t, v[j]);
     const float h = __builtin_bit_cast(float, b & 0xffff0000u);
-    // x == h covers +-Inf (x - h would be NaN) and values already exact in bf16.
     const float r = (v[j] == h) ? 0.0f : v[j] - h;
     const uint32_t r_bits = __builtin_bit_cast(uint32_t, r);
-    const float m = __builtin_bit_cast(float, r_bits & 0xffff0000u);
-    const float l = r - m;
+    const float l = r - __builtin_bit_cast(float, r_bits & 0xffff0000u);
     hb[j] = b;
     rb[j] = r_bits;
     lb[j] = __builtin_bit_cast(uint32_t, l);
@@ -126,32 +148,59 @@ struct Cols {
   static constexpr int PADC = 16 * P - 3 * MT;  // virtual columns that stay zero
 };
 
-template <int MT, int W, int KS>
+template <int MT, int W, int KSL>
 struct Shape {
   static constexpr int NT = 64 * W;               // threads
   static constexpr int R = 16 * W;                // output rows per workgroup
   static constexpr int P = Cols<MT>::P;
+  static constexpr int KS = 8;                    // blocks per chunk (one load set pair)
   static constexpr int NL = KS / 4;               // blocks per lane per chunk
-  static constexpr int BBUF = KS * P * 1024;      // B fragments of one chunk (bytes)
-  static constexpr int XITEMS = MT * KS * 4;      // (token, block, 8-wide k chunk)
+  static constexpr int NCH = KSL / KS;            // chunks per workgroup
+  static constexpr int BBUF = KSL * P * 1024;     // B fragments of the K slice (bytes)
+  static constexpr int XITEMS = MT * KSL * 4;     // (token, k chunk, block)
   static constexpr int XPT = (XITEMS + NT - 1) / NT;
   static constexpr int OUTS = 16 * MT;            // outputs per wave
   static constexpr int OPL = (OUTS + 63) / 64;    // outputs per lane
 };
 
-template <int MT, int W, int KS>
+// Byte offset of B-fragment slot (block kb, MFMA p, k chunk c, virtual column n).
+// The 16-byte slot of lane (c, n) sits at position (n + ROT c) % 16 of its
+// 16-slot row: the activation split runs tokens fastest, so 16 consecutive
+// threads write (8 tokens x 2 k chunks) or (4 x 4) distinct slots of a 256-byte
+// bank row, and an MFMA read of a fragment is a permutation within each row.
+// Fragments are 1 KB apart, so a lane's read address is one register plus an
+// immediate per (block, MFMA).
+template <int MT>
+struct Slot {
+  static constexpr int ROT = MT >= 8 ? 8 : 4;
+};
+template <int MT, int P>
+__device__ __forceinline__ int bslot(int kb, int p, int c, int n) {
+  return ((kb * P + p) * 64 + c * 16 + ((n + Slot<MT>::ROT * c) & 15)) * 16;
+}
+
+// Buffer resource over [base, base + bytes): loads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+template <int MT, int W, int KSL>
 __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K,
-    int chunks_per_split, float* __restrict__ partials, uint32_t* __restrict__ counters) {
-  using S = Shape<MT, W, KS>;
+    float* __restrict__ partials, uint32_t* __restrict__ counters) {
+  using S = Shape<MT, W, KSL>;
   constexpr int P = S::P;
+  constexpr int KS = S::KS;
   constexpr int NL = S::NL;
+  constexpr int NCH = S::NCH;
   constexpr int XPT = S::XPT;
-  static_assert(KS % 4 == 0, "chunk = whole load sets of 4 blocks");
-  __shared__ __attribute__((aligned(16))) uint8_t bfr[2][S::BBUF];
+  static_assert(KSL % KS == 0, "K slice = whole chunks");
+  __shared__ __attribute__((aligned(16))) uint8_t bfr[S::BBUF];
   __shared__ __attribute__((aligned(16))) float scl[W][KS][16];
   __shared__ float red[W][16][17];
+  __shared__ __attribute__((aligned(16))) uint8_t xdummy[16];
   __shared__ uint32_t arrived;
 
   const int tid = threadIdx.x;
@@ -159,97 +208,111 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   const int wave = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
   const int KB = K / kBlockElems;
-  const int n_chunks = (KB + KS - 1) / KS;
-  const int c_begin = blockIdx.y * chunks_per_split;
-  const int c_end = min(c_begin + chunks_per_split, n_chunks);
+  const uint32_t row_bytes = (uint32_t)KB * kBlockBytes;
+  const int kb0 = blockIdx.y * KSL;                 // first block of this K slice
+  const int nblk = min(KSL, KB - kb0);              // blocks in this slice
   const int64_t n0 = (int64_t)blockIdx.x * S::R;
-  // This lane's weight row; rows past N are clamped (outputs dropped at the end).
-  const int64_t my_row = min(n0 + wave * 16 + r16, (int64_t)N - 1);
-  const uint8_t* wrow = w + my_row * ((int64_t)KB * kBlockBytes);
 
-  auto load_w = [&](int c, RawBlock (&b)[NL]) {
+  // Weights: one buffer resource over this workgroup's rows (rows past N read
+  // as zero).  Lane (g, r16) of wave w loads row 16w + r16, blocks
+  // kb0 + 8c + 4u + g: a per-lane constant offset plus a wave-uniform one.  The
+  // uniform part is a multiple of 4 (34 * 4u, 34 * 8c), so each lane's block
+  // alignment (the realignment case of load_block_raw) never changes.
+  const uint8_t* wbase = w + n0 * row_bytes;
+  const int64_t rows_here = min((int64_t)S::R, (int64_t)N - n0);
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(wbase, (uint32_t)(rows_here * row_bytes));
+  const uint32_t lane_off = (uint32_t)(wave * 16 + r16) * row_bytes +
+                            (uint32_t)(kb0 + g) * kBlockBytes;
+  const uint32_t mis = (uint32_t)(((uintptr_t)wbase + lane_off) & 2u);
+  const uint32_t voff = lane_off + mis;
+  const uint32_t uoff = lane_off + (mis ? 0u : 32u);
+
+  // 1. Every weight load of this wave's 16 rows x KSL blocks, issued up front.
+  //    Blocks past the slice's end read as zeros (offset past the buffer).
+  RawBlock wr[NCH][NL];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
-      const int kb = min(c * KS + 4 * u + g, KB - 1);
-      b[u] = load_block_raw(wrow + (int64_t)kb * kBlockBytes);
+      const int b = KS * c + 4 * u;  // first block of the load set (lane adds g)
+      const uint32_t soff = b < nblk ? (uint32_t)b * kBlockBytes : 0x80000000u;
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrs, voff, soff, 0);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrs, voff + 16, soff, 0);
+      wr[c][u].v0 = u32x4_a4{v0.x, v0.y, v0.z, v0.w};
+      wr[c][u].v1 = u32x4_a4{v1.x, v1.y, v1.z, v1.w};
+      wr[c][u].u = __builtin_amdgcn_raw_buffer_load_b16(wrs, uoff, soff, 0);
+      wr[c][u].mis = mis;
     }
-  };
-  auto load_x = [&](int c, float (&xv)[XPT][8]) {
+
+  // 2. B fragments of the whole K slice (activations split into bf16 parts),
+  //    shared by the workgroup's waves.  B fragment (block kb, MFMA p): lane l
+  //    holds virtual column l % 16, k = 8 (l/16) .. +7.  Items past the end
+  //    (token >= M, block >= nblk, or no item) read zeros; every thread runs
+  //    every slot, those past XITEMS writing a dummy LDS slot.
+  {
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)((int64_t)M * K * 4));
+    f32x4 xv[XPT][2];
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int it = tid + S::NT * i;
-      const int m = it / (KS * 4), q = it % (KS * 4);
-      const int kbg = c * KS + (q >> 2);
-      if (it < S::XITEMS && m < M && kbg < KB) {
-        const f32x4* xp = reinterpret_cast<const f32x4*>(
-            x + (int64_t)m * K + (int64_t)kbg * kBlockElems + 8 * (q & 3));
-        const f32x4 a = xp[0], b = xp[1];
-        xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
-        xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xv[i][j] = 0.0f;
-      }
+      const int m = it % MT, q = it / MT;  // item = (token fastest, k chunk, block)
+      const int kb = q >> 2;
+      const uint32_t off = it < S::XITEMS && kb < nblk
+                               ? (uint32_t)((m * K + (kb0 + kb) * kBlockElems + 8 * (q & 3)) * 4)
+                               : 0x80000000u;
+      xv[i][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+      xv[i][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16, 0, 0));
     }
-  };
-  // B fragment (block kb, MFMA p): lane l holds virtual column l % 16, k = 8 (l/16) .. +7.
-  auto prep_x = [&](const float (&xv)[XPT][8], uint8_t* buf) {
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int it = tid + S::NT * i;
-      if (it >= S::XITEMS) continue;
-      const int m = it / (KS * 4), q = it % (KS * 4);
+      const bool real = S::XITEMS % S::NT == 0 || it < S::XITEMS;
+      const int m = it % MT, q = it / MT;
       const int kb = q >> 2, c = q & 3;
+      const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                          xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+      bool finite = true;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) finite &= !__builtin_amdgcn_class(v[j], 0x207);  // NaN, +-Inf
       uint32_t parts[3][4];
-      split3(xv[i], parts[0], parts[1], parts[2]);
+      if (__builtin_expect(finite, 1))
+        split3_finite(v, parts[0], parts[1], parts[2]);
+      else
+        split3_any(v, parts[0], parts[1], parts[2]);
 #pragma unroll
       for (int part = 0; part < 3; ++part) {
         const int vc = part * MT + m;
-        u32x4* dst = reinterpret_cast<u32x4*>(
-            buf + ((kb * P + (vc >> 4)) * 64 + c * 16 + (vc & 15)) * 16);
-        *dst = u32x4{parts[part][0], parts[part][1], parts[part][2], parts[part][3]};
+        uint8_t* dst = real ? bfr + bslot<MT, P>(kb, vc >> 4, c, vc & 15) : xdummy;
+        *reinterpret_cast<u32x4*>(dst) =
+            u32x4{parts[part][0], parts[part][1], parts[part][2], parts[part][3]};
       }
     }
-  };
-
-  // Virtual columns past 3*MT are never written by prep_x: zero them once.
-  if constexpr (Cols<MT>::PADC > 0) {
-    constexpr int PADC = Cols<MT>::PADC;
-    for (int it = tid; it < 2 * KS * 4 * PADC; it += S::NT) {
-      const int bsel = it / (KS * 4 * PADC);
-      const int rest = it % (KS * 4 * PADC);
-      const int kb = rest / (4 * PADC), q = rest % (4 * PADC);
-      const int c = q / PADC, vc = 3 * MT + q % PADC;
-      *reinterpret_cast<u32x4*>(bfr[bsel] + ((kb * P + (vc >> 4)) * 64 + c * 16 + (vc & 15)) *
-                                                16) = u32x4{0u, 0u, 0u, 0u};
+    // Virtual columns past 3*MT are never written above: zero them.
+    if constexpr (Cols<MT>::PADC > 0) {
+      constexpr int PADC = Cols<MT>::PADC;
+      for (int it = tid; it < KSL * 4 * PADC; it += S::NT) {
+        const int kb = it / (4 * PADC), q = it % (4 * PADC);
+        const int c = q / PADC, vc = 3 * MT + q % PADC;
+        *reinterpret_cast<u32x4*>(bfr + bslot<MT, P>(kb, vc >> 4, c, vc & 15)) =
+            u32x4{0u, 0u, 0u, 0u};
+      }
     }
   }
-
-  RawBlock wc[NL];
-  float xv[XPT][8];
-  load_x(c_begin, xv);
-  load_w(c_begin, wc);
-  prep_x(xv, bfr[0]);
   __syncthreads();
 
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c = c_begin; c < c_end; ++c) {
-    const int buf = (c - c_begin) & 1;
-    const bool more = c + 1 < c_end;
-    RawBlock wn[NL];
-    if (more) {
-      load_x(c + 1, xv);
-      load_w(c + 1, wn);
-    }
-    // Scales of this chunk: lane (g, r16) holds blocks 4u+g of row r16.
+  // 3. Each wave multiplies its rows chunk by chunk as the loads land: realign,
+  //    scales to (wave-private) LDS, in-register transpose into A fragments,
+  //    P chained MFMAs per block, fp32 scale FMA.  No barrier.
+  f32x4 accs[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
     Block blk[NL];
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
-      blk[u] = finish_block(wc[u]);
-      const bool valid = c * KS + 4 * u + g < KB;
+      blk[u] = finish_block(wr[c][u]);
+      const bool valid = KS * c + 4 * u + g < nblk;
       scl[wave][4 * u + g][r16] = valid ? scale_to_f32_fast(blk[u].scale_bits) : 0.0f;
     }
-    const uint8_t* bb = bfr[buf];
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
       uint32_t q[8];
@@ -258,31 +321,28 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
       transpose_chunks(q);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int kb = 4 * u + j;
+        const int kc = 4 * u + j;        // block within the chunk
+        const int kb = KS * c + kc;      // block within the slice
         const bf16x8_t a = quants_to_bf16(q[2 * j], q[2 * j + 1]);
         f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            a, *reinterpret_cast<const bf16x8_t*>(bb + ((kb * P) * 64 + lane) * 16),
+            a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot<MT, P>(kb, 0, g, r16)),
             f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
         for (int p = 1; p < P; ++p)
           d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              a, *reinterpret_cast<const bf16x8_t*>(bb + ((kb * P + p) * 64 + lane) * 16), d,
-              0, 0, 0);
+              a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot<MT, P>(kb, p, g, r16)), d, 0,
+              0, 0);
         // D layout: lane l holds rows 4 (l/16) + v (v = 0..3), virtual column l % 16.
-        const f32x4 s = *reinterpret_cast<const f32x4*>(&scl[wave][kb][4 * g]);
-        acc.x = __builtin_fmaf(s.x, d.x, acc.x);
-        acc.y = __builtin_fmaf(s.y, d.y, acc.y);
-        acc.z = __builtin_fmaf(s.z, d.z, acc.z);
-        acc.w = __builtin_fmaf(s.w, d.w, acc.w);
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(&scl[wave][kc][4 * g]);
+        f32x4& a4 = accs[j & 1];
+        a4.x = __builtin_fmaf(sc.x, d.x, a4.x);
+        a4.y = __builtin_fmaf(sc.y, d.y, a4.y);
+        a4.z = __builtin_fmaf(sc.z, d.z, a4.z);
+        a4.w = __builtin_fmaf(sc.w, d.w, a4.w);
       }
     }
-    if (more) {
-      prep_x(xv, bfr[buf ^ 1]);
-#pragma unroll
-      for (int u = 0; u < NL; ++u) wc[u] = wn[u];
-    }
-    __syncthreads();
   }
+  const f32x4 acc = accs[0] + accs[1];
 
   // Sum the part columns of each token (within the wave).
   red[wave][4 * g + 0][r16] = acc.x;
@@ -315,24 +375,32 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
     return;
   }
 
-  // Split K: partials [tile][split][wave][MT][16], then the last workgroup reduces.
+  // Split K: partials [tile][split][wave][MT][16], then the last workgroup
+  // reduces.  The partials travel by device-scope (sc1: L2 write-through /
+  // coherent) buffer stores and loads; plain (non-atomic) accesses, so the S
+  // loads of the reduction issue together instead of one round trip each.
   constexpr int REGION = S::R * MT;
-  float* tile_part = partials + (int64_t)blockIdx.x * gridDim.y * REGION;
+  constexpr int SC1 = 16;  // cache-policy bit: device scope
+  const __amdgpu_buffer_rsrc_t prs =
+      make_rsrc(partials + (int64_t)blockIdx.x * gridDim.y * REGION,
+                (uint32_t)(gridDim.y * REGION * 4));
 #pragma unroll
   for (int o = 0; o < S::OPL; ++o) {
     const int idx = lane + 64 * o;
     if (idx < S::OUTS && (idx >> 4) < M)
-      __hip_atomic_store(tile_part + (int64_t)blockIdx.y * REGION + wave * S::OUTS + idx,
-                         outv[o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_raw_buffer_store_b32(
+          __builtin_bit_cast(uint32_t, outv[o]), prs,
+          (uint32_t)((blockIdx.y * REGION + wave * S::OUTS + idx) * 4), 0, SC1);
   }
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_waitcnt(0);  // every partial has reached the coherence point
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   if (tid == 0)
     arrived = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   if (arrived != gridDim.y - 1) return;
 #pragma unroll
   for (int o = 0; o < S::OPL; ++o) {
@@ -341,9 +409,11 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
     const int64_t n = n0 + wave * 16 + rr;
     if (idx >= S::OUTS || m >= M || n >= N) continue;
     float s = 0.0f;
+#pragma unroll 8
     for (unsigned sp = 0; sp < gridDim.y; ++sp)
-      s += __hip_atomic_load(tile_part + (int64_t)sp * REGION + wave * S::OUTS + idx,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         prs, (uint32_t)((sp * REGION + wave * S::OUTS + idx) * 4),
+                                         0, SC1));
     y[(int64_t)m * N + n] = s + (bias ? bias[n] : 0.0f);
   }
   if (tid == 0)
@@ -352,29 +422,23 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
 
 struct Grid {
   unsigned tiles, splits;
-  int chunks_per_split;
 };
 
 Grid grid_of(const DecodeMfmaConfig& c, int N, int K) {
   const int KB = K / kBlockElems;
-  const int n_chunks = (KB + c.ks - 1) / c.ks;
-  const int rows = 16 * c.waves;
   Grid gr;
-  gr.tiles = (unsigned)((N + rows - 1) / rows);
-  int splits = c.splits > 0 ? c.splits : 1;
-  if (splits > n_chunks) splits = n_chunks;
-  gr.chunks_per_split = (n_chunks + splits - 1) / splits;
-  gr.splits = (unsigned)((n_chunks + gr.chunks_per_split - 1) / gr.chunks_per_split);
+  gr.tiles = (unsigned)((N + 16 * c.waves - 1) / (16 * c.waves));
+  gr.splits = (unsigned)((KB + c.kslice - 1) / c.kslice);
   return gr;
 }
 
-template <int MT, int W, int KS>
+template <int MT, int W, int KSL>
 hipError_t launch_t(const Grid& gr, const float* x, const uint8_t* w, const float* bias,
                     float* y, int M, int N, int K, const SplitKWorkspace& ws,
                     hipStream_t stream) {
-  hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KS>), dim3(gr.tiles, gr.splits),
-                     dim3(64 * W), 0, stream, x, w, bias, y, M, N, K, gr.chunks_per_split,
-                     ws.partials, ws.counters);
+  hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KSL>), dim3(gr.tiles, gr.splits),
+                     dim3(64 * W), 0, stream, x, w, bias, y, M, N, K, ws.partials,
+                     ws.counters);
   return hipGetLastError();
 }
 
@@ -382,10 +446,18 @@ template <int MT>
 hipError_t dispatch_shape(const DecodeMfmaConfig& c, const Grid& gr, const float* x,
                           const uint8_t* w, const float* bias, float* y, int M, int N, int K,
                           const SplitKWorkspace& ws, hipStream_t stream) {
-  if (c.waves == 4 && c.ks == 8) return launch_t<MT, 4, 8>(gr, x, w, bias, y, M, N, K, ws, stream);
-  if (c.waves == 4 && c.ks == 16) return launch_t<MT, 4, 16>(gr, x, w, bias, y, M, N, K, ws, stream);
-  if (c.waves == 2 && c.ks == 8) return launch_t<MT, 2, 8>(gr, x, w, bias, y, M, N, K, ws, stream);
-  if (c.waves == 8 && c.ks == 8) return launch_t<MT, 8, 8>(gr, x, w, bias, y, M, N, K, ws, stream);
+  if (c.kslice == 16) {
+    if (c.waves == 2) return launch_t<MT, 2, 16>(gr, x, w, bias, y, M, N, K, ws, stream);
+    if (c.waves == 4) return launch_t<MT, 4, 16>(gr, x, w, bias, y, M, N, K, ws, stream);
+    if (c.waves == 8) return launch_t<MT, 8, 16>(gr, x, w, bias, y, M, N, K, ws, stream);
+  }
+  if constexpr (Cols<MT>::P <= 2) {
+    if (c.kslice == 32) {
+      if (c.waves == 2) return launch_t<MT, 2, 32>(gr, x, w, bias, y, M, N, K, ws, stream);
+      if (c.waves == 4) return launch_t<MT, 4, 32>(gr, x, w, bias, y, M, N, K, ws, stream);
+      if (c.waves == 8) return launch_t<MT, 8, 32>(gr, x, w, bias, y, M, N, K, ws, stream);
+    }
+  }
   return hipErrorInvalidValue;
 }
 
@@ -393,9 +465,10 @@ hipError_t dispatch_shape(const DecodeMfmaConfig& c, const Grid& gr, const float
 
 bool decode_mfma_config_valid(const DecodeMfmaConfig& c) {
   const bool mt = c.mt == 1 || c.mt == 2 || c.mt == 4 || c.mt == 5 || c.mt == 8 || c.mt == 16;
-  const bool shape = (c.waves == 4 && (c.ks == 8 || c.ks == 16)) ||
-                     (c.waves == 2 && c.ks == 8) || (c.waves == 8 && c.ks == 8);
-  return mt && shape && c.splits >= 0 && c.splits <= 64;
+  const bool waves = c.waves == 2 || c.waves == 4 || c.waves == 8;
+  // A 32-block K slice of 3-MFMA (16-token) fragments would need 96 KB of LDS.
+  const bool kslice = c.kslice == 16 || (c.kslice == 32 && c.mt <= 8);
+  return mt && waves && kslice;
 }
 
 int decode_mfma_tile(int M) {
@@ -403,17 +476,15 @@ int decode_mfma_tile(int M) {
 }
 
 DecodeMfmaConfig decode_mfma_pick(int M, int N, int K) {
+  // Measured on MI355X over the BASELINE decode shapes: 16-block K slices
+  // (one-shot workgroups of ~35 KB) beat 32 unless K fits one 32-block slice
+  // (no split-K hand-off at all); 8 waves per workgroup pay off for 8+ tokens
+  // on wide weights, 4 otherwise.
   DecodeMfmaConfig c;
   c.mt = decode_mfma_tile(M);
-  c.waves = 4;
-  c.ks = 8;
-  // Enough workgroups to give every CU about two: split K when row tiles are few.
-  const int tiles = (N + 16 * c.waves - 1) / (16 * c.waves);
-  const int n_chunks = (K / kBlockElems + c.ks - 1) / c.ks;
-  int splits = (512 + tiles - 1) / tiles;
-  if (splits > n_chunks) splits = n_chunks;
-  if (splits < 1) splits = 1;
-  c.splits = splits;
+  const int KB = K / kBlockElems;
+  c.kslice = (c.mt <= 8 && KB <= 32) ? 32 : 16;
+  c.waves = (c.mt >= 8 && N >= 8192) ? 8 : 4;
   return c;
 }
 
@@ -427,9 +498,19 @@ SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K) {
   return need;
 }
 
+bool decode_mfma_fits(const DecodeMfmaConfig& c, int M, int N, int K) {
+  // Buffer offsets are 32-bit: one workgroup's rows of weights and all M rows of
+  // activations must stay below 2^31 bytes.
+  const int64_t row_bytes = (int64_t)(K / kBlockElems) * kBlockBytes;
+  (void)N;
+  return (int64_t)16 * c.waves * row_bytes < (int64_t(1) << 31) &&
+         (int64_t)M * K * 4 < (int64_t(1) << 31);
+}
+
 hipError_t launch_gemv_mfma(const DecodeMfmaConfig& c, const float* x, const uint8_t* w,
                             const float* bias, float* y, int M, int N, int K,
                             const SplitKWorkspace& ws, hipStream_t stream) {
+  if (!decode_mfma_fits(c, M, N, K)) return hipErrorInvalidValue;
   const Grid gr = grid_of(c, N, K);
   switch (c.mt) {
     case 1: return dispatch_shape<1>(c, gr, x, w, bias, y, M, N, K, ws, stream);

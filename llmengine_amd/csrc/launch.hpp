@@ -23,13 +23,12 @@ hipError_t launch_gemv(const GemvConfig& cfg, const float* x, const uint8_t* w,
 
 // Linear decode on bf16 MFMA with FP32-exact activations (1 <= M <= 16 per
 // launch; larger M in chunks).  A workgroup of `waves` waves owns 16*waves output
-// rows and walks K in chunks of `ks` blocks (software-pipelined); K chunks are
-// split over `splits` workgroups whose partial sums meet in a workspace.
+// rows and a K slice of `kslice` blocks; the K slices of a row tile meet in a
+// split-K workspace.
 struct DecodeMfmaConfig {
   int mt;      // token tile: 1, 2, 4, 5, 8 or 16 (>= M)
   int waves;   // waves per workgroup: 2, 4 or 8
-  int ks;      // K blocks per chunk: 8 or 16 (valid pairs: see config_valid)
-  int splits;  // workgroups along K (clamped to the number of chunks)
+  int kslice;  // K blocks per workgroup: 16 or 32 (32 only for mt <= 8)
 };
 struct SplitKNeed {
   int splits;             // workgroups along K
@@ -44,6 +43,9 @@ int decode_mfma_tile(int M);
 DecodeMfmaConfig decode_mfma_pick(int M, int N, int K);
 bool decode_mfma_config_valid(const DecodeMfmaConfig& c);
 SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K);
+// False when the shape's buffer offsets would not fit 32 bits (the caller then
+// takes the FP32 GEMV path, which uses 64-bit addressing).
+bool decode_mfma_fits(const DecodeMfmaConfig& c, int M, int N, int K);
 hipError_t launch_gemv_mfma(const DecodeMfmaConfig& c, const float* x, const uint8_t* w,
                             const float* bias, float* y, int M, int N, int K,
                             const SplitKWorkspace& ws, hipStream_t stream);

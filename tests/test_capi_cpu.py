@@ -71,7 +71,7 @@ def test_linear_ex_rejects_bad_launch_shape():
     rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 5, 0, 0, 0, 0, None)
     assert rc == 1 and "path" in capi.last_error()
     # MFMA decode: token tile 3 does not exist, 6 waves is not a shape, 65 splits too many
-    for t in [(3, 4, 8, 0), (4, 6, 8, 0), (4, 4, 8, 65), (4, 4, 12, 1)]:
+    for t in [(3, 4, 16, 0), (4, 6, 16, 0), (4, 4, 16, 1), (4, 4, 8, 0), (16, 4, 32, 0)]:
         rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 3, *t, None)
         assert rc == 1 and "MFMA decode shape" in capi.last_error(), t
     rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 2, 1, 0, 0, 0, None)

@@ -230,26 +230,28 @@ def test_linear_gemv_deterministic_and_linear(dev):
 
 # ----------------------------------------------------------------------------- linear MFMA decode
 
-DECODE_SHAPES = [(4, 8), (4, 16), (2, 8), (8, 8)]
+DECODE_SHAPES = [(2, 16), (4, 16), (8, 16), (2, 32), (4, 32), (8, 32)]
 
 
 def test_linear_every_decode_mfma_shape(dev, orc):
-    """All (mt, waves, ks) instantiations of the MFMA decode kernel, each with and
-    without K splits, on a ragged shape (N = 77 rows, K = 1312: 41 blocks, so the
-    last K chunk is partial), M from mt-1 to mt, with bias."""
-    N, K = 77, 1312
-    w = weight(72, N, K)
-    bias = S.activations(73, (N,), tag=S.TAG_BIAS)
-    for mt in (1, 2, 4, 5, 8, 16):
-        for M in sorted({max(1, mt - 1), mt}):
-            x = acts(74 + M, M, K)
-            want = orc.linear(x, w, bias, M, N, K)
-            for waves, ks in DECODE_SHAPES:
-                for splits in (1, 2, 5, 64):
-                    note(f"decode mfma mt={mt} waves={waves} ks={ks} splits={splits} M={M}")
-                    got = run_linear(dev, x, w, bias, M, N, K, path=3, mt=mt, waves=waves,
-                                     ks=ks, splits=splits)
-                    assert rel_l2(got, want) <= GEMV_TOL, (mt, waves, ks, splits, M)
+    """All (mt, waves, kslice) instantiations of the MFMA decode kernel on a ragged
+    shape (N = 77 rows, K = 1312: 41 blocks, so K splits into 3 or 2 slices and the
+    last is partial), M from mt-1 to mt, with bias; then a shape with one slice."""
+    w = weight(72, 77, 1312)
+    bias = S.activations(73, (77,), tag=S.TAG_BIAS)
+    for N, K in ((77, 1312), (77, 160)):
+        wNK = w if K == 1312 else weight(72, N, K)
+        for mt in (1, 2, 4, 5, 8, 16):
+            for M in sorted({max(1, mt - 1), mt}):
+                x = acts(74 + M, M, K)
+                want = orc.linear(x, wNK, bias, M, N, K)
+                for waves, kslice in DECODE_SHAPES:
+                    if mt == 16 and kslice == 32:
+                        continue
+                    note(f"decode mfma mt={mt} waves={waves} kslice={kslice} M={M} K={K}")
+                    got = run_linear(dev, x, wNK, bias, M, N, K, path=3, mt=mt, waves=waves,
+                                     kslice=kslice)
+                    assert rel_l2(got, want) <= GEMV_TOL, (mt, waves, kslice, M, K)
 
 
 @pytest.mark.parametrize("M", [2, 3, 5, 7, 16, 17, 40])
