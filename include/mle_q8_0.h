@@ -9,9 +9,12 @@
  *     the raw GGUF block_q8_0 stream: per 34-byte block a little-endian binary16
  *     scale d followed by 32 int8 quants q; value = d * q.
  *   - Work is enqueued on `stream` (NULL = the default stream) and is
- *     asynchronous; the caller synchronises.  Nothing is allocated and nothing
- *     is freed.  Entry points are re-entrant; calls writing the same output
- *     buffer on different streams race, as with any kernel.
+ *     asynchronous; the caller synchronises.  The Linear entry points keep one
+ *     split-K workspace (partial sums + tile counters) per (device, stream),
+ *     allocated with hipMalloc on first need and grown (after a synchronise of
+ *     that stream) when a larger shape arrives; it lives until process exit.
+ *     Nothing else is allocated.  Entry points are re-entrant; calls writing
+ *     the same output buffer on different streams race, as with any kernel.
  *   - Return value: 0 on success, else a value of the reference's ErrorCode
  *     enum (include/minillm/core/status.h:20-32): 1 InvalidArgument,
  *     2 OutOfRange, 3 ShapeMismatch, 4 Unsupported, 6 RuntimeError.  The
@@ -51,9 +54,12 @@ int mle_q8_0_abi_version(void);
  * minillm::cuda::add_bias(float*, const float*, int, int) (cuda_kernels.h:22),
  * which this entry point fuses when `bias` is non-NULL (NULL = no bias).
  *
- * Paths: M <= 8 runs the FP32 decode GEMV; 8 < M < 64 runs the GEMV in chunks
- * of 8 tokens; M >= 64 runs the bf16-MFMA prefill GEMM (relative L2 error vs
- * FP32 about 2e-3).
+ * Paths: M == 1 runs the FP32 decode GEMV; 2 <= M < 64 runs the MFMA decode
+ * kernel in chunks of up to 16 tokens (FP32 activations split exactly into
+ * three bf16 parts, so it matches FP32 to about 1e-7 relative L2);
+ * M >= 64 runs the bf16-MFMA prefill GEMM (relative L2 error vs FP32 about
+ * 2e-3).  Both MFMA paths may split K over workgroups and reduce the partials
+ * in a fixed order, so results are deterministic run to run.
  * Errors: NULL x/w/y -> InvalidArgument; M, N or K <= 0 -> InvalidArgument;
  * K % 32 != 0 -> Unsupported ("... requires K to be a multiple of 32").
  */
@@ -117,6 +123,7 @@ size_t mle_q8_0_bytes(int64_t numel);
  *   shape t0..t3 (all four 0 = automatic):
  *     path 1: t0 = token tile mt in {1,2,4,8} >= min(M,8), t1 = lanes per row
  *             in {16,32,64}, t2 = rows per lane group in {1,2,4,8}, t3 = 0;
+ *     path 2: t0 = K splits in [1, 64], t1 = t2 = t3 = 0;
  *     path 3: t0 = token tile in {1,2,4,5,8,16} >= min(M,16), t1 = waves per
  *             workgroup in {2,4,8} (16 rows each), t2 = K blocks per
  *             workgroup in {16, 32} (32 only for a token tile <= 8), t3 = 0.

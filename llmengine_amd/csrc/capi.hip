@@ -144,6 +144,7 @@ int pick_path(int M) { return M >= 64 ? 2 : M == 1 ? 1 : 3; }
 struct Tune {
   mle::GemvConfig gemv{0, 0, 0};
   mle::DecodeMfmaConfig dec{0, 0, 0};
+  int gemm_splits = 0;  // 0 = automatic
 };
 
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
@@ -154,9 +155,16 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
                                             M < 16 ? M : 16, N, K))
       path = 1;
   }
-  if (path == 2)
-    return check_launch(mle::launch_gemm_mfma(x, w, bias, y, M, N, K, stream),
+  if (path == 2) {
+    if (!mle::gemm_mfma_fits(M, N, K))
+      return fail(MLE_UNSUPPORTED, "hip sgemm_nt Q8_0: K too large for the MFMA GEMM");
+    const int splits = tune.gemm_splits > 0 ? tune.gemm_splits
+                                            : mle::gemm_mfma_pick_splits(M, N, K);
+    mle::SplitKWorkspace ws;
+    MLE_TRY(get_workspace(mle::gemm_mfma_workspace(M, N, K, splits), stream, &ws));
+    return check_launch(mle::launch_gemm_mfma(x, w, bias, y, M, N, K, splits, ws, stream),
                         "hip sgemm_nt Q8_0 launch failed");
+  }
   if (path == 3) {
     // MFMA decode in chunks of at most 16 tokens.
     for (int m0 = 0; m0 < M; m0 += 16) {
@@ -238,9 +246,15 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
                     "hip sgemm_nt_q8_0_weight: invalid MFMA decode shape (mt " +
                         std::to_string(t0) + ", waves " + std::to_string(t1) + ", kslice " +
                         std::to_string(t2) + ")");
+    } else if (path == 2) {
+      tune.gemm_splits = t0;
+      if (t0 < 1 || t0 > 64 || t1 != 0 || t2 != 0 || t3 != 0)
+        return fail(MLE_INVALID_ARGUMENT,
+                    "hip sgemm_nt_q8_0_weight: invalid MFMA GEMM shape (splits " +
+                        std::to_string(t0) + ")");
     } else {
       return fail(MLE_INVALID_ARGUMENT,
-                  "hip sgemm_nt_q8_0_weight: a launch shape needs path 1 or 3");
+                  "hip sgemm_nt_q8_0_weight: a launch shape needs path 1, 2 or 3");
     }
   }
   return run_linear(x, w_q8_0, bias, y, M, N, K, path, tune, stream);

@@ -51,8 +51,13 @@ hipError_t launch_gemv_mfma(const DecodeMfmaConfig& c, const float* x, const uin
                             const SplitKWorkspace& ws, hipStream_t stream);
 
 // Linear GEMM on bf16 MFMA (prefill): same contract as launch_gemv, any M.
-hipError_t launch_gemm_mfma(const float* x, const uint8_t* w, const float* bias,
-                            float* y, int M, int N, int K, hipStream_t stream);
+// `splits` K splits (1 = none) meet in a split-K workspace.
+int gemm_mfma_pick_splits(int M, int N, int K);
+SplitKNeed gemm_mfma_workspace(int M, int N, int K, int splits);
+bool gemm_mfma_fits(int M, int N, int K);
+hipError_t launch_gemm_mfma(const float* x, const uint8_t* w, const float* bias, float* y,
+                            int M, int N, int K, int splits, const SplitKWorkspace& ws,
+                            hipStream_t stream);
 
 // MatMul C[M,N] = A[M,K] . B[K,N] with B in Q8_0 blocks along N.
 hipError_t launch_matmul(const float* a, const uint8_t* b, float* c, int M,

@@ -363,6 +363,25 @@ def test_linear_mfma_ragged_with_bias(dev, orc, M, N, K):
     assert err <= MFMA_TOL, err
 
 
+def test_linear_mfma_split_k(dev, orc):
+    """The prefill GEMM with its K split 1..5 ways (ragged M, N and K, bias):
+    every split count agrees with the oracle, and repeats are bitwise equal."""
+    import torch
+    M, N, K = 200, 333, 1312
+    w, x = weight(93, N, K), acts(94, M, K)
+    bias = S.activations(95, (N,), tag=S.TAG_BIAS)
+    want = orc.linear(x, w, bias, M, N, K)
+    dx, dw, db = to_dev(x, dev), to_dev(w, dev), to_dev(bias, dev)
+    for splits in (1, 2, 3, 5):
+        note(f"mfma split-K splits={splits}")
+        ya, yb = empty_f32((M, N), dev), empty_f32((M, N), dev)
+        capi.linear_ex(dx, dw, db, ya, M, N, K, path=2, splits=splits)
+        capi.linear_ex(dx, dw, db, yb, M, N, K, path=2, splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb)
+        assert rel_l2(to_host(ya), want) <= MFMA_TOL, splits
+
+
 @pytest.mark.parametrize("N,K", [(11008, 4096), (4096, 11008)])
 def test_linear_c3_prefill_full(dev, orc, N, K):
     """Config 3 at full size (M=512): sampled rows against the oracle, the whole
