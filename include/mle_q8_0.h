@@ -123,7 +123,9 @@ size_t mle_q8_0_bytes(int64_t numel);
  *   shape t0..t3 (all four 0 = automatic):
  *     path 1: t0 = token tile mt in {1,2,4,8} >= min(M,8), t1 = lanes per row
  *             in {16,32,64}, t2 = rows per lane group in {1,2,4,8}, t3 = 0;
- *     path 2: t0 = K splits in [1, 64], t1 = t2 = t3 = 0;
+ *     path 2: t0 = K splits in [1, 64], t1 = tile rows in {128, 256},
+ *             t2 = tile columns in {64, 96, 128} (at most 96 for 256 rows),
+ *             t3 = 0 (a 0 among t0..t2 keeps that field automatic);
  *     path 3: t0 = token tile in {1,2,4,5,8,16} >= min(M,16), t1 = waves per
  *             workgroup in {2,4,8} (16 rows each), t2 = K blocks per
  *             workgroup in {16, 32} (32 only for a token tile <= 8), t3 = 0.

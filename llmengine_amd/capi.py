@@ -110,15 +110,15 @@ def linear(x, w, bias, y, M, N, K, stream=None) -> None:
 
 
 def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice=0,
-              splits=0, stream=None) -> None:
+              splits=0, bm=0, bn=0, stream=None) -> None:
     """Linear with a forced path and launch shape (test / tuning hook).
 
-    path 1 (FP32 GEMV) takes mt, lpr, rw; path 2 (MFMA GEMM) takes splits; path 3
-    (MFMA decode) takes mt, waves, kslice; all zero = automatic."""
+    path 1 (FP32 GEMV) takes mt, lpr, rw; path 2 (MFMA GEMM) takes splits, bm, bn;
+    path 3 (MFMA decode) takes mt, waves, kslice; zero = automatic."""
     if path == 3:
         t = (mt, waves, kslice, 0)
     elif path == 2:
-        t = (splits, 0, 0, 0)
+        t = (splits, bm, bn, 0)
     else:
         t = (mt, lpr, rw, 0)
     rc = load().mle_q8_0_linear_ex(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K,

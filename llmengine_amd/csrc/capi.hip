@@ -88,13 +88,14 @@ int validate_linear(const float* x, const uint8_t* w, const float* bias, float* 
   return MLE_OK;
 }
 
-// Split-K workspace of the MFMA decode path, one per (device, stream): calls on
-// one stream run in order, so its partial sums and tile counters are never used
-// by two launches at once.  Allocated on the first call that needs it (and grown
-// when a larger shape comes), kept until the process ends.
+// Workspace of the MFMA paths, one per (device, stream): split-K partial sums
+// and tile counters, and the prefill GEMM's bf16 copy of X.  Calls on one
+// stream run in order, so the workspace is never used by two launches at once.
+// Allocated on the first call that needs it (and grown when a larger shape
+// comes), kept until the process ends.
 struct StreamWorkspace {
-  float* partials = nullptr;
-  size_t partial_cap = 0;
+  uint8_t* buf = nullptr;  // partial sums, then scratch
+  size_t buf_cap = 0;      // bytes
   uint32_t* counters = nullptr;
   size_t counter_cap = 0;
 };
@@ -103,37 +104,40 @@ std::map<std::pair<int, hipStream_t>, StreamWorkspace> g_ws;
 
 int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWorkspace* out) {
   *out = mle::SplitKWorkspace{};
-  if (need.partial_floats == 0) return MLE_OK;
+  if (need.partial_floats == 0 && need.scratch_bytes == 0) return MLE_OK;
+  const size_t partial_bytes = (need.partial_floats * sizeof(float) + 255) / 256 * 256;
+  const size_t bytes = partial_bytes + need.scratch_bytes;
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 workspace");
   std::lock_guard<std::mutex> lock(g_ws_mu);
   StreamWorkspace& e = g_ws[{dev, stream}];
-  if (e.partial_cap < need.partial_floats || e.counter_cap < need.counters) {
-    if (e.partials != nullptr || e.counters != nullptr) {
+  if (e.buf_cap < bytes || e.counter_cap < need.counters) {
+    if (e.buf != nullptr || e.counters != nullptr) {
       // Earlier launches on this stream may still read the old buffers.
       err = hipStreamSynchronize(stream);
       if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 workspace");
-      (void)hipFree(e.partials);
+      (void)hipFree(e.buf);
       (void)hipFree(e.counters);
       e = StreamWorkspace{};
     }
-    const size_t pc = std::max<size_t>(need.partial_floats, size_t(1) << 20);
+    const size_t bc = std::max<size_t>(bytes, size_t(4) << 20);
     const size_t cc = std::max<size_t>(need.counters, 4096);
-    err = hipMalloc(&e.partials, pc * sizeof(float));
+    err = hipMalloc(&e.buf, bc);
     if (err == hipSuccess) err = hipMalloc(&e.counters, cc * sizeof(uint32_t));
     if (err == hipSuccess) err = hipMemsetAsync(e.counters, 0, cc * sizeof(uint32_t), stream);
     if (err != hipSuccess) {
-      (void)hipFree(e.partials);
+      (void)hipFree(e.buf);
       (void)hipFree(e.counters);
       e = StreamWorkspace{};
       return check_launch(err, "hip sgemm_nt Q8_0 workspace allocation failed");
     }
-    e.partial_cap = pc;
+    e.buf_cap = bc;
     e.counter_cap = cc;
   }
-  out->partials = e.partials;
+  out->partials = reinterpret_cast<float*>(e.buf);
   out->counters = e.counters;
+  out->scratch = need.scratch_bytes ? e.buf + partial_bytes : nullptr;
   return MLE_OK;
 }
 
@@ -144,7 +148,7 @@ int pick_path(int M) { return M >= 64 ? 2 : M == 1 ? 1 : 3; }
 struct Tune {
   mle::GemvConfig gemv{0, 0, 0};
   mle::DecodeMfmaConfig dec{0, 0, 0};
-  int gemm_splits = 0;  // 0 = automatic
+  mle::GemmConfig gemm{0, 0, 0};  // 0 fields = automatic
 };
 
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
@@ -156,13 +160,22 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
       path = 1;
   }
   if (path == 2) {
-    if (!mle::gemm_mfma_fits(M, N, K))
+    mle::GemmConfig c = mle::gemm_mfma_pick(M, N, K);
+    if (tune.gemm.bm) c.bm = tune.gemm.bm;
+    if (tune.gemm.bn) {
+      c.bn = tune.gemm.bn;
+      if (!tune.gemm.bm && !mle::gemm_mfma_config_valid(c)) c.bm = 128;
+    }
+    if (tune.gemm.splits) c.splits = tune.gemm.splits;
+    if (!mle::gemm_mfma_config_valid(c))
+      return fail(MLE_INVALID_ARGUMENT, "hip sgemm_nt_q8_0_weight: invalid MFMA GEMM shape (bm " +
+                                            std::to_string(c.bm) + ", bn " +
+                                            std::to_string(c.bn) + ")");
+    if (!mle::gemm_mfma_fits(c, M, N, K))
       return fail(MLE_UNSUPPORTED, "hip sgemm_nt Q8_0: K too large for the MFMA GEMM");
-    const int splits = tune.gemm_splits > 0 ? tune.gemm_splits
-                                            : mle::gemm_mfma_pick_splits(M, N, K);
     mle::SplitKWorkspace ws;
-    MLE_TRY(get_workspace(mle::gemm_mfma_workspace(M, N, K, splits), stream, &ws));
-    return check_launch(mle::launch_gemm_mfma(x, w, bias, y, M, N, K, splits, ws, stream),
+    MLE_TRY(get_workspace(mle::gemm_mfma_workspace(c, M, N, K), stream, &ws));
+    return check_launch(mle::launch_gemm_mfma(c, x, w, bias, y, M, N, K, ws, stream),
                         "hip sgemm_nt Q8_0 launch failed");
   }
   if (path == 3) {
@@ -247,11 +260,13 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
                         std::to_string(t0) + ", waves " + std::to_string(t1) + ", kslice " +
                         std::to_string(t2) + ")");
     } else if (path == 2) {
-      tune.gemm_splits = t0;
-      if (t0 < 1 || t0 > 64 || t1 != 0 || t2 != 0 || t3 != 0)
+      tune.gemm = mle::GemmConfig{t1, t2, t0};
+      const mle::GemmConfig probe{t1 ? t1 : 128, t2 ? t2 : 64, t0 ? t0 : 1};
+      if (t3 != 0 || !mle::gemm_mfma_config_valid(probe))
         return fail(MLE_INVALID_ARGUMENT,
                     "hip sgemm_nt_q8_0_weight: invalid MFMA GEMM shape (splits " +
-                        std::to_string(t0) + ")");
+                        std::to_string(t0) + ", bm " + std::to_string(t1) + ", bn " +
+                        std::to_string(t2) + ")");
     } else {
       return fail(MLE_INVALID_ARGUMENT,
                   "hip sgemm_nt_q8_0_weight: a launch shape needs path 1, 2 or 3");

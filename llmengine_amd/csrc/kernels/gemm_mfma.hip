@@ -4,44 +4,61 @@
 // Same contract as cpu::sgemm_nt(const float*, const uint8_t*, ...)
 // (src/runtime/kernels/cpu_kernels.cpp:208-218); used for M >= 64.
 //
-// Workgroup tile BM x BN = 128 x 128, K step BK = 64 (two Q8_0 blocks per
-// output row), 256 threads = 4 wavefronts in a 2 x 2 grid, each owning a 64 x 64
-// sub-tile as 2 x 2 v_mfma_f32_32x32x16_bf16 accumulators.
+// Two launches:
+//   1. x_to_frag: X (fp32) -> Xf (bf16, round to nearest even) in a workspace,
+//      stored in MFMA A-fragment order (rows padded to 32, K to 64, with zeros).
+//      X is re-read by every column tile of the GEMM: converting it once halves
+//      those re-reads and takes the conversion off the GEMM's vector ALUs, and
+//      the fragment order turns each A-fragment load into 1 KB of contiguous
+//      memory (loading fragments from a row-major X spreads each load
+//      instruction over 32 rows, which halves the L2->CU throughput).
+//   2. the GEMM.  Workgroup tile BM x BN (BM = 128 MI, BN = 32 NJ), K step 64
+//      (two Q8_0 blocks per W row), 256 threads = 4 wavefronts stacked along M;
+//      wave w owns rows [32 MI w, 32 MI (w+1)) of the tile and all BN columns as
+//      MI x NJ v_mfma_f32_32x32x16_bf16 accumulators.
 //
-// Operands are staged in LDS as bf16 (rows padded by 16 bytes against bank
-// conflicts):
-//   * X tile: fp32 -> bf16 (v_cvt_pk_bf16_f32, round to nearest even);
-//   * W tile: each thread takes one 34-byte block, forms v = d * q in fp32
-//     (exactly the reference's element value) and rounds it once to bf16.
-// The per-block scale is thus folded into the B operand before the MFMA
-// instead of being applied to the accumulator after every 32-wide K block:
-// the latter costs one VALU FMA per output per block, i.e. one VALU op per 64
-// MFMA flops, which on CDNA4 equals the whole non-packed VALU rate and would cap
-// the MFMA pipe at about half its peak.  Error vs the fp32 reference is then
-// the bf16 rounding of both operands (relative L2 ~2e-3), inside the 1e-2 bound
-// stated for this path.
+// Operands:
+//   * A (X): each wave loads its own rows' bf16 fragments straight from the
+//     fragment-ordered copy into registers (no LDS; no row is read by two waves).
+//   * B (W): per K step, thread t < 2 BN takes one 34-byte block (row t/2,
+//     block t%2 of the step), forms v = d * q in fp32 (exactly the reference's
+//     element value), rounds it once to bf16 and writes the 32 values to an LDS
+//     tile that all four waves read.  Each W element is thus dequantised once
+//     per workgroup, and one dequantised element feeds 2 BM flops.
+//   The per-block scale is folded into B rather than applied to the accumulator
+//   after every 32-wide K block: the latter costs one fp32 FMA per output per
+//   block, i.e. one VALU op per 64 MFMA flops, which is the whole non-packed VALU
+//   rate and would cap the MFMA pipe at about half its peak.  Error vs the fp32
+//   reference is the bf16 rounding of both operands (relative L2 ~2e-3), inside
+//   the 1e-2 bound stated for this path.
 //
-// Software pipeline: while the MFMAs consume K step t from one LDS buffer, the
-// global loads of steps t+1 and t+2 (buffer loads, every one unconditional:
-// rows and steps past the end read as zero) are in flight into registers; step
-// t+1 is then converted into the other LDS buffer.  One barrier per K step.
+// K order inside a step: MFMA j (0..3) of a step gives lane half h (lanes 32h..)
+// the eight K values 32 h + 8 j .. +7, i.e. half h walks block h of the step.  A
+// and B use the same order, so the product is unchanged, and each W block is
+// dequantised by a single thread into contiguous LDS.
+//
+// Software pipeline (three register stages, unrolled by three): iteration t
+// issues the global loads of X(t+2) and W(t+3), runs the MFMAs of step t from
+// registers (A) and LDS buffer t%2 (B), dequantises W(t+1) into the other LDS
+// buffer, and ends with one barrier.  Every load is unconditional: rows past M or
+// N and blocks past K read as zero through the buffer range check, and steps
+// past the end re-read the last step.
 //
 // Split K (gridDim.z > 1, for shapes with too few tiles to fill the GPU): each
-// workgroup stores its 128 x 128 fp32 partial tile with device-scope (sc1)
+// workgroup stores its BM x BN fp32 partial tile with device-scope (sc1)
 // stores, waits for their completion and bumps a per-tile counter; the last
-// workgroup of the tile adds the partials in split order (deterministic),
-// adds the bias, writes Y and resets the counter for the next launch.
+// workgroup of the tile adds the partials in split order (deterministic), adds
+// the bias, writes Y and resets the counter for the next launch.
 #include "../launch.hpp"
 #include "../q8_0_device.hpp"
+
+#include <type_traits>
 
 namespace mle {
 namespace {
 
-constexpr int BM = 128;
-constexpr int BN = 128;
 constexpr int BK = 64;
-constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row (144 bytes)
-constexpr int TILE_ELEMS = BM * BN;
+constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row of the W tile (144 bytes)
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -55,23 +72,62 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
                                            0x00020000);
 }
 
-// Global data of one K step held by one thread.
-struct Stage {
-  f32x4 x[8];    // X: 8 float4 of the 128 x 64 tile
-  RawBlock w;    // W: one 34-byte block of the 128 x 2-block tile
+int padded_k(int K) { return (K + BK - 1) / BK * BK; }
+
+// X fp32 [M, K] -> Xf: bf16 (round to nearest even) in MFMA fragment order.
+// Piece p (16 bytes = 8 bf16) is lane p % 64 of fragment f = p / 64, with
+// f = (R * n_steps + s) * 4 + j: rows 32 R + lane % 32, K values
+// 64 s + 32 (lane / 32) + 8 j .. +7.  Rows >= M and K values >= K are zero.  A
+// wave then loads one whole A fragment as 1 KB of contiguous memory.
+__global__ __launch_bounds__(256) void x_to_frag_kernel(const float* __restrict__ x,
+                                                        u32x4* __restrict__ xf, int M, int K,
+                                                        int n_steps, uint32_t pieces) {
+  const uint32_t p = blockIdx.x * 256u + threadIdx.x;
+  if (p >= pieces) return;
+  const uint32_t lane = p & 63u, j = (p >> 6) & 3u, rest = p >> 8;
+  const uint32_t s = rest % (uint32_t)n_steps, R = rest / (uint32_t)n_steps;
+  const int64_t m = (int64_t)R * 32 + (lane & 31u);
+  const int k = (int)(s * 64u + 32u * (lane >> 5) + 8u * j);
+  u32x4 out = {0u, 0u, 0u, 0u};
+  if (m < M && k < K) {  // K % 8 == 0: the 8 values are all inside or all outside
+    const f32x4 a = *reinterpret_cast<const f32x4*>(x + m * K + k);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(x + m * K + k + 4);
+    out = u32x4{cvt_bf16x2(a.x, a.y), cvt_bf16x2(a.z, a.w), cvt_bf16x2(b.x, b.y),
+                cvt_bf16x2(b.z, b.w)};
+  }
+  xf[p] = out;
+}
+
+// X fragments of one K step held by one consumer lane.
+template <int MI>
+struct XStage {
+  u32x4 x[MI][4];
 };
 
-__global__ __launch_bounds__(256, 2) void gemm_q8_0_mfma_kernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ w,
+constexpr int kThreads = 512;  // 4 consumer (MFMA) waves + 4 producer (W) waves
+constexpr int kWRing = 4;      // W raw blocks in flight per producer thread
+
+template <int MI, int NJ>
+__global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
+    const u32x4* __restrict__ xf, uint32_t xf_bytes, const uint8_t* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K,
     int steps_per_split, float* __restrict__ partials, uint32_t* __restrict__ counters) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LDS_STRIDE];
+  constexpr int BM = 128 * MI;
+  constexpr int BN = 32 * NJ;
+  constexpr int NBLK = 2 * BN;  // W blocks per K step (<= 256 producer threads)
+  constexpr int TILE_ELEMS = BM * BN;
+  constexpr int BUF = BN * LDS_STRIDE;
+  // X register stages per consumer lane (32 MI VGPRs each).
+  constexpr int XS = 3;
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2 * BUF];
   __shared__ uint32_t arrived;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const bool consumer = wave < 4;  // wave-uniform role
+  const int cw = wave & 3;         // consumer wave: rows 32 MI cw .. of the tile
+  const int pt = tid & 255;        // producer thread: W block pt of each step
   const int64_t m0 = (int64_t)blockIdx.y * BM;
   const int64_t n0 = (int64_t)blockIdx.x * BN;
   const int KB = K / kBlockElems;
@@ -79,155 +135,90 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_0_mfma_kernel(
   const int n_steps = (K + BK - 1) / BK;
   const int s_begin = blockIdx.z * steps_per_split;
   const int s_end = min(s_begin + steps_per_split, n_steps);
+  const int s_last = s_end - 1;
 
-  // Buffer resources starting at this tile's first row: offsets stay small and
-  // rows past M (X) or N (W) read as zero.
-  const int64_t xrows = min((int64_t)BM, (int64_t)M - m0);
-  const __amdgpu_buffer_rsrc_t xrs = rsrc(x + m0 * K, (uint32_t)(xrows * K * 4));
-  const int64_t wrows = min((int64_t)BN, (int64_t)N - n0);
-  const uint8_t* wtile = w + n0 * row_bytes;
-  const __amdgpu_buffer_rsrc_t wrs = rsrc(wtile, (uint32_t)(wrows * row_bytes));
-
-  // This thread's load slots: X float4 f = tid + 256 i is row f/16, columns
-  // 4 (f%16) .. +3 of the step; W block is row tid/2, block tid%2 of the step.
-  const int wr_row = tid >> 1, wr_hb = tid & 1;
-
-  auto load = [&](int s, Stage& st) {
-    const bool live = s < s_end;
-    const int k0 = s * BK;
+  // Epilogue (consumer waves store; every wave takes part in the barriers).
+  // D[i][jj] of lane l holds rows 4 (l/32) + v%4 + 8 (v/4), column l%32, i.e.
+  // four rows of one column per register quad: storing that directly takes one
+  // 4-byte store per value.  Instead each consumer wave stages 16-row chunks of
+  // its 32 MI x BN tile in its own part of the (now idle) W buffers and writes
+  // them back as 16-byte pieces of contiguous rows (bias added on the way).
+  const int wm = cw * 32 * MI;
+  constexpr int EP_STRIDE = BN + 4;  // floats per staged row: 16-byte rows, banks spread
+  static_assert(4 * 16 * EP_STRIDE * 4 <= 2 * BUF * 2, "epilogue staging exceeds LDS");
+  auto store_tile = [&](auto role, const f32x16 (&v)[MI][NJ]) {
+    constexpr bool kConsumer = decltype(role)::value;
+    float* ep = reinterpret_cast<float*>(Bs) + cw * 16 * EP_STRIDE;
+    const bool vec = (N & 3) == 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = tid + 256 * i;
-      const int r = f >> 4, c4 = (f & 15) * 4;
-      const uint32_t off = live && k0 + c4 < K ? (uint32_t)(r * K + k0 + c4) * 4u : 0x80000000u;
-      st.x[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
-    }
-    const int kb = s * (BK / kBlockElems) + wr_hb;
-    const uint32_t boff = (uint32_t)wr_row * row_bytes + (uint32_t)kb * kBlockBytes;
-    const uint32_t mis = (uint32_t)(((uintptr_t)wtile + boff) & 2u);
-    const bool wlive = live && kb < KB;
-    const uint32_t v8 = wlive ? boff + mis : 0x80000000u;
-    const uint32_t v2 = wlive ? boff + (mis ? 0u : 32u) : 0x80000000u;
-    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, 0, 0);
-    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, 0, 0);
-    st.w.v0 = u32x4_a4{a.x, a.y, a.z, a.w};
-    st.w.v1 = u32x4_a4{b.x, b.y, b.z, b.w};
-    st.w.u = __builtin_amdgcn_raw_buffer_load_b16(wrs, v2, 0, 0);
-    st.w.mis = mis;
-  };
-
-  auto store = [&](const Stage& st, uint16_t* as, uint16_t* bs) {
+    for (int c = 0; c < 2 * MI; ++c) {  // rows 16 c .. 16 c + 15 of this wave's rows
+      const int i = c >> 1, h = c & 1;
+      __syncthreads();  // the previous reads of this staging area are done
+      if constexpr (kConsumer) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = tid + 256 * i;
-      const int r = f >> 4, c4 = (f & 15) * 4;
-      const f32x4 v = st.x[i];
-      *reinterpret_cast<uint2*>(as + r * LDS_STRIDE + c4) =
-          make_uint2(cvt_bf16x2(v.x, v.y), cvt_bf16x2(v.z, v.w));
-    }
-    const Block b = finish_block(st.w);
-    const float d = scale_to_f32_fast(b.scale_bits);
-    u32x4* dst = reinterpret_cast<u32x4*>(bs + wr_row * LDS_STRIDE + wr_hb * kBlockElems);
+        for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t q0 = b.q[2 * i], q1 = b.q[2 * i + 1];
-      dst[i] = u32x4{cvt_bf16x2(d * q_at(q0, 0), d * q_at(q0, 1)),
-                     cvt_bf16x2(d * q_at(q0, 2), d * q_at(q0, 3)),
-                     cvt_bf16x2(d * q_at(q1, 0), d * q_at(q1, 1)),
-                     cvt_bf16x2(d * q_at(q1, 2), d * q_at(q1, 3))};
-    }
-  };
-
-  const int wm = (wave >> 1) * 64;
-  const int wn = (wave & 1) * 64;
-  f32x16 acc[2][2];
+          for (int q = 0; q < 2; ++q)
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+            for (int e = 0; e < 4; ++e)
+              ep[(4 * (lane >> 5) + e + 8 * q) * EP_STRIDE + 32 * jj + (lane & 31)] =
+                  v[i][jj][4 * (2 * h + q) + e];
+      }
+      __syncthreads();
+      if constexpr (!kConsumer) continue;
+      constexpr int PER_ROW = BN / 4;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int u = 0; u < 16 * PER_ROW / 64; ++u) {
+        const int idx = lane + 64 * u;
+        const int rr = idx / PER_ROW, c4 = idx % PER_ROW;
+        f32x4 val = *reinterpret_cast<const f32x4*>(ep + rr * EP_STRIDE + 4 * c4);
+        const int64_t m = m0 + wm + 16 * c + rr;
+        const int64_t n = n0 + 4 * c4;
+        if (m >= M) continue;
+        if (vec) {
+          if (n >= N) continue;
+          if (bias) val += f32x4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
+          *reinterpret_cast<f32x4*>(y + m * N + n) = val;
+        } else {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-  auto mfma_step = [&](const uint16_t* as, const uint16_t* bs) {
-#pragma unroll
-    for (int ks = 0; ks < BK; ks += 16) {
-      const int kk = ks + 8 * (lane >> 5);
-      bf16x8 a[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(as + (wm + 32 * i + (lane & 31)) * LDS_STRIDE + kk);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const bf16x8*>(bs + (wn + 32 * j + (lane & 31)) * LDS_STRIDE + kk);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-  };
-
-  // Two K steps of global data in flight: step s loads step s+2 into the
-  // register stage freed by step s+1's store, so two stages alternate (unroll 2).
-  Stage sa, sb;
-  load(s_begin, sa);
-  load(s_begin + 1, sb);
-  store(sa, As[0], Bs[0]);
-  __syncthreads();
-  auto step = [&](int s, int buf, Stage& next, Stage& far) {
-    load(s + 2, far);  // past s_end: zeros
-    mfma_step(As[buf], Bs[buf]);
-    store(next, As[buf ^ 1], Bs[buf ^ 1]);
-    __syncthreads();
-  };
-  int s = s_begin;
-  for (; s + 2 <= s_end; s += 2) {
-    step(s, 0, sb, sa);
-    step(s + 1, 1, sa, sb);
-  }
-  if (s < s_end) step(s, 0, sb, sa);
-
-  // D[i][j] of lane l is row 4*(l/32) + (v%4) + 8*(v/4), column l%32.
-  if (gridDim.z == 1) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t n = n0 + wn + 32 * j + (lane & 31);
-      if (n >= N) continue;
-      const float bv = bias ? bias[n] : 0.0f;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t m = m0 + wm + 32 * i + 4 * (lane >> 5) + (v & 3) + 8 * (v >> 2);
-          if (m < M) y[m * N + n] = acc[i][j][v] + bv;
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) y[m * N + n + e] = val[e] + (bias ? bias[n + e] : 0.0f);
         }
+      }
     }
+  };
+  auto finish = [&](auto role, f32x16 (&acc)[MI][NJ]) {
+  constexpr bool kConsumer = decltype(role)::value;
+  if (gridDim.z == 1) {
+    store_tile(role, acc);
     return;
   }
 
-  // Split K: partial tile [tile][split][16 KB x 4] by device-scope stores; the
+  // Split K: partial tile [tile][split][TILE_ELEMS] by device-scope stores; the
   // last workgroup of the tile reduces in split order.  Partials are stored
-  // lane-major (slot (i, j, quad) x 256 threads x 16 bytes), so each store
-  // instruction writes 4 KB contiguously and the reader finds its own slots.
+  // lane-major (slot (i, jj, quad) x 256 consumer threads x 16 bytes), so each
+  // store instruction writes 4 KB contiguously and the reader finds its own slots.
   constexpr int SC1 = 16;  // cache-policy bit: device scope
   const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
   const __amdgpu_buffer_rsrc_t prs =
       rsrc(partials + (int64_t)tile * gridDim.z * TILE_ELEMS, gridDim.z * TILE_ELEMS * 4u);
-  auto slot = [&](int i, int j, int q) {  // byte offset of 4 accumulators
-    return (uint32_t)((((i * 2 + j) * 4 + q) * 256 + tid) * 16);
+  auto slot = [&](int i, int jj, int q) {  // byte offset of 4 accumulators
+    return (uint32_t)((((i * NJ + jj) * 4 + q) * 256 + pt) * 16);
   };
+  if constexpr (kConsumer) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 v = f32x4{acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                              acc[i][j][4 * q + 3]};
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
-                                               blockIdx.z * TILE_ELEMS * 4u + slot(i, j, q), 0,
-                                               SC1);
-      }
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = f32x4{acc[i][jj][4 * q + 0], acc[i][jj][4 * q + 1],
+                                acc[i][jj][4 * q + 2], acc[i][jj][4 * q + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
+                                                 blockIdx.z * TILE_ELEMS * 4u + slot(i, jj, q),
+                                                 0, SC1);
+        }
+  }
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);  // every partial has reached the coherence point
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -238,30 +229,165 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_0_mfma_kernel(
   __syncthreads();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   if (arrived != gridDim.z - 1) return;
+  if constexpr (kConsumer) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      f32x4 sum[4];
+      for (int jj = 0; jj < NJ; ++jj) {
+        f32x4 sum[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) sum[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (unsigned sp = 0; sp < gridDim.z; ++sp)
+        for (int q = 0; q < 4; ++q) sum[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (unsigned sp = 0; sp < gridDim.z; ++sp)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          sum[q] += __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         prs, sp * TILE_ELEMS * 4u + slot(i, j, q), 0, SC1));
-      const int64_t n = n0 + wn + 32 * j + (lane & 31);
-      if (n >= N) continue;
-      const float bv = bias ? bias[n] : 0.0f;
+          for (int q = 0; q < 4; ++q)
+            sum[q] += __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           prs, sp * TILE_ELEMS * 4u + slot(i, jj, q), 0, SC1));
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t m = m0 + wm + 32 * i + 4 * (lane >> 5) + (v & 3) + 8 * (v >> 2);
-        if (m < M) y[m * N + n] = sum[v >> 2][v & 3] + bv;
+        for (int v = 0; v < 16; ++v) acc[i][jj][v] = sum[v >> 2][v & 3];
       }
-    }
+  }
   if (tid == 0)
     __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  store_tile(role, acc);
+  };
+
+
+  // Both roles run the same number of iterations, each ending in one barrier:
+  // iteration t publishes the bf16 W tile of step t+1 (producers) and retires
+  // the MFMAs of step t (consumers), which read LDS buffer (t - s_begin) % 2.
+  if (consumer) {
+    f32x16 acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][jj][v] = 0.0f;
+    // A: fragments of 32-row tile R at step s start at byte ((R n_steps + s) 4
+    // + j) KB; tiles past the converted rows read as zero.
+    const __amdgpu_buffer_rsrc_t xrs = rsrc(xf, xf_bytes);
+    uint32_t xoff[MI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+      xoff[i] = (uint32_t)((m0 / 32 + cw * MI + i) * n_steps) * 4096u + lane * 16u;
+    auto load_x = [&](int s, XStage<MI>& st) {
+      const uint32_t sx = (uint32_t)min(s, s_last) * 4096u;
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          st.x[i][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[i] + 1024 * j, sx, 0);
+    };
+    // B fragment of lane (c, h) for MFMA j: row 32 jj + c, K values 32 h + 8 j .. +7.
+    const int boff_lds = (lane & 31) * LDS_STRIDE + 32 * (lane >> 5);
+    auto mfma_step = [&](const uint16_t* bs, const XStage<MI>& st) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bf16x8 bf[NJ];
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj)
+          bf[jj] = *reinterpret_cast<const bf16x8*>(bs + jj * 32 * LDS_STRIDE + boff_lds + 8 * j);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const bf16x8 a = __builtin_bit_cast(bf16x8, st.x[i][j]);
+#pragma unroll
+          for (int jj = 0; jj < NJ; ++jj)
+            acc[i][jj] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bf[jj], acc[i][jj], 0, 0, 0);
+        }
+      }
+    };
+    // Ring of XS register stages: slot (s - s_begin) % XS holds X of step s,
+    // loaded XS - 1 iterations before its MFMAs.
+    XStage<MI> st[XS];
+#pragma unroll
+    for (int u = 0; u < XS - 1; ++u) load_x(s_begin + u, st[u]);
+    __syncthreads();  // W of step s_begin is in buffer 0
+    int p = 0;
+    auto iter = [&](int t, int u) {  // u = (t - s_begin) % XS
+      load_x(t + XS - 1, st[(u + XS - 1) % XS]);
+      mfma_step(Bs + p * BUF, st[u]);
+      __syncthreads();
+      p ^= 1;
+    };
+    int t = s_begin;
+    for (; t + XS <= s_end; t += XS) {
+#pragma unroll
+      for (int u = 0; u < XS; ++u) iter(t + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < XS - 1; ++u)
+      if (t + u < s_end) iter(t + u, u);
+    finish(std::true_type{}, acc);
+  } else {
+    // B: buffer over this tile's rows of W; rows past N read as zero.  Thread pt
+    // loads block (2 s + h) of row n every step s; the block's 2-byte alignment
+    // phase is the same for every step (a step advances 68 bytes).
+    const bool w_thread = NBLK == 256 || pt < NBLK;
+    const int wn_row = pt >> 1, wn_h = pt & 1;
+    const int64_t wrows = min((int64_t)BN, (int64_t)N - n0);
+    const uint8_t* wtile = w + n0 * row_bytes;
+    const __amdgpu_buffer_rsrc_t wrs = rsrc(wtile, (uint32_t)(wrows * row_bytes));
+    const uint32_t boff = (uint32_t)wn_row * row_bytes + (uint32_t)wn_h * kBlockBytes;
+    const uint32_t wmis = (uint32_t)(((uintptr_t)wtile + boff) & 2u);
+    const uint32_t wv8 = boff + wmis;
+    const uint32_t wv2 = boff + (wmis ? 0u : 32u);
+    // Steps s with block 2 s + h < KB (none for threads without a W block,
+    // whose loads are then all masked).
+    const int w_steps = w_thread ? (KB - wn_h + 1) >> 1 : 0;
+    auto load_w = [&](int s, RawBlock& r) {
+      s = min(s, s_last);
+      const bool live = s < w_steps;
+      const uint32_t so = (uint32_t)s * (2 * kBlockBytes);
+      const uint32_t v8 = live ? wv8 : 0x80000000u;
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, so, 0);
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, so, 0);
+      r.v0 = u32x4_a4{a.x, a.y, a.z, a.w};
+      r.v1 = u32x4_a4{b.x, b.y, b.z, b.w};
+      r.u = __builtin_amdgcn_raw_buffer_load_b16(wrs, live ? wv2 : 0x80000000u, so, 0);
+      r.mis = wmis;
+    };
+    auto dequant = [&](const RawBlock& r, uint16_t* bs) {
+      if (!w_thread) return;
+      const Block b = finish_block(r);
+      const float d = scale_to_f32_fast(b.scale_bits);
+      u32x4* dst = reinterpret_cast<u32x4*>(bs + wn_row * LDS_STRIDE + wn_h * kBlockElems);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t q0 = b.q[2 * i], q1 = b.q[2 * i + 1];
+        dst[i] = u32x4{cvt_bf16x2(d * q_at(q0, 0), d * q_at(q0, 1)),
+                       cvt_bf16x2(d * q_at(q0, 2), d * q_at(q0, 3)),
+                       cvt_bf16x2(d * q_at(q1, 0), d * q_at(q1, 1)),
+                       cvt_bf16x2(d * q_at(q1, 2), d * q_at(q1, 3))};
+      }
+    };
+    // Ring of kWRing raw blocks: slot (s - s_begin) % kWRing holds W of step s,
+    // loaded kWRing - 1 iterations before its dequantisation.
+    RawBlock r[kWRing];
+#pragma unroll
+    for (int u = 0; u < kWRing; ++u) load_w(s_begin + u, r[u]);
+    dequant(r[0], Bs);
+    __syncthreads();
+    int p = 0;
+    auto iter = [&](int t, int u) {  // u = (t - s_begin) % kWRing
+      load_w(t + kWRing, r[u]);      // W(t) was dequantised at iteration t-1
+      dequant(r[(u + 1) % kWRing], Bs + (p ^ 1) * BUF);
+      __syncthreads();
+      p ^= 1;
+    };
+    int t = s_begin;
+    for (; t + kWRing <= s_end; t += kWRing) {
+#pragma unroll
+      for (int u = 0; u < kWRing; ++u) iter(t + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < kWRing - 1; ++u)
+      if (t + u < s_end) iter(t + u, u);
+    f32x16 none[MI][NJ];  // never read: producers only join the barriers
+    finish(std::false_type{}, none);
+  }
+
 }
 
 struct GemmGrid {
@@ -269,53 +395,118 @@ struct GemmGrid {
   int steps_per_split;
 };
 
-GemmGrid gemm_grid(int M, int N, int K, int splits) {
+GemmGrid gemm_grid(const GemmConfig& c, int M, int N, int K) {
   GemmGrid g;
-  g.tn = (unsigned)((N + BN - 1) / BN);
-  g.tm = (unsigned)((M + BM - 1) / BM);
-  const int n_steps = (K + BK - 1) / BK;
-  if (splits < 1) splits = 1;
+  g.tn = (unsigned)((N + c.bn - 1) / c.bn);
+  g.tm = (unsigned)((M + c.bm - 1) / c.bm);
+  const int n_steps = padded_k(K) / BK;
+  int splits = c.splits < 1 ? 1 : c.splits;
   if (splits > n_steps) splits = n_steps;
   g.steps_per_split = (n_steps + splits - 1) / splits;
   g.splits = (unsigned)((n_steps + g.steps_per_split - 1) / g.steps_per_split);
   return g;
 }
 
-}  // namespace
-
-int gemm_mfma_pick_splits(int M, int N, int K) {
-  // Split K until the tiles give every CU (256) about one workgroup.
-  const int64_t tiles = (int64_t)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
-  int splits = 1;
-  while (tiles * splits * 2 <= 256 && splits < 8) splits *= 2;
-  return gemm_grid(M, N, K, splits).splits;
+template <int MI, int NJ>
+void launch_tile(const GemmGrid& g, const u32x4* xf, uint32_t xf_bytes, const uint8_t* w,
+                 const float* bias, float* y, int M, int N, int K, const SplitKWorkspace& ws,
+                 hipStream_t stream) {
+  hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ>), dim3(g.tn, g.tm, g.splits), dim3(kThreads), 0,
+                     stream, xf, xf_bytes, w, bias, y, M, N, K, g.steps_per_split,
+                     ws.partials, ws.counters);
 }
 
-SplitKNeed gemm_mfma_workspace(int M, int N, int K, int splits) {
-  const GemmGrid g = gemm_grid(M, N, K, splits);
+// Bytes of the fragment-ordered bf16 copy of X: rows rounded up to 32, K to 64.
+size_t xf_bytes_of(int M, int K) { return (size_t)(M + 31) / 32 * 32 * padded_k(K) * 2; }
+
+constexpr size_t kScratchAlign = 256;
+
+}  // namespace
+
+bool gemm_mfma_config_valid(const GemmConfig& c) {
+  // 256 x 128 tiles would need more than the 256 registers a wave gets.
+  return ((c.bm == 128 && (c.bn == 64 || c.bn == 96 || c.bn == 128)) ||
+          (c.bm == 256 && (c.bn == 64 || c.bn == 96))) &&
+         c.splits >= 1 && c.splits <= 64;
+}
+
+GemmConfig gemm_mfma_pick(int M, int N, int K) {
+  // Estimated time = rounds of workgroups over the 256 CUs x K steps per
+  // workgroup x the measured time of one K step of the tile shape (MI355X,
+  // microseconds), plus the split-K partial traffic (written and read once per
+  // split, at the ~2 TB/s it sustains).  Tile heights of 256 only once M
+  // exceeds 128.
+  struct Shape {
+    int bm, bn;
+    double step_us;
+  };
+  static const Shape shapes[] = {{256, 96, 0.98}, {256, 64, 0.73}, {128, 128, 0.71},
+                                 {128, 96, 0.67}, {128, 64, 0.55}};
+  const int n_steps = padded_k(K) / BK;
+  GemmConfig best{128, 64, 1};
+  double best_us = 1e300;
+  for (const Shape& sh : shapes) {
+    if (sh.bm == 256 && M <= 128) continue;
+    const int64_t tiles = (int64_t)((N + sh.bn - 1) / sh.bn) * ((M + sh.bm - 1) / sh.bm);
+    for (int splits = 1; splits <= 4; splits *= 2) {
+      if (splits > n_steps) break;
+      const int64_t rounds = (tiles * splits + 255) / 256;
+      const int steps = (n_steps + splits - 1) / splits;
+      const double split_us = splits > 1 ? (double)splits * M * N * 8 / 2.1e6 : 0.0;
+      const double us = (double)rounds * steps * sh.step_us + split_us;
+      if (us < best_us) {
+        best_us = us;
+        best = GemmConfig{sh.bm, sh.bn, splits};
+      }
+    }
+  }
+  return best;
+}
+
+SplitKNeed gemm_mfma_workspace(const GemmConfig& c, int M, int N, int K) {
+  const GemmGrid g = gemm_grid(c, M, N, K);
   SplitKNeed need;
   need.splits = (int)g.splits;
   const size_t tiles = (size_t)g.tn * g.tm;
-  need.partial_floats = g.splits > 1 ? tiles * g.splits * TILE_ELEMS : 0;
+  need.partial_floats = g.splits > 1 ? tiles * g.splits * (size_t)c.bm * c.bn : 0;
   need.counters = g.splits > 1 ? tiles : 0;
+  need.scratch_bytes = (xf_bytes_of(M, K) + kScratchAlign - 1) / kScratchAlign * kScratchAlign;
   return need;
 }
 
-bool gemm_mfma_fits(int M, int N, int K) {
-  // 32-bit buffer offsets within one tile's rows of X and of W.
+bool gemm_mfma_fits(const GemmConfig& c, int M, int N, int K) {
+  // 32-bit buffer offsets within the bf16 copy of X (whole) and within one
+  // tile's rows of W.
   const int64_t row_bytes = (int64_t)(K / kBlockElems) * kBlockBytes;
-  (void)M;
   (void)N;
-  return (int64_t)BM * K * 4 < (int64_t(1) << 31) && (int64_t)BN * row_bytes < (int64_t(1) << 31);
+  return (int64_t)(M + c.bm) * padded_k(K) * 2 < (int64_t(1) << 31) &&
+         (int64_t)c.bn * row_bytes < (int64_t(1) << 31);
 }
 
-hipError_t launch_gemm_mfma(const float* x, const uint8_t* w, const float* bias, float* y,
-                            int M, int N, int K, int splits, const SplitKWorkspace& ws,
-                            hipStream_t stream) {
-  if (!gemm_mfma_fits(M, N, K)) return hipErrorInvalidValue;
-  const GemmGrid g = gemm_grid(M, N, K, splits);
-  hipLaunchKernelGGL(gemm_q8_0_mfma_kernel, dim3(g.tn, g.tm, g.splits), dim3(256), 0, stream,
-                     x, w, bias, y, M, N, K, g.steps_per_split, ws.partials, ws.counters);
+hipError_t launch_gemm_mfma(const GemmConfig& c, const float* x, const uint8_t* w,
+                            const float* bias, float* y, int M, int N, int K,
+                            const SplitKWorkspace& ws, hipStream_t stream) {
+  if (!gemm_mfma_config_valid(c) || !gemm_mfma_fits(c, M, N, K) || ws.scratch == nullptr)
+    return hipErrorInvalidValue;
+  const GemmGrid g = gemm_grid(c, M, N, K);
+  if (g.splits > 1 && (ws.partials == nullptr || ws.counters == nullptr))
+    return hipErrorInvalidValue;
+  const size_t xfb = xf_bytes_of(M, K);
+  const uint32_t pieces = (uint32_t)(xfb / 16);
+  u32x4* xf = static_cast<u32x4*>(ws.scratch);
+  hipLaunchKernelGGL(x_to_frag_kernel, dim3((pieces + 255) / 256), dim3(256), 0, stream, x, xf,
+                     M, K, padded_k(K) / BK, pieces);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int mi = c.bm / 128;
+  switch (mi * 1000 + c.bn) {
+    case 1064: launch_tile<1, 2>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
+    case 1096: launch_tile<1, 3>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
+    case 1128: launch_tile<1, 4>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
+    case 2064: launch_tile<2, 2>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
+    case 2096: launch_tile<2, 3>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -31,13 +31,15 @@ struct DecodeMfmaConfig {
   int kslice;  // K blocks per workgroup: 16 or 32 (32 only for mt <= 8)
 };
 struct SplitKNeed {
-  int splits;             // workgroups along K
-  size_t partial_floats;  // workspace floats (0 when splits == 1)
-  size_t counters;        // per-tile arrival counters (0 when splits == 1)
+  int splits = 1;             // workgroups along K
+  size_t partial_floats = 0;  // workspace floats (0 when splits == 1)
+  size_t counters = 0;        // per-tile arrival counters (0 when splits == 1)
+  size_t scratch_bytes = 0;   // other device scratch (256-byte multiple)
 };
 struct SplitKWorkspace {
-  float* partials = nullptr;     // [splits][mt][N]
+  float* partials = nullptr;     // split-K partial sums
   uint32_t* counters = nullptr;  // zero between launches (the kernel resets them)
+  void* scratch = nullptr;       // 256-byte aligned, scratch_bytes long
 };
 int decode_mfma_tile(int M);
 DecodeMfmaConfig decode_mfma_pick(int M, int N, int K);
@@ -51,13 +53,20 @@ hipError_t launch_gemv_mfma(const DecodeMfmaConfig& c, const float* x, const uin
                             const SplitKWorkspace& ws, hipStream_t stream);
 
 // Linear GEMM on bf16 MFMA (prefill): same contract as launch_gemv, any M.
-// `splits` K splits (1 = none) meet in a split-K workspace.
-int gemm_mfma_pick_splits(int M, int N, int K);
-SplitKNeed gemm_mfma_workspace(int M, int N, int K, int splits);
-bool gemm_mfma_fits(int M, int N, int K);
-hipError_t launch_gemm_mfma(const float* x, const uint8_t* w, const float* bias, float* y,
-                            int M, int N, int K, int splits, const SplitKWorkspace& ws,
-                            hipStream_t stream);
+// X is first converted to bf16 into the workspace scratch; `splits` K splits
+// (1 = none) meet in the split-K partials.
+struct GemmConfig {
+  int bm;      // tile rows: 128 or 256
+  int bn;      // tile columns: 64, 96 or 128
+  int splits;  // K splits, 1..64
+};
+GemmConfig gemm_mfma_pick(int M, int N, int K);
+bool gemm_mfma_config_valid(const GemmConfig& c);
+SplitKNeed gemm_mfma_workspace(const GemmConfig& c, int M, int N, int K);
+bool gemm_mfma_fits(const GemmConfig& c, int M, int N, int K);
+hipError_t launch_gemm_mfma(const GemmConfig& c, const float* x, const uint8_t* w,
+                            const float* bias, float* y, int M, int N, int K,
+                            const SplitKWorkspace& ws, hipStream_t stream);
 
 // MatMul C[M,N] = A[M,K] . B[K,N] with B in Q8_0 blocks along N.
 hipError_t launch_matmul(const float* a, const uint8_t* b, float* c, int M,

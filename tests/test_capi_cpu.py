@@ -74,7 +74,10 @@ def test_linear_ex_rejects_bad_launch_shape():
     for t in [(3, 4, 16, 0), (4, 6, 16, 0), (4, 4, 16, 1), (4, 4, 8, 0), (16, 4, 32, 0)]:
         rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 3, *t, None)
         assert rc == 1 and "MFMA decode shape" in capi.last_error(), t
-    for t in [(0, 0, 0, 1), (65, 0, 0, 0), (2, 1, 0, 0)]:
+    # MFMA GEMM: t3 unused, 65 splits too many, 1 / 192 tile rows, 80 tile columns,
+    # 256 x 128 tiles
+    for t in [(0, 0, 0, 1), (65, 0, 0, 0), (2, 1, 0, 0), (0, 192, 0, 0), (1, 128, 80, 0),
+              (1, 256, 128, 0)]:
         rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 2, *t, None)
         assert rc == 1 and "MFMA GEMM shape" in capi.last_error(), t
 
