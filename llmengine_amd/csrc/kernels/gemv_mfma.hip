@@ -228,24 +228,24 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   const uint32_t uoff = lane_off + (mis ? 0u : 32u);
 
   // 1. Every weight load of this wave's 16 rows x KSL blocks, issued up front.
-  //    Load sets past the slice's end read as zeros: their per-lane offset is
-  //    put past the buffer (the range check applies to the per-lane offset).
+  //    Blocks past the slice's end read as zeros: their per-lane offset is put
+  //    past the buffer (the range check applies to the per-lane offset), so no
+  //    lane ever addresses a byte outside its slice of the weight tensor.
   RawBlock wr[NCH][NL];
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
       const int b = KS * c + 4 * u;  // first block of the load set (lane adds g)
-      const bool live = b < nblk;
-      const uint32_t soff = (uint32_t)b * kBlockBytes;
+      const bool live = b + g < nblk;
+      const uint32_t soff = b < nblk ? (uint32_t)b * kBlockBytes : 0u;  // uniform
       const uint32_t v8 = live ? voff : 0x80000000u;
       const uint32_t v2 = live ? uoff : 0x80000000u;
-      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, live ? soff : 0u, 0);
-      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + (live ? 16u : 0u),
-                                                            live ? soff : 0u, 0);
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, soff, 0);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, soff, 0);
       wr[c][u].v0 = u32x4_a4{v0.x, v0.y, v0.z, v0.w};
       wr[c][u].v1 = u32x4_a4{v1.x, v1.y, v1.z, v1.w};
-      wr[c][u].u = __builtin_amdgcn_raw_buffer_load_b16(wrs, v2, live ? soff : 0u, 0);
+      wr[c][u].u = __builtin_amdgcn_raw_buffer_load_b16(wrs, v2, soff, 0);
       wr[c][u].mis = mis;
     }
 
