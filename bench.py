@@ -47,6 +47,15 @@ def gemv_bytes(M, N, K):
     return N * (K // 32) * 34 + 4 * M * K + 4 * M * N
 
 
+def decode_kernel_name(M):
+    """Kernel the C ABI runs for an M-token Linear (mle_q8_0_linear's path choice)."""
+    if M == 1:
+        return "gemv_q8_0_kernel (FP32 GEMV)"
+    if M < 64:
+        return "gemv_q8_0_mfma_kernel (MFMA decode, exact bf16 activation split)"
+    return "gemm_q8_0_mfma_kernel (bf16 MFMA GEMM)"
+
+
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -197,7 +206,8 @@ def main():
     achieved = dom_bytes / dom["us"] / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"gemv_q8_0 M={dom['M']} {dom['op']} [{dom['N']}x{dom['K']}]",
+                "kernel": f"{decode_kernel_name(dom['M'])} M={dom['M']} {dom['op']} "
+                          f"[{dom['N']}x{dom['K']}]",
                 "bytes_per_launch": dom_bytes, "us_per_launch": dom["us"]}
 
     extras = {}
@@ -221,7 +231,8 @@ def main():
             tflops = 2.0 * M * N * K / us / 1e6
             pre.append({"M": M, "N": N, "K": K, "us": round(us, 2),
                         "TFLOPs": round(tflops, 1),
-                        "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)})
+                        "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "note": "per call: X->bf16 fragment pre-pass + GEMM kernel"})
         extras["prefill"] = pre
         # ---- embedding gather, configs[4]
         V, H, T = 151936, 896, 8 * 512
