@@ -42,6 +42,11 @@ LLAMA_SET = [("qkv", 12288, 4096), ("o_proj", 4096, 4096), ("gate", 11008, 4096)
 MS = (1, 4, 8)
 SEED_W = {"qkv": 21, "o_proj": 22, "gate": 23, "up": 24, "down": 25}
 
+# HBM bytes per dispatch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on
+# `bench.py --profile-kernel M,N,K` (FETCH_SIZE scaled by a device copy's read/write
+# ratio), keyed by (M, N, K); see profiles/gemv_q8_0_mfma_m8_4096x11008_traffic.txt.
+MEASURED_TRAFFIC = {(8, 4096, 11008): 57.230e6}
+
 
 def gemv_bytes(M, N, K):
     return N * (K // 32) * 34 + 4 * M * K + 4 * M * N
@@ -204,8 +209,11 @@ def main():
     dom = max(per_launch, key=lambda r: r["us"])
     dom_bytes = gemv_bytes(dom["M"], dom["N"], dom["K"])
     achieved = dom_bytes / dom["us"] / 1e3
+    traffic = MEASURED_TRAFFIC.get((dom["M"], dom["N"], dom["K"]))
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": int(traffic) if traffic else None,
+                "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE)",
                 "kernel": f"{decode_kernel_name(dom['M'])} M={dom['M']} {dom['op']} "
                           f"[{dom['N']}x{dom['K']}]",
                 "bytes_per_launch": dom_bytes, "us_per_launch": dom["us"]}
