@@ -78,24 +78,34 @@ int padded_k(int K) { return (K + BK - 1) / BK * BK; }
 // Piece p (16 bytes = 8 bf16) is lane p % 64 of fragment f = p / 64, with
 // f = (R * n_steps + s) * 4 + j: rows 32 R + lane % 32, K values
 // 64 s + 32 (lane / 32) + 8 j .. +7.  Rows >= M and K values >= K are zero.  A
-// wave then loads one whole A fragment as 1 KB of contiguous memory.
+// GEMM wave then loads one whole A fragment as 1 KB of contiguous memory.
+//
+// One workgroup converts one (32-row tile R, K step s): 256 threads read the
+// 32 x 64 fp32 tile row by row (8 threads per 256-byte row piece: coalesced),
+// round to bf16 into LDS, then each thread writes one 16-byte piece of the four
+// 1 KB fragments (coalesced).
 __global__ __launch_bounds__(256) void x_to_frag_kernel(const float* __restrict__ x,
                                                         u32x4* __restrict__ xf, int M, int K,
-                                                        int n_steps, uint32_t pieces) {
-  const uint32_t p = blockIdx.x * 256u + threadIdx.x;
-  if (p >= pieces) return;
-  const uint32_t lane = p & 63u, j = (p >> 6) & 3u, rest = p >> 8;
-  const uint32_t s = rest % (uint32_t)n_steps, R = rest / (uint32_t)n_steps;
-  const int64_t m = (int64_t)R * 32 + (lane & 31u);
-  const int k = (int)(s * 64u + 32u * (lane >> 5) + 8u * j);
-  u32x4 out = {0u, 0u, 0u, 0u};
-  if (m < M && k < K) {  // K % 8 == 0: the 8 values are all inside or all outside
-    const f32x4 a = *reinterpret_cast<const f32x4*>(x + m * K + k);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(x + m * K + k + 4);
-    out = u32x4{cvt_bf16x2(a.x, a.y), cvt_bf16x2(a.z, a.w), cvt_bf16x2(b.x, b.y),
-                cvt_bf16x2(b.z, b.w)};
+                                                        int n_steps) {
+  __shared__ u32x4 tile[32][9];  // [row][8-value chunk], padded against bank conflicts
+  const int tid = threadIdx.x;
+  const int R = blockIdx.y, s = blockIdx.x;
+  {
+    const int r = tid >> 3, c8 = tid & 7;
+    const int64_t m = (int64_t)R * 32 + r;
+    const int k = s * 64 + 8 * c8;
+    u32x4 out = {0u, 0u, 0u, 0u};
+    if (m < M && k < K) {  // K % 8 == 0: the 8 values are all inside or all outside
+      const f32x4 a = *reinterpret_cast<const f32x4*>(x + m * K + k);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(x + m * K + k + 4);
+      out = u32x4{cvt_bf16x2(a.x, a.y), cvt_bf16x2(a.z, a.w), cvt_bf16x2(b.x, b.y),
+                  cvt_bf16x2(b.z, b.w)};
+    }
+    tile[r][c8] = out;
   }
-  xf[p] = out;
+  __syncthreads();
+  const int j = tid >> 6, lane = tid & 63;
+  xf[((int64_t)((int64_t)R * n_steps + s) * 4 + j) * 64 + lane] = tile[lane & 31][4 * (lane >> 5) + j];
 }
 
 // X fragments of one K step held by one consumer lane.
@@ -476,11 +486,11 @@ SplitKNeed gemm_mfma_workspace(const GemmConfig& c, int M, int N, int K) {
 
 bool gemm_mfma_fits(const GemmConfig& c, int M, int N, int K) {
   // 32-bit buffer offsets within the bf16 copy of X (whole) and within one
-  // tile's rows of W.
+  // tile's rows of W; the X conversion grid has one y index per 32 rows.
   const int64_t row_bytes = (int64_t)(K / kBlockElems) * kBlockBytes;
   (void)N;
   return (int64_t)(M + c.bm) * padded_k(K) * 2 < (int64_t(1) << 31) &&
-         (int64_t)c.bn * row_bytes < (int64_t(1) << 31);
+         (int64_t)c.bn * row_bytes < (int64_t(1) << 31) && (M + 31) / 32 <= 65535;
 }
 
 hipError_t launch_gemm_mfma(const GemmConfig& c, const float* x, const uint8_t* w,
@@ -492,10 +502,10 @@ hipError_t launch_gemm_mfma(const GemmConfig& c, const float* x, const uint8_t* 
   if (g.splits > 1 && (ws.partials == nullptr || ws.counters == nullptr))
     return hipErrorInvalidValue;
   const size_t xfb = xf_bytes_of(M, K);
-  const uint32_t pieces = (uint32_t)(xfb / 16);
   u32x4* xf = static_cast<u32x4*>(ws.scratch);
-  hipLaunchKernelGGL(x_to_frag_kernel, dim3((pieces + 255) / 256), dim3(256), 0, stream, x, xf,
-                     M, K, padded_k(K) / BK, pieces);
+  const int n_steps = padded_k(K) / BK;
+  hipLaunchKernelGGL(x_to_frag_kernel, dim3((unsigned)n_steps, (unsigned)((M + 31) / 32)),
+                     dim3(256), 0, stream, x, xf, M, K, n_steps);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int mi = c.bm / 128;
