@@ -227,6 +227,25 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   const uint32_t voff = lane_off + mis;
   const uint32_t uoff = lane_off + (mis ? 0u : 32u);
 
+  // 0. The slice's activation loads go first: vector-memory loads complete in
+  //    order, so the split below then waits only for these, and it and the
+  //    barrier overlap the weight loads still in flight.  Item = (token m
+  //    fastest, k quarter, block); items past the end (token >= M, block >=
+  //    nblk, or no item) read zeros.
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)((int64_t)M * K * 4));
+  f32x4 xv[XPT][2];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int it = tid + S::NT * i;
+    const int m = it % MT, q = it / MT;
+    const int kb = q >> 2;
+    const uint32_t off = it < S::XITEMS && kb < nblk
+                             ? (uint32_t)((m * K + (kb0 + kb) * kBlockElems + 8 * (q & 3)) * 4)
+                             : 0x80000000u;
+    xv[i][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+    xv[i][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16, 0, 0));
+  }
+
   // 1. Every weight load of this wave's 16 rows x KSL blocks, issued up front.
   //    Blocks past the slice's end read as zeros: their per-lane offset is put
   //    past the buffer (the range check applies to the per-lane offset), so no
@@ -251,23 +270,9 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
 
   // 2. B fragments of the whole K slice (activations split into bf16 parts),
   //    shared by the workgroup's waves.  B fragment (block kb, MFMA p): lane l
-  //    holds virtual column l % 16, k = 8 (l/16) .. +7.  Items past the end
-  //    (token >= M, block >= nblk, or no item) read zeros; every thread runs
-  //    every slot, those past XITEMS writing a dummy LDS slot.
+  //    holds virtual column l % 16, k = 8 (l/16) .. +7.  Every thread runs every
+  //    item slot, those past XITEMS writing a dummy LDS slot.
   {
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)((int64_t)M * K * 4));
-    f32x4 xv[XPT][2];
-#pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-      const int it = tid + S::NT * i;
-      const int m = it % MT, q = it / MT;  // item = (token fastest, k chunk, block)
-      const int kb = q >> 2;
-      const uint32_t off = it < S::XITEMS && kb < nblk
-                               ? (uint32_t)((m * K + (kb0 + kb) * kBlockElems + 8 * (q & 3)) * 4)
-                               : 0x80000000u;
-      xv[i][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
-      xv[i][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16, 0, 0));
-    }
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int it = tid + S::NT * i;
