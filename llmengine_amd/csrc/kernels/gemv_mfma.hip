@@ -142,10 +142,19 @@ __device__ __forceinline__ void transpose_chunks(uint32_t (&q)[8]) {
     }
 }
 
-template <int MT>
+template <int MT, int W = 4>
 struct Cols {
   static constexpr int P = (3 * MT + 15) / 16;  // chained MFMAs per tile
-  static constexpr int PADC = 16 * P - 3 * MT;  // virtual columns that stay zero
+  // Real virtual columns of the last MFMA; when they fit in 8, its B fragment is
+  // stored at half size plus one zero slot that lanes of columns 8..15 read.  The
+  // smaller LDS footprint lets one more 4-wave workgroup share a CU; 8-wave
+  // workgroups are register-bound already and run faster on full fragments
+  // (measured on MI355X).
+  static constexpr int RL = 3 * MT - 16 * (P - 1);
+  static constexpr bool HALF = RL <= 8 && W <= 4;
+  static constexpr int LASTC = HALF ? 8 : 16;            // stored columns, last MFMA
+  static constexpr int PADC = 16 * (P - 1) + LASTC - 3 * MT;  // stored columns kept zero
+  static constexpr int FB = (P - 1) * 1024 + (HALF ? 512 + 16 : 1024);  // bytes per block
 };
 
 template <int MT, int W, int KSL>
@@ -156,27 +165,39 @@ struct Shape {
   static constexpr int KS = 8;                    // blocks per chunk (one load set pair)
   static constexpr int NL = KS / 4;               // blocks per lane per chunk
   static constexpr int NCH = KSL / KS;            // chunks per workgroup
-  static constexpr int BBUF = KSL * P * 1024;     // B fragments of the K slice (bytes)
+  static constexpr int BBUF = KSL * Cols<MT, W>::FB;  // B fragments of the K slice (bytes)
   static constexpr int XITEMS = MT * KSL * 4;     // (token, k chunk, block)
   static constexpr int XPT = (XITEMS + NT - 1) / NT;
   static constexpr int OUTS = 16 * MT;            // outputs per wave
   static constexpr int OPL = (OUTS + 63) / 64;    // outputs per lane
 };
 
-// Byte offset of B-fragment slot (block kb, MFMA p, k chunk c, virtual column n).
-// The 16-byte slot of lane (c, n) sits at position (n + ROT c) % 16 of its
-// 16-slot row: the activation split runs tokens fastest, so 16 consecutive
-// threads write (8 tokens x 2 k chunks) or (4 x 4) distinct slots of a 256-byte
-// bank row, and an MFMA read of a fragment is a permutation within each row.
-// Fragments are 1 KB apart, so a lane's read address is one register plus an
-// immediate per (block, MFMA).
+// Byte offset of B-fragment slot (block kb, MFMA p, k chunk c, virtual column n
+// of the MFMA; n < 8 for a half-size last fragment).  The 16-byte slot of lane
+// (c, n) sits at position (n + ROT c) % 16 of its 16-slot row (% 8 of an 8-slot
+// row in a half fragment): the activation split runs tokens fastest, so 16
+// consecutive threads write (8 tokens x 2 k chunks) or (4 x 4) distinct slots of
+// a 256-byte bank row, and an MFMA read of a fragment is a permutation within
+// each row.  A block's fragments are FB bytes apart, so a lane's read address is
+// one register plus an immediate per (block, MFMA).
 template <int MT>
 struct Slot {
   static constexpr int ROT = MT >= 8 ? 8 : 4;
 };
-template <int MT, int P>
+template <int MT, int W, int P>
 __device__ __forceinline__ int bslot(int kb, int p, int c, int n) {
-  return ((kb * P + p) * 64 + c * 16 + ((n + Slot<MT>::ROT * c) & 15)) * 16;
+  using C = Cols<MT, W>;
+  if (C::HALF && p == P - 1)
+    return kb * C::FB + p * 1024 + (c * 8 + ((n + 4 * c) & 7)) * 16;
+  return kb * C::FB + p * 1024 + (c * 16 + ((n + Slot<MT>::ROT * c) & 15)) * 16;
+}
+// Read slot of lane (c, n): as bslot, except that columns 8..15 of a half-size
+// last fragment read the block's zero slot.
+template <int MT, int W, int P>
+__device__ __forceinline__ int bslot_rd(int kb, int p, int c, int n) {
+  using C = Cols<MT, W>;
+  if (C::HALF && p == P - 1 && n >= 8) return kb * C::FB + p * 1024 + 512;
+  return bslot<MT, W, P>(kb, p, c, n);
 }
 
 // Buffer resource over [base, base + bytes): loads past the end return zero.
@@ -292,18 +313,23 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
 #pragma unroll
       for (int part = 0; part < 3; ++part) {
         const int vc = part * MT + m;
-        uint8_t* dst = real ? bfr + bslot<MT, P>(kb, vc >> 4, c, vc & 15) : xdummy;
+        uint8_t* dst = real ? bfr + bslot<MT, W, P>(kb, vc >> 4, c, vc & 15) : xdummy;
         *reinterpret_cast<u32x4*>(dst) =
             u32x4{parts[part][0], parts[part][1], parts[part][2], parts[part][3]};
       }
     }
     // Virtual columns past 3*MT are never written above: zero them.
-    if constexpr (Cols<MT>::PADC > 0) {
-      constexpr int PADC = Cols<MT>::PADC;
+    if constexpr (Cols<MT, W>::HALF) {
+      for (int kb = tid; kb < KSL; kb += S::NT)
+        *reinterpret_cast<u32x4*>(bfr + kb * Cols<MT, W>::FB + (P - 1) * 1024 + 512) =
+            u32x4{0u, 0u, 0u, 0u};
+    }
+    if constexpr (Cols<MT, W>::PADC > 0) {
+      constexpr int PADC = Cols<MT, W>::PADC;
       for (int it = tid; it < KSL * 4 * PADC; it += S::NT) {
         const int kb = it / (4 * PADC), q = it % (4 * PADC);
         const int c = q / PADC, vc = 3 * MT + q % PADC;
-        *reinterpret_cast<u32x4*>(bfr + bslot<MT, P>(kb, vc >> 4, c, vc & 15)) =
+        *reinterpret_cast<u32x4*>(bfr + bslot<MT, W, P>(kb, vc >> 4, c, vc & 15)) =
             u32x4{0u, 0u, 0u, 0u};
       }
     }
@@ -335,12 +361,12 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
         const int kb = KS * c + kc;      // block within the slice
         const bf16x8_t a = quants_to_bf16(q[2 * j], q[2 * j + 1]);
         f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot<MT, P>(kb, 0, g, r16)),
+            a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, W, P>(kb, 0, g, r16)),
             f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
         for (int p = 1; p < P; ++p)
           d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot<MT, P>(kb, p, g, r16)), d, 0,
+              a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, W, P>(kb, p, g, r16)), d, 0,
               0, 0);
         // D layout: lane l holds rows 4 (l/16) + v (v = 0..3), virtual column l % 16.
         const f32x4 sc = *reinterpret_cast<const f32x4*>(&scl[wave][kc][4 * g]);
