@@ -6,7 +6,10 @@
 //   tests/test_cuda_kernels.cpp:1063-1123 rejects K % 32 != 0 and short storage
 //   tests/test_runtime.cpp:561-626        Linear with bias through the executor
 // plus embedding through the executor (device semantics for bad ids), a
-// caller-owned stream, and a prefill-sized Linear (bf16 MFMA path).
+// caller-owned stream, a prefill-sized Linear (bf16 MFMA path), and a synthetic
+// GGUF model loaded by the weight loader's HIP branch (raw Q8_0 host-to-device
+// copy, reference src/io/gguf_weight_loader.cpp:100-117, 526-541) and run end
+// to end: Embedding -> Linear -> Linear -> tied lm_head Linear.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -17,6 +20,8 @@
 #include <string>
 #include <vector>
 
+#include "gguf_writer.h"
+#include "minillm_hip/io.h"
 #include "minillm_hip/runtime.h"
 
 using namespace minillm;
@@ -438,6 +443,140 @@ static void test_executor_prefill_linear() {
   std::printf("  PASS test_executor_prefill_linear\n");
 }
 
+// Seeded Q8_0 blocks: q uniform in [-127, 127], scale |z| * 0.02 / 127 rounded
+// to binary16 (the BASELINE weight distribution, here from a small LCG).
+static std::vector<uint8_t> synth_q8(size_t rows, size_t cols, uint32_t seed) {
+  std::vector<uint8_t> out(rows * (cols / 32) * 34);
+  uint32_t s = seed;
+  auto next = [&]() { s = s * 1664525u + 1013904223u; return s; };
+  for (size_t b = 0; b < out.size() / 34; ++b) {
+    const float d = float((next() >> 8) % 1000 + 1) * 1e-3f * 0.02f / 127.0f;
+    const _Float16 hd = static_cast<_Float16>(d);  // round to nearest even
+    uint16_t h;
+    std::memcpy(&h, &hd, 2);
+    out[b * 34] = uint8_t(h & 0xff);
+    out[b * 34 + 1] = uint8_t(h >> 8);
+    for (int i = 0; i < 32; ++i) out[b * 34 + 2 + i] = uint8_t(int8_t(int(next() >> 24) % 255 - 127));
+  }
+  return out;
+}
+
+static float host_half(uint16_t h) {
+  const int e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  const float mag = e == 0 ? float(m) * 0x1p-24f : std::ldexp(float(m | 0x400), e - 25);
+  return (h & 0x8000) ? -mag : mag;
+}
+
+// Element (row, col) of a row-major Q8_0 matrix with `cols` columns: d * q.
+static float q8_at(const std::vector<uint8_t>& w, size_t cols, size_t row, size_t col) {
+  const uint8_t* blk = w.data() + (row * (cols / 32) + col / 32) * 34;
+  return float(int8_t(blk[2 + col % 32])) * host_half(uint16_t(blk[0] | (blk[1] << 8)));
+}
+
+// y = x . W^T in double from the same fp32 inputs; relative L2 of `got` against it.
+static double linear_rel_l2(const std::vector<float>& x, const std::vector<uint8_t>& w,
+                            const std::vector<float>& got, int M, int N, int K) {
+  double num = 0, den = 0;
+  for (int m = 0; m < M; ++m)
+    for (int n = 0; n < N; ++n) {
+      double acc = 0;
+      for (int k = 0; k < K; ++k) acc += double(x[size_t(m) * K + k]) * q8_at(w, K, n, k);
+      const double e = double(got[size_t(m) * N + n]) - acc;
+      num += e * e;
+      den += acc * acc;
+    }
+  return std::sqrt(num / den);
+}
+
+static void test_gguf_model_end_to_end() {
+  const int V = 320, H = 128, I = 256;
+  const auto embd = synth_q8(V, H, 11), up = synth_q8(I, H, 12), down = synth_q8(H, I, 13);
+  GgufWriter w;
+  w.kv_str("general.architecture", "llama");
+  w.kv_u32("llama.embedding_length", H);
+  w.tensor("token_embd.weight", {V, H}, 8, embd);
+  w.tensor("blk.0.ffn_up.weight", {I, H}, 8, up);
+  w.tensor("blk.0.ffn_down.weight", {H, I}, 8, down);  // no output.weight: lm_head is tied
+  const std::string path = w.write("mle_e2e");
+
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  for (int T : {5, 70}) {  // MFMA decode path (FP32-exact) and the bf16 MFMA GEMM path
+    Graph g;
+    GraphBuilder gb(g);
+    const Device dev = Device::hip(0);
+    auto ids = gb.input("input_ids", Shape({1, T}), DType::Int32, dev);
+    auto tok = gb.constant("tok_embeddings.weight", Shape({V, H}), DType::Float32, dev);
+    auto wup = gb.constant("layer_0.up_proj.weight", Shape({I, H}), DType::Float32, dev);
+    auto wdn = gb.constant("layer_0.down_proj.weight", Shape({H, I}), DType::Float32, dev);
+    auto lm = gb.constant("lm_head.weight", Shape({V, H}), DType::Float32, dev);
+    CHECK(ids && tok && wup && wdn && lm);
+    auto x = gb.embedding(*ids, *tok, "embed");
+    CHECK(x);
+    auto h = gb.linear(*x, *wup, std::nullopt, "up");
+    CHECK(h);
+    auto o = gb.linear(*h, *wdn, std::nullopt, "down");
+    CHECK(o);
+    auto logits = gb.linear(*o, *lm, std::nullopt, "lm_head");
+    CHECK(logits && gb.output(*logits, "logits"));
+
+    WeightLoader loader(path);
+    auto file = loader.open();
+    CHECK(file);
+    auto store = loader.load_shared_weights(*file, g);
+    CHECK(store);
+    CHECK(store->tensor_count() == 3 && store->alias_count() == 4);
+    // Raw Q8_0 bytes on the device, unchanged; the tied lm_head shares the table.
+    const std::pair<const char*, const std::vector<uint8_t>*> raw[] = {
+        {"tok_embeddings.weight", &embd}, {"layer_0.up_proj.weight", &up},
+        {"layer_0.down_proj.weight", &down}};
+    for (const auto& [name, bytes] : raw) {
+      Tensor* t = store->get(name);
+      CHECK(t && t->device().type == DeviceType::HIP && t->dtype() == DType::Q8_0);
+      CHECK(t->allocated_bytes() == bytes->size());
+      std::vector<uint8_t> back(bytes->size());
+      check_hip(hipMemcpy(back.data(), t->data(), back.size(), hipMemcpyDeviceToHost));
+      CHECK(back == *bytes);
+    }
+    CHECK(store->get("lm_head.weight") == store->get("tok_embeddings.weight"));
+
+    std::vector<int32_t> hid(T);
+    for (int i = 0; i < T; ++i) hid[i] = (i * 37 + 5) % V;
+    Tensor tids("input_ids", Shape({1, T}), DType::Int32, dev);
+    check_status(tids.allocate_hip());
+    upload(tids, hid.data(), hid.size() * 4);
+    RuntimeContext ctx;
+    check_status(ctx.bind(*ids, &tids));
+    check_status(store->bind(g, ctx));
+    check_status(ctx.allocate_intermediates(g));
+    HipExecutor ex(std::make_shared<HipBackend>(), registry);
+    check_status(ex.compile(g));
+    check_status(ex.run(ctx));
+    check_hip(hipDeviceSynchronize());
+
+    // Each stage against a double-precision reference fed with the GPU's own
+    // input to that stage: the embedding bit for bit, the Linears within the
+    // per-path bound (1e-5 FP32-exact decode for M < 64, 1e-2 bf16 GEMM otherwise).
+    const auto ex_ = download(ctx.get(*x), size_t(T) * H);
+    for (int t = 0; t < T; ++t)
+      for (int c = 0; c < H; ++c) {
+        const float want = q8_at(embd, H, hid[t], c);
+        CHECK(std::memcmp(&ex_[size_t(t) * H + c], &want, 4) == 0);
+      }
+    const double tol = T < 64 ? 1e-5 : 1e-2;
+    const auto eh = download(ctx.get(*h), size_t(T) * I);
+    const auto eo = download(ctx.get(*o), size_t(T) * H);
+    const auto el = download(ctx.get(*logits), size_t(T) * V);
+    const double e1 = linear_rel_l2(ex_, up, eh, T, I, H);
+    const double e2 = linear_rel_l2(eh, down, eo, T, H, I);
+    const double e3 = linear_rel_l2(eo, embd, el, T, V, H);
+    std::printf("    T=%d rel L2: up %.2e down %.2e lm_head %.2e (bound %.0e)\n", T, e1, e2, e3, tol);
+    CHECK(e1 <= tol && e2 <= tol && e3 <= tol);
+  }
+  std::remove(path.c_str());
+  std::printf("  PASS test_gguf_model_end_to_end\n");
+}
+
 int main() {
   int count = 0;
   check_hip(hipGetDeviceCount(&count));
@@ -450,6 +589,7 @@ int main() {
   test_executor_embedding_and_stream();
   test_executor_rejects_invalid_inputs();
   test_executor_prefill_linear();
+  test_gguf_model_end_to_end();
   std::printf("test_hip_q8_0: all passed\n");
   return 0;
 }

@@ -5,13 +5,18 @@
 // bound to placeholder device addresses that are never dereferenced: each case
 // here is rejected by validation first).  Mirrors the reference's runtime
 // tests where they apply (tests/test_runtime.cpp:686-756,
-// tests/test_cuda_kernels.cpp:1063-1091).
+// tests/test_cuda_kernels.cpp:1063-1091), and the GGUF reader / weight loader
+// on the host (tests/test_gguf_parser.cpp:334-340, 569-592, 855-899).
+#include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <cstdlib>
 #include <memory>
 #include <stdexcept>
 #include <string>
 
+#include "gguf_writer.h"
+#include "minillm_hip/io.h"
 #include "minillm_hip/runtime.h"
 
 using namespace minillm;
@@ -256,6 +261,169 @@ static void test_matmul_and_embedding_validation() {
   std::printf("  PASS test_matmul_and_embedding_validation\n");
 }
 
+// Q8_0 blocks for `n` elements from a seeded generator: q in [-127, 127],
+// scale bits cycling through normal and subnormal binary16 values.
+static std::vector<uint8_t> q8_blocks(size_t n, uint32_t seed) {
+  const size_t blocks = (n + 31) / 32;
+  std::vector<uint8_t> out(blocks * 34);
+  uint32_t s = seed;
+  const uint16_t scales[4] = {0x3800, 0x1c00, 0x0203, 0x2e66};  // 0.5, 2^-8, subnormal, ~0.1
+  for (size_t b = 0; b < blocks; ++b) {
+    const uint16_t d = scales[b % 4];
+    out[b * 34] = uint8_t(d & 0xff);
+    out[b * 34 + 1] = uint8_t(d >> 8);
+    for (int i = 0; i < 32; ++i) {
+      s = s * 1664525u + 1013904223u;
+      out[b * 34 + 2 + i] = uint8_t(int8_t(int((s >> 24) % 255) - 127));
+    }
+  }
+  return out;
+}
+
+static void test_gguf_parse_and_host_load() {
+  // F16 known answers: 1, -0, 65504, smallest subnormal, largest subnormal, +Inf.
+  const uint16_t f16[6] = {0x3c00, 0x8000, 0x7bff, 0x0001, 0x03ff, 0x7c00};
+  const float f16_want[6] = {1.0f, -0.0f, 65504.0f, 0x1p-24f, 1023.0f * 0x1p-24f, INFINITY};
+  std::vector<uint8_t> f16_bytes(64 * 2, 0);
+  for (int i = 0; i < 64; ++i) {
+    f16_bytes[2 * i] = uint8_t(f16[i % 6] & 0xff);
+    f16_bytes[2 * i + 1] = uint8_t(f16[i % 6] >> 8);
+  }
+  std::vector<uint8_t> f32_bytes(64 * 4);
+  for (int i = 0; i < 64; ++i) {
+    const float v = 0.25f * float(i) - 3.0f;
+    std::memcpy(&f32_bytes[4 * i], &v, 4);
+  }
+  const auto embd = q8_blocks(6 * 64, 7);
+
+  GgufWriter w;
+  w.alignment = 64;
+  w.kv_str("general.architecture", "llama");
+  w.kv_u32("llama.block_count", 1);
+  w.kv_u32("general.alignment", 64);
+  w.kv_f32("llama.attention.layer_norm_rms_epsilon", 1e-5f);
+  w.kv_str_array("tokenizer.ggml.tokens", {"a", "b", "c", "d", "e"});
+  w.tensor("token_embd.weight", {6, 64}, 8, embd);
+  w.tensor("blk.0.ffn_norm.weight", {64}, 1, f16_bytes);
+  w.tensor("output_norm.weight", {64}, 0, f32_bytes);
+  const std::string path = w.write("mle_host_gguf");
+
+  auto file = GGUFParser::parse(path);
+  CHECK(file);
+  CHECK(file->version == 3 && file->tensor_count == 3 && file->metadata_kv_count == 5);
+  CHECK(file->alignment == 64 && file->data_offset % 64 == 0);
+  CHECK(get_metadata_or<std::string>(file->metadata, "general.architecture", "") == "llama");
+  CHECK(get_metadata_or<uint32_t>(file->metadata, "llama.block_count", 0) == 1);
+  CHECK(*get_metadata_array_size(file->metadata, "tokenizer.ggml.tokens") == 5);
+  CHECK(get_metadata_array_size(file->metadata, "llama.block_count").error().code() ==
+        ErrorCode::TypeError);
+  CHECK(get_metadata(file->metadata, "nope").error().code() == ErrorCode::NotFound);
+  const GGUFTensorInfo* te = file->find_tensor("token_embd.weight");
+  CHECK(te && te->dtype == GgmlDataType::Q8_0);
+  CHECK(te->dimensions.size() == 2 && te->dimensions[0] == 6 && te->dimensions[1] == 64);
+  CHECK(*te->num_elements() == 384 && *te->bytes() == 12 * 34);
+  CHECK(ggml_dtype_size(GgmlDataType::Q8_0) == 34 && ggml_blck_size(GgmlDataType::Q8_0) == 32);
+  CHECK(!map_ggml_dtype(GgmlDataType::Q4_0));
+  GGUFTensorInfo q4{"x", GgmlDataType::Q4_0, {32}, 0};
+  CHECK(q4.bytes().error().code() == ErrorCode::Unsupported);
+
+  // Name mapping (the graph's naming contract).
+  CHECK(*WeightLoader::gguf_name_to_value_name("blk.12.ffn_gate.weight") ==
+        "layer_12.gate_proj.weight");
+  CHECK(*WeightLoader::gguf_name_to_value_name("output.weight") == "lm_head.weight");
+  CHECK(WeightLoader::gguf_name_to_value_name("blk.x.ffn_up.weight").error().code() ==
+        ErrorCode::InvalidArgument);
+  CHECK(WeightLoader::gguf_name_to_value_name("rope_freqs").error().code() ==
+        ErrorCode::NotFound);
+
+  // Shared host load: Q8_0 keeps its raw bytes (also for the tied lm_head), F16
+  // and F32 become Float32.
+  Graph g;
+  GraphBuilder gb(g);
+  auto tok = gb.constant("tok_embeddings.weight", Shape({6, 64}), DType::Float32);
+  auto lm = gb.constant("lm_head.weight", Shape({6, 64}), DType::Float32);
+  auto norm = gb.constant("layer_0.ffn_norm.weight", Shape({64}), DType::Float32);
+  auto onorm = gb.constant("output_norm.weight", Shape({64}), DType::Float32);
+  CHECK(tok && lm && norm && onorm);
+  WeightLoader loader(path);
+  auto store = loader.load_shared_weights(*file, g);
+  CHECK(store);
+  CHECK(store->tensor_count() == 3 && store->alias_count() == 4);
+  CHECK(store->total_bytes() == 12 * 34 + 64 * 4 + 64 * 4);
+  Tensor* t = store->get("tok_embeddings.weight");
+  CHECK(t && t == store->get("lm_head.weight") && t->dtype() == DType::Q8_0);
+  CHECK(t->allocated_bytes() == embd.size() &&
+        std::memcmp(t->data(), embd.data(), embd.size()) == 0);
+  const float* nv = static_cast<const float*>(store->get("layer_0.ffn_norm.weight")->data());
+  for (int i = 0; i < 64; ++i) {
+    const float want = f16_want[i % 6];
+    CHECK(std::memcmp(&nv[i], &want, 4) == 0);
+  }
+  const float* ov = static_cast<const float*>(store->get("output_norm.weight")->data());
+  CHECK(std::memcmp(ov, f32_bytes.data(), f32_bytes.size()) == 0);
+  RuntimeContext ctx;
+  CHECK(store->bind(g, ctx).ok() && ctx.get(*tok) == t && ctx.get(*lm) == t);
+
+  // Q8_0 dequantisation: value = (float)q * d.
+  std::vector<float> deq(384);
+  CHECK(WeightLoader::dequantize_to_f32(GgmlDataType::Q8_0, embd.data(), deq.data(), 384).ok());
+  for (int i = 0; i < 384; ++i) {
+    const uint8_t* blk = embd.data() + (i / 32) * 34;
+    const uint16_t bits = uint16_t(blk[0] | (blk[1] << 8));
+    float d;
+    if ((bits & 0x7c00) == 0) d = float(bits & 0x3ff) * 0x1p-24f;
+    else d = std::ldexp(float((bits & 0x3ff) | 0x400), int((bits >> 10) & 0x1f) - 25);
+    CHECK(deq[i] == float(int8_t(blk[2 + i % 32])) * d);
+  }
+
+  // load_weights into tensors bound beforehand; a too-small tensor is rejected.
+  {
+    RuntimeContext c2;
+    Tensor small("tok_embeddings.weight", Shape({6, 64}), DType::Q8_0);
+    CHECK(small.allocate_cpu_bytes(100).ok());
+    CHECK(c2.bind(*tok, &small).ok());
+    const Status st = loader.load_weights(*file, g, c2);
+    CHECK(st.code() == ErrorCode::OutOfRange && contains(st.message(), "too small"));
+  }
+
+  // Error paths.
+  CHECK(GGUFParser::parse(path + ".missing").error().code() == ErrorCode::IOError);
+  {
+    GgufWriter bad = w;
+    bad.magic = "GGUX";
+    auto r = GGUFParser::parse(bad.write("mle_bad_magic"));
+    CHECK(r.error().code() == ErrorCode::InvalidArgument && contains(r.error().message(), "magic"));
+  }
+  {
+    GgufWriter bad = w;
+    bad.version = 2;
+    CHECK(GGUFParser::parse(bad.write("mle_bad_version")).error().code() == ErrorCode::Unsupported);
+  }
+  {
+    GgufWriter bad;
+    bad.tensor("blk.0.ffn_up.weight", {4, 0}, 8, {});
+    CHECK(GGUFParser::parse(bad.write("mle_zero_dim")).error().code() ==
+          ErrorCode::InvalidArgument);
+  }
+  {
+    auto bytes = w.bytes();
+    bytes.resize(40);  // cut inside the metadata
+    const std::string cut = path + ".cut";
+    std::FILE* f = std::fopen(cut.c_str(), "wb");
+    CHECK(f && std::fwrite(bytes.data(), 1, bytes.size(), f) == bytes.size());
+    std::fclose(f);
+    CHECK(GGUFParser::parse(cut).error().code() == ErrorCode::IOError);
+    std::remove(cut.c_str());
+  }
+  {
+    std::vector<uint8_t> buf(16);
+    CHECK(GGUFParser::read_tensor_data(path, file->data_offset, 1u << 20, buf.data(), 16).code() ==
+          ErrorCode::OutOfRange);
+  }
+  std::remove(path.c_str());
+  std::printf("  PASS test_gguf_parse_and_host_load\n");
+}
+
 int main() {
   std::printf("test_host_cpu:\n");
   test_core_types();
@@ -263,6 +431,7 @@ int main() {
   test_registry_and_executor_contract();
   test_linear_validation();
   test_matmul_and_embedding_validation();
+  test_gguf_parse_and_host_load();
   std::printf("test_host_cpu: all passed\n");
   return 0;
 }
