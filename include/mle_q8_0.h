@@ -67,6 +67,39 @@ int mle_q8_0_linear(const float* x, const uint8_t* w_q8_0, const float* bias,
                     float* y, int M, int N, int K, hipStream_t stream);
 
 /*
+ * Fused gate/up Linear + SwiGLU: y[M,N] = silu(x . Wg^T) * (x . Wu^T), with
+ * silu(g) = g / (1 + exp(-g)) evaluated as the reference does
+ * (src/runtime/kernels/cpu_kernels.cpp:848-858).  Wg and Wu are [N,K] Q8_0.
+ *
+ * Replaces the three ops of the reference's FFN front
+ * (src/model/transformer_graph_builder.cpp:261-268): Linear(gate), Linear(up) and
+ * SwiGLU (cuda_kernels.cu:245-248), i.e. two sgemm_nt launches, one swiglu launch
+ * and two [M,N] fp32 intermediates written and read back.  One launch reads
+ * both weights against one copy of the activations.  Paths and precision as for
+ * mle_q8_0_linear (FP32 GEMV for M == 1, FP32-exact MFMA decode for M < 64,
+ * bf16 MFMA GEMM otherwise).  No bias.
+ * Errors: as mle_q8_0_linear; a NULL w_up -> InvalidArgument.
+ */
+int mle_q8_0_linear_swiglu(const float* x, const uint8_t* w_gate, const uint8_t* w_up,
+                           float* y, int M, int N, int K, hipStream_t stream);
+
+/*
+ * Multi-output Q8_0 Linear: y[i][M,N[i]] = x[M,K] . W[i]^T (+ bias[i][N[i]]) for
+ * i < count (1..3), in one launch that reads x once for all weights.
+ *
+ * Replaces the q/k/v projections of one layer, three Linears on the same input
+ * (src/model/transformer_graph_builder.cpp:214-221).  `bias` may be NULL (no
+ * bias anywhere) or hold NULL entries.  For M < 64 each output is bit-identical
+ * to mle_q8_0_linear on the same operands (same kernel arithmetic); M >= 64
+ * takes the bf16 MFMA GEMM with a tile choice of its own.
+ * Errors: count outside 1..3 or NULL w / y / N arrays -> InvalidArgument; each
+ * output is validated as mle_q8_0_linear validates its operands.
+ */
+int mle_q8_0_linear_multi(const float* x, int count, const uint8_t* const* w,
+                          const float* const* bias, float* const* y, const int* N, int M,
+                          int K, hipStream_t stream);
+
+/*
  * Q8_0 MatMul: c[M,N] = a[M,K] . B[K,N], B = [K,N] Q8_0 stored row-major, so
  * element (k,n) is flat index k*N+n and blocks run along N.
  *

@@ -21,8 +21,8 @@ ERROR_NAMES = {0: "Ok", 1: "InvalidArgument", 2: "OutOfRange", 3: "ShapeMismatch
                4: "Unsupported", 5: "NotImplemented", 6: "RuntimeError"}
 
 EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
-            "mle_q8_0_matmul", "mle_q8_0_embedding", "mle_last_error", "mle_q8_0_bytes",
-            "mle_q8_0_f16_decode")
+            "mle_q8_0_linear_swiglu", "mle_q8_0_linear_multi", "mle_q8_0_matmul",
+            "mle_q8_0_embedding", "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode")
 
 
 class Q8_0Error(RuntimeError):
@@ -54,6 +54,10 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_linear_ex.restype = _i
     lib.mle_q8_0_linear_ex.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
                                        _vp]
+    lib.mle_q8_0_linear_swiglu.restype = _i
+    lib.mle_q8_0_linear_swiglu.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_q8_0_linear_multi.restype = _i
+    lib.mle_q8_0_linear_multi.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp]
     lib.mle_q8_0_matmul.restype = _i
     lib.mle_q8_0_matmul.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_q8_0_embedding.restype = _i
@@ -124,6 +128,38 @@ def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice
     rc = load().mle_q8_0_linear_ex(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K,
                                    path, *t, _stream(stream))
     _raise(rc)
+
+
+def linear_swiglu_status(x, w_gate, w_up, y, M, N, K, stream=None):
+    rc = load().mle_q8_0_linear_swiglu(_addr(x), _addr(w_gate), _addr(w_up), _addr(y), M, N,
+                                       K, _stream(stream))
+    return _status(rc)
+
+
+def linear_swiglu(x, w_gate, w_up, y, M, N, K, stream=None) -> None:
+    """y[M,N] = silu(x . Wg^T) * (x . Wu^T); Wg, Wu raw Q8_0 [N,K]."""
+    _raise(linear_swiglu_status(x, w_gate, w_up, y, M, N, K, stream)[0])
+
+
+def linear_multi_status(x, ws, biases, ys, Ns, M, K, stream=None):
+    count = len(ws)
+    vp_arr = _vp * max(count, 1)
+    w_arr = vp_arr(*[_addr(w) for w in ws]) if ws is not None else None
+    y_arr = vp_arr(*[_addr(y) for y in ys]) if ys is not None else None
+    b_arr = vp_arr(*[_addr(b) for b in biases]) if biases is not None else None
+    n_arr = (_i * max(count, 1))(*Ns) if Ns is not None else None
+    rc = load().mle_q8_0_linear_multi(_addr(x), count,
+                                      ctypes.cast(w_arr, _vp) if w_arr else None,
+                                      ctypes.cast(b_arr, _vp) if b_arr else None,
+                                      ctypes.cast(y_arr, _vp) if y_arr else None,
+                                      ctypes.cast(n_arr, _vp) if n_arr else None,
+                                      M, K, _stream(stream))
+    return _status(rc)
+
+
+def linear_multi(x, ws, biases, ys, Ns, M, K, stream=None) -> None:
+    """ys[i][M,Ns[i]] = x . ws[i]^T (+ biases[i]) for up to three weights, one launch."""
+    _raise(linear_multi_status(x, ws, biases, ys, Ns, M, K, stream)[0])
 
 
 def matmul_status(a, b, c, M, N, K, stream=None):

@@ -214,11 +214,53 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
   return ok();
 }
 
+// One launch over 1-3 output segments (multi-output Linear) or a gate/up pair
+// (SwiGLU): the bf16 MFMA GEMM for M >= 64, the FP32 GEMV for M == 1, else the
+// MFMA decode kernel in chunks of up to 16 tokens (FP32-exact activations) --
+// the same path choice as a single Linear.
+int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, int K,
+             hipStream_t stream) {
+  const bool swi = s.mode == mle::Epilogue::kSwiGLU;
+  int total_n = 0;
+  for (int i = 0; i < s.count; ++i) total_n += s.seg[i].N;
+  if (M >= 64) {
+    const mle::GemmConfig c = mle::gemm_mfma_pick_segs(M, s, K);
+    if (!mle::gemm_mfma_fits(c, M, 0, K))
+      return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": K too large for the MFMA GEMM");
+    mle::SplitKWorkspace ws;
+    MLE_TRY(get_workspace(mle::gemm_mfma_workspace_segs(c, M, s, K), stream, &ws));
+    return check_launch(mle::launch_gemm_mfma_segs(c, x, s, M, K, ws, stream),
+                        "hip Q8_0 fused Linear launch failed");
+  }
+  if (M == 1) {
+    const mle::GemvConfig c = mle::gemv_pick_config(1, total_n, K);
+    return check_launch(mle::launch_gemv_segs(c, x, s, 1, K, stream),
+                        "hip Q8_0 fused Linear launch failed");
+  }
+  for (int m0 = 0; m0 < M; m0 += 16) {
+    const int mc = M - m0 < 16 ? M - m0 : 16;
+    const mle::DecodeMfmaConfig c = mle::decode_mfma_pick(mc, total_n, K);
+    if (!mle::decode_mfma_fits(c, mc, 1, K))
+      return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": K too large for the MFMA decode");
+    mle::LinearSegs chunk = s;
+    for (int i = 0; i < s.count; ++i) {
+      if (swi && i == 1) break;  // the up segment has no output of its own
+      chunk.seg[i].y = s.seg[i].y + (int64_t)m0 * s.seg[i].N;
+    }
+    mle::SplitKWorkspace ws;
+    MLE_TRY(get_workspace(mle::decode_mfma_workspace_segs(c, chunk, K), stream, &ws));
+    const hipError_t err =
+        mle::launch_gemv_mfma_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ws, stream);
+    if (err != hipSuccess) return check_launch(err, "hip Q8_0 fused Linear launch failed");
+  }
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
 
-int mle_q8_0_abi_version(void) { return 2; }
+int mle_q8_0_abi_version(void) { return 3; }
 
 const char* mle_last_error(void) { return g_last_error.c_str(); }
 
@@ -273,6 +315,40 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
     }
   }
   return run_linear(x, w_q8_0, bias, y, M, N, K, path, tune, stream);
+}
+
+int mle_q8_0_linear_swiglu(const float* x, const uint8_t* w_gate, const uint8_t* w_up,
+                           float* y, int M, int N, int K, hipStream_t stream) {
+  const char* ctx = "linear_swiglu_q8_0";
+  MLE_TRY(validate_linear(x, w_gate, nullptr, y, M, N, K));
+  if (w_up == nullptr)
+    return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": up pointer must not be null");
+  MLE_TRY(check_align(ctx, w_up, 2, "up"));
+  mle::LinearSegs s;
+  s.mode = mle::Epilogue::kSwiGLU;
+  s.count = 2;
+  s.seg[0] = mle::LinearSeg{w_gate, nullptr, y, N};
+  s.seg[1] = mle::LinearSeg{w_up, nullptr, y, N};
+  return run_segs(ctx, x, s, M, K, stream);
+}
+
+int mle_q8_0_linear_multi(const float* x, int count, const uint8_t* const* w,
+                          const float* const* bias, float* const* y, const int* N, int M, int K,
+                          hipStream_t stream) {
+  const char* ctx = "linear_multi_q8_0";
+  if (count < 1 || count > 3)
+    return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": count must be 1, 2 or 3");
+  if (w == nullptr || y == nullptr || N == nullptr)
+    return fail(MLE_INVALID_ARGUMENT,
+                std::string("hip ") + ctx + ": weight, output and N arrays must not be null");
+  mle::LinearSegs s;
+  s.count = count;
+  for (int i = 0; i < count; ++i) {
+    const float* b = bias ? bias[i] : nullptr;
+    MLE_TRY(validate_linear(x, w[i], b, y[i], M, N[i], K));
+    s.seg[i] = mle::LinearSeg{w[i], b, y[i], N[i]};
+  }
+  return run_segs(ctx, x, s, M, K, stream);
 }
 
 int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M, int N, int K,

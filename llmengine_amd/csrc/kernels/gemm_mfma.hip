@@ -126,13 +126,34 @@ struct XStage {
 
 constexpr int kThreads = 512;  // 4 consumer (MFMA) waves + 4 producer (W) waves
 
-template <int MI, int NJ>
+// Output segments as the kernel sees them: segment i owns the column tiles
+// [tile_end[i-1], tile_end[i]) of the grid.
+struct GemmArgs {
+  LinearSeg seg[3];
+  unsigned tile_end[3];
+  int count;
+};
+
+// silu(g) * u with the reference's operation order (cpu_kernels.cpp:848-858).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return (g / (1.0f + expf(-g))) * u;
+}
+
+// MODE 0: plain / multi-output Linear.  MODE 1 (SwiGLU): tile columns
+// [0, BN/2) are rows of the gate weight and [BN/2, BN) the same rows of the up
+// weight; producer waves 0-1 dequantise the gate rows and 2-3 the up rows, so
+// each wave reads one weight; the epilogue writes silu(gate) * up for BN/2
+// output columns.
+template <int MI, int NJ, int MODE>
 __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
-    const u32x4* __restrict__ xf, uint32_t xf_bytes, const uint8_t* __restrict__ w,
-    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K,
+    const u32x4* __restrict__ xf, uint32_t xf_bytes, const GemmArgs args, int M, int K,
     int steps_per_split, float* __restrict__ partials, uint32_t* __restrict__ counters) {
   constexpr int BM = 128 * MI;
   constexpr int BN = 32 * NJ;
+  constexpr bool kSwi = MODE == 1;
+  constexpr int BNO = kSwi ? BN / 2 : BN;  // output columns per tile
+  // SwiGLU: two producer waves (128 threads) cover each weight's 2 BNO blocks per step.
+  static_assert(!kSwi || (BNO <= 64 && BNO % 4 == 0), "SwiGLU tiles need BN <= 128");
   constexpr int NBLK = 2 * BN;  // W blocks per K step (<= 256 producer threads)
   constexpr int TILE_ELEMS = BM * BN;
   constexpr int BUF = BN * LDS_STRIDE;
@@ -148,7 +169,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
   const int cw = wave & 3;         // consumer wave: rows 32 MI cw .. of the tile
   const int pt = tid & 255;        // producer thread: W block pt of each step
   const int64_t m0 = (int64_t)blockIdx.y * BM;
-  const int64_t n0 = (int64_t)blockIdx.x * BN;
+  // Segment of this column tile (uniform selects: no indexing into the argument).
+  const unsigned tile = blockIdx.x;
+  const int si = (!kSwi && args.count > 1 && tile >= args.tile_end[0])
+                     ? ((args.count > 2 && tile >= args.tile_end[1]) ? 2 : 1)
+                     : 0;
+  const unsigned tile0 = si == 0 ? 0u : si == 1 ? args.tile_end[0] : args.tile_end[1];
+  const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
+  const float* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
+  const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
+  const int64_t n0 = (int64_t)(tile - tile0) * BNO;
   const int KB = K / kBlockElems;
   const uint32_t row_bytes = (uint32_t)KB * kBlockBytes;
   const int n_steps = (K + BK - 1) / BK;
@@ -185,12 +216,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
       }
       __syncthreads();
       if constexpr (!kConsumer) continue;
-      constexpr int PER_ROW = BN / 4;
+      constexpr int PER_ROW = BNO / 4;
 #pragma unroll
-      for (int u = 0; u < 16 * PER_ROW / 64; ++u) {
+      for (int u = 0; u < (16 * PER_ROW + 63) / 64; ++u) {
         const int idx = lane + 64 * u;
+        if (16 * PER_ROW % 64 != 0 && idx >= 16 * PER_ROW) continue;
         const int rr = idx / PER_ROW, c4 = idx % PER_ROW;
         f32x4 val = *reinterpret_cast<const f32x4*>(ep + rr * EP_STRIDE + 4 * c4);
+        if constexpr (kSwi) {
+          const f32x4 up = *reinterpret_cast<const f32x4*>(ep + rr * EP_STRIDE + BNO + 4 * c4);
+          val = f32x4{silu_mul(val.x, up.x), silu_mul(val.y, up.y), silu_mul(val.z, up.z),
+                      silu_mul(val.w, up.w)};
+        }
         const int64_t m = m0 + wm + 16 * c + rr;
         const int64_t n = n0 + 4 * c4;
         if (m >= M) continue;
@@ -351,12 +388,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
     // B: buffer over this tile's rows of W; rows past N read as zero.  Thread pt
     // loads block (2 s + h) of row n every step s; the block's 2-byte alignment
     // phase is the same for every step (a step advances 68 bytes).
-    const bool w_thread = NBLK == 256 || pt < NBLK;
-    const int wn_row = pt >> 1, wn_h = pt & 1;
-    const int64_t wrows = min((int64_t)BN, (int64_t)N - n0);
-    const uint8_t* wtile = w + n0 * row_bytes;
+    // Item (row, block) of this thread within its weight.  Plain: items
+    // pt < 2 BN.  SwiGLU: producer waves 0-1 take the gate items, 2-3 the up
+    // items (tile rows BNO + row), so the weight is uniform per wave.
+    const int pwave = __builtin_amdgcn_readfirstlane(wave) - 4;
+    const bool up_rows = kSwi && pwave >= 2;
+    const int item = kSwi ? (pwave & 1) * 64 + lane : pt;
+    const int prow = item >> 1, wn_h = item & 1;  // row within its weight, block of the step
+    const bool w_thread = kSwi ? prow < BNO : (NBLK == 256 || pt < NBLK);
+    const int wn_row = (up_rows ? BNO : 0) + prow;  // tile row
+    const uint8_t* wsrc = up_rows ? args.seg[1].w : w;
+    const int64_t wrows = min((int64_t)BNO, (int64_t)N - n0);
+    const uint8_t* wtile = wsrc + n0 * row_bytes;
     const __amdgpu_buffer_rsrc_t wrs = rsrc(wtile, (uint32_t)(wrows * row_bytes));
-    const uint32_t boff = (uint32_t)wn_row * row_bytes + (uint32_t)wn_h * kBlockBytes;
+    const uint32_t boff = (uint32_t)prow * row_bytes + (uint32_t)wn_h * kBlockBytes;
     const uint32_t wmis = (uint32_t)(((uintptr_t)wtile + boff) & 2u);
     const uint32_t wv8 = boff + wmis;
     const uint32_t wv2 = boff + (wmis ? 0u : 32u);
@@ -424,11 +469,29 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
 struct GemmGrid {
   unsigned tn, tm, splits;
   int steps_per_split;
+  GemmArgs args;
 };
 
-GemmGrid gemm_grid(const GemmConfig& c, int M, int N, int K) {
-  GemmGrid g;
-  g.tn = (unsigned)((N + c.bn - 1) / c.bn);
+LinearSegs single_seg(const uint8_t* w, const float* bias, float* y, int N) {
+  LinearSegs s;
+  s.seg[0] = LinearSeg{w, bias, y, N};
+  return s;
+}
+
+GemmGrid gemm_grid(const GemmConfig& c, int M, const LinearSegs& s, int K) {
+  GemmGrid g{};
+  const bool swi = s.mode == Epilogue::kSwiGLU;
+  const int cols = swi ? c.bn / 2 : c.bn;
+  const int count = swi ? 1 : s.count;
+  unsigned end = 0;
+  for (int i = 0; i < 3; ++i) {
+    g.args.seg[i] = s.seg[i];
+    if (i < count) end += (unsigned)((s.seg[i].N + cols - 1) / cols);
+    g.args.tile_end[i] = end;
+  }
+  if (swi) g.args.seg[1].N = s.seg[0].N;
+  g.args.count = count;
+  g.tn = end;
   g.tm = (unsigned)((M + c.bm - 1) / c.bm);
   const int n_steps = padded_k(K) / BK;
   int splits = c.splits < 1 ? 1 : c.splits;
@@ -439,12 +502,16 @@ GemmGrid gemm_grid(const GemmConfig& c, int M, int N, int K) {
 }
 
 template <int MI, int NJ>
-void launch_tile(const GemmGrid& g, const u32x4* xf, uint32_t xf_bytes, const uint8_t* w,
-                 const float* bias, float* y, int M, int N, int K, const SplitKWorkspace& ws,
-                 hipStream_t stream) {
-  hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ>), dim3(g.tn, g.tm, g.splits), dim3(kThreads), 0,
-                     stream, xf, xf_bytes, w, bias, y, M, N, K, g.steps_per_split,
-                     ws.partials, ws.counters);
+void launch_tile(const GemmGrid& g, Epilogue mode, const u32x4* xf, uint32_t xf_bytes, int M,
+                 int K, const SplitKWorkspace& ws, hipStream_t stream) {
+  const dim3 grid(g.tn, g.tm, g.splits);
+  if (mode == Epilogue::kSwiGLU) {
+    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 1>), grid, dim3(kThreads), 0, stream, xf,
+                       xf_bytes, g.args, M, K, g.steps_per_split, ws.partials, ws.counters);
+  } else {
+    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 0>), grid, dim3(kThreads), 0, stream, xf,
+                       xf_bytes, g.args, M, K, g.steps_per_split, ws.partials, ws.counters);
+  }
 }
 
 // Bytes of the fragment-ordered bf16 copy of X: rows rounded up to 32, K to 64.
@@ -461,29 +528,38 @@ bool gemm_mfma_config_valid(const GemmConfig& c) {
          c.splits >= 1 && c.splits <= 64;
 }
 
-GemmConfig gemm_mfma_pick(int M, int N, int K) {
+GemmConfig gemm_mfma_pick_segs(int M, const LinearSegs& s, int K) {
   // Estimated time = rounds of workgroups over the 256 CUs x K steps per
   // workgroup x the measured time of one K step of the tile shape (MI355X,
   // microseconds), plus the split-K partial traffic (written and read once per
   // split, at the ~2 TB/s it sustains).  Tile heights of 256 only once M
-  // exceeds 128.
+  // exceeds 128.  A SwiGLU tile holds BN/2 rows of each weight.
   struct Shape {
     int bm, bn;
     double step_us;
   };
   static const Shape shapes[] = {{256, 96, 0.98}, {256, 64, 0.73}, {128, 128, 0.71},
                                  {128, 96, 0.67}, {128, 64, 0.55}};
+  const bool swi = s.mode == Epilogue::kSwiGLU;
+  const int count = swi ? 1 : s.count;
   const int n_steps = padded_k(K) / BK;
   GemmConfig best{128, 64, 1};
   double best_us = 1e300;
   for (const Shape& sh : shapes) {
     if (sh.bm == 256 && M <= 128) continue;
-    const int64_t tiles = (int64_t)((N + sh.bn - 1) / sh.bn) * ((M + sh.bm - 1) / sh.bm);
+    const int cols = swi ? sh.bn / 2 : sh.bn;
+    int64_t col_tiles = 0, out_cols = 0;
+    for (int i = 0; i < count; ++i) {
+      col_tiles += (s.seg[i].N + cols - 1) / cols;
+      out_cols += s.seg[i].N;
+    }
+    const int64_t tiles = col_tiles * ((M + sh.bm - 1) / sh.bm);
     for (int splits = 1; splits <= 4; splits *= 2) {
       if (splits > n_steps) break;
       const int64_t rounds = (tiles * splits + 255) / 256;
       const int steps = (n_steps + splits - 1) / splits;
-      const double split_us = splits > 1 ? (double)splits * M * N * 8 / 2.1e6 : 0.0;
+      const double split_us =
+          splits > 1 ? (double)splits * M * out_cols * (swi ? 2 : 1) * 8 / 2.1e6 : 0.0;
       const double us = (double)rounds * steps * sh.step_us + split_us;
       if (us < best_us) {
         best_us = us;
@@ -494,8 +570,12 @@ GemmConfig gemm_mfma_pick(int M, int N, int K) {
   return best;
 }
 
-SplitKNeed gemm_mfma_workspace(const GemmConfig& c, int M, int N, int K) {
-  const GemmGrid g = gemm_grid(c, M, N, K);
+GemmConfig gemm_mfma_pick(int M, int N, int K) {
+  return gemm_mfma_pick_segs(M, single_seg(nullptr, nullptr, nullptr, N), K);
+}
+
+SplitKNeed gemm_mfma_workspace_segs(const GemmConfig& c, int M, const LinearSegs& s, int K) {
+  const GemmGrid g = gemm_grid(c, M, s, K);
   SplitKNeed need;
   need.splits = (int)g.splits;
   const size_t tiles = (size_t)g.tn * g.tm;
@@ -503,6 +583,10 @@ SplitKNeed gemm_mfma_workspace(const GemmConfig& c, int M, int N, int K) {
   need.counters = g.splits > 1 ? tiles : 0;
   need.scratch_bytes = (xf_bytes_of(M, K) + kScratchAlign - 1) / kScratchAlign * kScratchAlign;
   return need;
+}
+
+SplitKNeed gemm_mfma_workspace(const GemmConfig& c, int M, int N, int K) {
+  return gemm_mfma_workspace_segs(c, M, single_seg(nullptr, nullptr, nullptr, N), K);
 }
 
 bool gemm_mfma_fits(const GemmConfig& c, int M, int N, int K) {
@@ -514,12 +598,16 @@ bool gemm_mfma_fits(const GemmConfig& c, int M, int N, int K) {
          (int64_t)c.bn * row_bytes < (int64_t(1) << 31) && (M + 31) / 32 <= 65535;
 }
 
-hipError_t launch_gemm_mfma(const GemmConfig& c, const float* x, const uint8_t* w,
-                            const float* bias, float* y, int M, int N, int K,
-                            const SplitKWorkspace& ws, hipStream_t stream) {
-  if (!gemm_mfma_config_valid(c) || !gemm_mfma_fits(c, M, N, K) || ws.scratch == nullptr)
+hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const LinearSegs& s,
+                                 int M, int K, const SplitKWorkspace& ws, hipStream_t stream) {
+  const bool swi = s.mode == Epilogue::kSwiGLU;
+  if (!gemm_mfma_config_valid(c) || !gemm_mfma_fits(c, M, 0, K) || ws.scratch == nullptr)
     return hipErrorInvalidValue;
-  const GemmGrid g = gemm_grid(c, M, N, K);
+  if (s.count < 1 || s.count > 3 || (swi && s.count != 2))
+    return hipErrorInvalidValue;
+  for (int i = 0; i < s.count; ++i)
+    if (s.seg[i].N <= 0 || s.seg[i].w == nullptr) return hipErrorInvalidValue;
+  const GemmGrid g = gemm_grid(c, M, s, K);
   if (g.splits > 1 && (ws.partials == nullptr || ws.counters == nullptr))
     return hipErrorInvalidValue;
   const size_t xfb = xf_bytes_of(M, K);
@@ -531,14 +619,20 @@ hipError_t launch_gemm_mfma(const GemmConfig& c, const float* x, const uint8_t* 
   if (err != hipSuccess) return err;
   const int mi = c.bm / 128;
   switch (mi * 1000 + c.bn) {
-    case 1064: launch_tile<1, 2>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
-    case 1096: launch_tile<1, 3>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
-    case 1128: launch_tile<1, 4>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
-    case 2064: launch_tile<2, 2>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
-    case 2096: launch_tile<2, 3>(g, xf, (uint32_t)xfb, w, bias, y, M, N, K, ws, stream); break;
+    case 1064: launch_tile<1, 2>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 1096: launch_tile<1, 3>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 1128: launch_tile<1, 4>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 2064: launch_tile<2, 2>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 2096: launch_tile<2, 3>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_mfma(const GemmConfig& c, const float* x, const uint8_t* w,
+                            const float* bias, float* y, int M, int N, int K,
+                            const SplitKWorkspace& ws, hipStream_t stream) {
+  return launch_gemm_mfma_segs(c, x, single_seg(w, bias, y, N), M, K, ws, stream);
 }
 
 }  // namespace mle

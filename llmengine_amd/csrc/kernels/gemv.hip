@@ -28,10 +28,23 @@ namespace {
 constexpr int kXPad = 36;  // floats per staged 32-activation block (144 B: conflict-free)
 
 template <int RW>
-__device__ __forceinline__ void load_rows(Block (&blk)[RW], const uint8_t* __restrict__ w,
-                                          const int64_t (&row_off)[RW], int b) {
+__device__ __forceinline__ void load_rows(Block (&blk)[RW], const uint8_t* const (&row)[RW],
+                                          int b) {
 #pragma unroll
-  for (int r = 0; r < RW; ++r) blk[r] = load_block(w + row_off[r] + (int64_t)b * kBlockBytes);
+  for (int r = 0; r < RW; ++r) blk[r] = load_block(row[r] + (int64_t)b * kBlockBytes);
+}
+
+// Output segments as the kernel sees them: segment i owns the workgroups
+// [wg_end[i-1], wg_end[i]) of the grid.
+struct GemvArgs {
+  LinearSeg seg[3];
+  unsigned wg_end[3];
+  int count;
+};
+
+// silu(g) * u with the reference's operation order (cpu_kernels.cpp:848-858).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return (g / (1.0f + expf(-g))) * u;
 }
 
 // One lane's contribution of block `blk[r]` (activations from LDS) to acc[m][r].
@@ -87,37 +100,56 @@ __device__ __forceinline__ void consume(float (&acc)[MT][RW], const Block (&blk)
 
 // Activations are staged in LDS one K-chunk of `ckb` blocks at a time, as
 // [token][block][kXPad] floats; rows of weights stream straight from HBM.
-template <int MT, int LPR, int RW>
-__global__ __launch_bounds__(256) void gemv_q8_0_kernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ w,
-    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int ckb) {
+// MODE 0: plain / multi-output Linear (RT = RW rows per lane group).  MODE 1
+// (SwiGLU): a lane group computes RW rows of the gate weight and the same RW
+// rows of the up weight (RT = 2 RW) and writes silu(gate) * up.
+template <int MT, int LPR, int RW, int MODE>
+__global__ __launch_bounds__(256) void gemv_q8_0_kernel(const float* __restrict__ x,
+                                                        const GemvArgs args, int M, int K,
+                                                        int ckb) {
   extern __shared__ __attribute__((aligned(16))) float xs[];
-  constexpr int G = 256 / LPR;  // lane groups per workgroup
+  constexpr bool kSwi = MODE == 1;
+  constexpr int RT = kSwi ? 2 * RW : RW;  // weight rows per lane group
+  constexpr int G = 256 / LPR;            // lane groups per workgroup
   const int li = threadIdx.x % LPR;
   const int grp = threadIdx.x / LPR;
-  const int64_t row0 = ((int64_t)blockIdx.x * G + grp) * RW;
+  // Segment of this workgroup (uniform selects: no indexing into the argument).
+  const unsigned wg = blockIdx.x;
+  const int si = (!kSwi && args.count > 1 && wg >= args.wg_end[0])
+                     ? ((args.count > 2 && wg >= args.wg_end[1]) ? 2 : 1)
+                     : 0;
+  const unsigned wg0 = si == 0 ? 0u : si == 1 ? args.wg_end[0] : args.wg_end[1];
+  const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
+  const float* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
+  const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
+  const int64_t row0 = ((int64_t)(wg - wg0) * G + grp) * RW;
   const int KB = K / kBlockElems;
   const int64_t row_bytes = (int64_t)KB * kBlockBytes;
   const int xm_stride = ckb * kXPad;
 
   // Rows past N are clamped to row N-1 so that every weight load is
   // unconditional (loads issue back to back); their results are dropped.
-  int64_t row_off[RW];
+  const uint8_t* row_ptr[RT];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) row_off[r] = (row0 + r < N ? row0 + r : (int64_t)N - 1) * row_bytes;
+  for (int r = 0; r < RT; ++r) {
+    const int rr = r % RW;
+    const uint8_t* base = (kSwi && r >= RW) ? args.seg[1].w : w;
+    row_ptr[r] = base + (row0 + rr < N ? row0 + rr : (int64_t)N - 1) * row_bytes;
+  }
 
-  float acc[MT][RW];
+  float acc[MT][RT];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int r = 0; r < RW; ++r) acc[m][r] = 0.0f;
+    for (int r = 0; r < RT; ++r) acc[m][r] = 0.0f;
 
   for (int c0 = 0; c0 < KB; c0 += ckb) {
     const int cend = c0 + ckb < KB ? c0 + ckb : KB;
     // Issue this lane's first weight loads before waiting on the barrier.
     int b = c0 + li;
-    Block cur[RW];
-    if (b < cend) load_rows<RW>(cur, w, row_off, b);
+    Block cur[RT];
+    if (b < cend) load_rows<RT>(cur, row_ptr, b);
 
     __syncthreads();  // the previous chunk's readers are done with xs
     {
@@ -134,12 +166,12 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(
     __syncthreads();
 
     for (; b < cend; b += LPR) {
-      Block nxt[RW];
+      Block nxt[RT];
       const int bn = b + LPR;
-      if (bn < cend) load_rows<RW>(nxt, w, row_off, bn);
-      consume<MT, RW>(acc, cur, xs + (b - c0) * kXPad, xm_stride);
+      if (bn < cend) load_rows<RT>(nxt, row_ptr, bn);
+      consume<MT, RT>(acc, cur, xs + (b - c0) * kXPad, xm_stride);
 #pragma unroll
-      for (int r = 0; r < RW; ++r) cur[r] = nxt[r];
+      for (int r = 0; r < RT; ++r) cur[r] = nxt[r];
     }
   }
 
@@ -149,17 +181,22 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int r = 0; r < RW; ++r) acc[m][r] += __shfl_xor(acc[m][r], off, LPR);
+      for (int r = 0; r < RT; ++r) acc[m][r] += __shfl_xor(acc[m][r], off, LPR);
   }
 
   if (li == 0) {
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       if (row0 + r >= N) continue;
-      const float bv = bias ? bias[row0 + r] : 0.0f;
+      const float bv = (!kSwi && bias) ? bias[row0 + r] : 0.0f;
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
-        if (m < M) y[(int64_t)m * N + row0 + r] = acc[m][r] + bv;
+      for (int m = 0; m < MT; ++m) {
+        if (m >= M) continue;
+        if constexpr (kSwi)
+          y[(int64_t)m * N + row0 + r] = silu_mul(acc[m][r], acc[m][RW + r]);
+        else
+          y[(int64_t)m * N + row0 + r] = acc[m][r] + bv;
+      }
     }
   }
 }
@@ -167,10 +204,19 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(
 constexpr int kXLdsBudget = 48 * 1024;  // bytes of staged activations per workgroup
 
 template <int MT, int LPR, int RW>
-hipError_t launch_one(const float* x, const uint8_t* w, const float* bias, float* y,
-                      int M, int N, int K, hipStream_t stream) {
+hipError_t launch_one(const float* x, const LinearSegs& s, int M, int K, hipStream_t stream) {
   constexpr int rows_per_wg = (256 / LPR) * RW;
-  const int64_t grid = ((int64_t)N + rows_per_wg - 1) / rows_per_wg;
+  const bool swi = s.mode == Epilogue::kSwiGLU;
+  GemvArgs args{};
+  int64_t grid = 0;
+  const int count = swi ? 1 : s.count;
+  for (int i = 0; i < 3; ++i) {
+    args.seg[i] = s.seg[i];
+    if (i < count) grid += ((int64_t)s.seg[i].N + rows_per_wg - 1) / rows_per_wg;
+    args.wg_end[i] = (unsigned)grid;
+  }
+  if (swi) args.seg[1].N = s.seg[0].N;
+  args.count = count;
   const int KB = K / kBlockElems;
   // Chunk of blocks staged per pass: whole K if it fits, else a multiple of LPR.
   int ckb = kXLdsBudget / (MT * kXPad * 4);
@@ -181,31 +227,38 @@ hipError_t launch_one(const float* x, const uint8_t* w, const float* bias, float
     if (ckb < LPR) ckb = LPR;
   }
   const size_t lds = (size_t)MT * ckb * kXPad * sizeof(float);
-  hipLaunchKernelGGL((gemv_q8_0_kernel<MT, LPR, RW>), dim3((unsigned)grid), dim3(256),
-                     lds, stream, x, w, bias, y, M, N, K, ckb);
+  if (swi) {
+    if constexpr (MT == 1 && RW <= 4)
+      hipLaunchKernelGGL((gemv_q8_0_kernel<MT, LPR, RW, 1>), dim3((unsigned)grid), dim3(256),
+                         lds, stream, x, args, M, K, ckb);
+    else
+      return hipErrorInvalidValue;
+  } else {
+    hipLaunchKernelGGL((gemv_q8_0_kernel<MT, LPR, RW, 0>), dim3((unsigned)grid), dim3(256), lds,
+                       stream, x, args, M, K, ckb);
+  }
   return hipGetLastError();
 }
 
 template <int MT, int LPR>
-hipError_t dispatch_rw(int rw, const float* x, const uint8_t* w, const float* bias,
-                       float* y, int M, int N, int K, hipStream_t stream) {
+hipError_t dispatch_rw(int rw, const float* x, const LinearSegs& s, int M, int K,
+                       hipStream_t stream) {
   switch (rw) {
-    case 1: return launch_one<MT, LPR, 1>(x, w, bias, y, M, N, K, stream);
-    case 2: return launch_one<MT, LPR, 2>(x, w, bias, y, M, N, K, stream);
-    case 4: return launch_one<MT, LPR, 4>(x, w, bias, y, M, N, K, stream);
-    case 8: return launch_one<MT, LPR, 8>(x, w, bias, y, M, N, K, stream);
+    case 1: return launch_one<MT, LPR, 1>(x, s, M, K, stream);
+    case 2: return launch_one<MT, LPR, 2>(x, s, M, K, stream);
+    case 4: return launch_one<MT, LPR, 4>(x, s, M, K, stream);
+    case 8: return launch_one<MT, LPR, 8>(x, s, M, K, stream);
   }
   return hipErrorInvalidValue;
 }
 
 template <int MT>
-hipError_t dispatch_lpr(int lpr, int rw, const float* x, const uint8_t* w,
-                        const float* bias, float* y, int M, int N, int K,
+hipError_t dispatch_lpr(int lpr, int rw, const float* x, const LinearSegs& s, int M, int K,
                         hipStream_t stream) {
   switch (lpr) {
-    case 16: return dispatch_rw<MT, 16>(rw, x, w, bias, y, M, N, K, stream);
-    case 32: return dispatch_rw<MT, 32>(rw, x, w, bias, y, M, N, K, stream);
-    case 64: return dispatch_rw<MT, 64>(rw, x, w, bias, y, M, N, K, stream);
+    case 16: return dispatch_rw<MT, 16>(rw, x, s, M, K, stream);
+    case 32: return dispatch_rw<MT, 32>(rw, x, s, M, K, stream);
+    case 64: return dispatch_rw<MT, 64>(rw, x, s, M, K, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -232,16 +285,25 @@ GemvConfig gemv_pick_config(int M, int N, int K) {
   return c;
 }
 
+hipError_t launch_gemv_segs(const GemvConfig& cfg, const float* x, const LinearSegs& s, int M,
+                            int K, hipStream_t stream) {
+  if (s.count < 1 || s.count > 3 || (s.mode == Epilogue::kSwiGLU && s.count != 2))
+    return hipErrorInvalidValue;
+  switch (cfg.mt) {
+    case 1: return dispatch_lpr<1>(cfg.lpr, cfg.rw, x, s, M, K, stream);
+    case 2: return dispatch_lpr<2>(cfg.lpr, cfg.rw, x, s, M, K, stream);
+    case 4: return dispatch_lpr<4>(cfg.lpr, cfg.rw, x, s, M, K, stream);
+    case 8: return dispatch_lpr<8>(cfg.lpr, cfg.rw, x, s, M, K, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv(const GemvConfig& cfg, const float* x, const uint8_t* w,
                        const float* bias, float* y, int M, int N, int K,
                        hipStream_t stream) {
-  switch (cfg.mt) {
-    case 1: return dispatch_lpr<1>(cfg.lpr, cfg.rw, x, w, bias, y, M, N, K, stream);
-    case 2: return dispatch_lpr<2>(cfg.lpr, cfg.rw, x, w, bias, y, M, N, K, stream);
-    case 4: return dispatch_lpr<4>(cfg.lpr, cfg.rw, x, w, bias, y, M, N, K, stream);
-    case 8: return dispatch_lpr<8>(cfg.lpr, cfg.rw, x, w, bias, y, M, N, K, stream);
-  }
-  return hipErrorInvalidValue;
+  LinearSegs s;
+  s.seg[0] = LinearSeg{w, bias, y, N};
+  return launch_gemv_segs(cfg, x, s, M, K, stream);
 }
 
 }  // namespace mle

@@ -206,12 +206,31 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            0x00020000);
 }
 
-template <int MT, int W, int KSL>
+// Output segments as the kernel sees them: segment i owns the row tiles
+// [tile_end[i-1], tile_end[i]) of the grid.
+struct DecodeArgs {
+  LinearSeg seg[3];
+  unsigned tile_end[3];
+  int count;
+};
+
+// silu(g) * u with the reference's operation order (cpu_kernels.cpp:848-858).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return (g / (1.0f + expf(-g))) * u;
+}
+
+// MODE 0: plain / multi-output Linear.  MODE 1 (SwiGLU): waves [0, W/2) take
+// rows of the gate weight, waves [W/2, W) the same rows of the up weight, and
+// the epilogue writes silu(gate) * up.
+template <int MT, int W, int KSL, int MODE>
 __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ w,
-    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K,
+    const float* __restrict__ x, const DecodeArgs args, int M, int K,
     float* __restrict__ partials, uint32_t* __restrict__ counters) {
   using S = Shape<MT, W, KSL>;
+  constexpr bool kSwi = MODE == 1;
+  static_assert(!kSwi || W % 2 == 0, "SwiGLU pairs gate and up waves");
+  constexpr int RW = kSwi ? W / 2 : W;  // waves per weight
+  constexpr int ROUT = 16 * RW;         // output rows per workgroup
   constexpr int P = S::P;
   constexpr int KS = S::KS;
   constexpr int NL = S::NL;
@@ -222,6 +241,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   __shared__ __attribute__((aligned(16))) float scl[W][KS][16];
   __shared__ float red[W][16][17];
   __shared__ __attribute__((aligned(16))) uint8_t xdummy[16];
+  __shared__ float gate_out[kSwi ? RW : 1][kSwi ? S::OPL * 64 : 1];
   __shared__ uint32_t arrived;
 
   const int tid = threadIdx.x;
@@ -232,7 +252,20 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   const uint32_t row_bytes = (uint32_t)KB * kBlockBytes;
   const int kb0 = blockIdx.y * KSL;                 // first block of this K slice
   const int nblk = min(KSL, KB - kb0);              // blocks in this slice
-  const int64_t n0 = (int64_t)blockIdx.x * S::R;
+
+  // Segment of this row tile (uniform selects: no indexing into the argument).
+  const unsigned tile = blockIdx.x;
+  const int si = (!kSwi && args.count > 1 && tile >= args.tile_end[0])
+                     ? ((args.count > 2 && tile >= args.tile_end[1]) ? 2 : 1)
+                     : 0;
+  const unsigned tile0 = si == 0 ? 0u : si == 1 ? args.tile_end[0] : args.tile_end[1];
+  const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
+  const float* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
+  const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
+  const int wrow = kSwi ? wave % RW : wave;  // this wave's 16-row group
+  if (kSwi && wave >= RW) w = args.seg[1].w;
+  const int64_t n0 = (int64_t)(tile - tile0) * ROUT;
 
   // Weights: one buffer resource over this workgroup's rows (rows past N read
   // as zero).  Lane (g, r16) of wave w loads row 16w + r16, blocks
@@ -240,9 +273,9 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   // uniform part is a multiple of 4 (34 * 4u, 34 * 8c), so each lane's block
   // alignment (the realignment case of load_block_raw) never changes.
   const uint8_t* wbase = w + n0 * row_bytes;
-  const int64_t rows_here = min((int64_t)S::R, (int64_t)N - n0);
+  const int64_t rows_here = min((int64_t)ROUT, (int64_t)N - n0);
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(wbase, (uint32_t)(rows_here * row_bytes));
-  const uint32_t lane_off = (uint32_t)(wave * 16 + r16) * row_bytes +
+  const uint32_t lane_off = (uint32_t)(wrow * 16 + r16) * row_bytes +
                             (uint32_t)(kb0 + g) * kBlockBytes;
   const uint32_t mis = (uint32_t)(((uintptr_t)wbase + lane_off) & 2u);
   const uint32_t voff = lane_off + mis;
@@ -400,14 +433,32 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
     outv[o] = s;
   }
 
-  if (gridDim.y == 1) {
+  // Final values of this wave's outputs -> y (plain: + bias; SwiGLU: the up
+  // waves combine with the gate waves' values through LDS).
+  auto write_out = [&](const float (&v)[S::OPL]) {
+    if constexpr (kSwi) {
+      if (wave < RW) {
+#pragma unroll
+        for (int o = 0; o < S::OPL; ++o) gate_out[wrow][64 * o + lane] = v[o];
+      }
+      __syncthreads();
+      if (wave < RW) return;
+    }
 #pragma unroll
     for (int o = 0; o < S::OPL; ++o) {
       const int idx = lane + 64 * o;
       const int m = idx >> 4, rr = idx & 15;
-      const int64_t n = n0 + wave * 16 + rr;
-      if (idx < S::OUTS && m < M && n < N) y[(int64_t)m * N + n] = outv[o] + (bias ? bias[n] : 0.0f);
+      const int64_t n = n0 + wrow * 16 + rr;
+      if (idx >= S::OUTS || m >= M || n >= N) continue;
+      if constexpr (kSwi)
+        y[(int64_t)m * N + n] = silu_mul(gate_out[wrow][64 * o + lane], v[o]);
+      else
+        y[(int64_t)m * N + n] = v[o] + (bias ? bias[n] : 0.0f);
     }
+  };
+
+  if (gridDim.y == 1) {
+    write_out(outv);
     return;
   }
 
@@ -438,63 +489,86 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   __syncthreads();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   if (arrived != gridDim.y - 1) return;
+  float total[S::OPL];
 #pragma unroll
   for (int o = 0; o < S::OPL; ++o) {
     const int idx = lane + 64 * o;
-    const int m = idx >> 4, rr = idx & 15;
-    const int64_t n = n0 + wave * 16 + rr;
-    if (idx >= S::OUTS || m >= M || n >= N) continue;
     float s = 0.0f;
+    if (idx < S::OUTS && (idx >> 4) < M) {
 #pragma unroll 8
-    for (unsigned sp = 0; sp < gridDim.y; ++sp)
-      s += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         prs, (uint32_t)((sp * REGION + wave * S::OUTS + idx) * 4),
-                                         0, SC1));
-    y[(int64_t)m * N + n] = s + (bias ? bias[n] : 0.0f);
+      for (unsigned sp = 0; sp < gridDim.y; ++sp)
+        s += __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(
+                       prs, (uint32_t)((sp * REGION + wave * S::OUTS + idx) * 4), 0, SC1));
+    }
+    total[o] = s;
   }
   if (tid == 0)
     __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  write_out(total);
 }
 
 struct Grid {
   unsigned tiles, splits;
+  DecodeArgs args;
 };
 
-Grid grid_of(const DecodeMfmaConfig& c, int N, int K) {
+// Row tiles of each segment (SwiGLU: 8 W output rows per tile, else 16 W).
+Grid grid_of(const DecodeMfmaConfig& c, const LinearSegs& s, int K) {
   const int KB = K / kBlockElems;
-  Grid gr;
-  gr.tiles = (unsigned)((N + 16 * c.waves - 1) / (16 * c.waves));
+  const int rows = s.mode == Epilogue::kSwiGLU ? 8 * c.waves : 16 * c.waves;
+  Grid gr{};
+  unsigned end = 0;
+  const int count = s.mode == Epilogue::kSwiGLU ? 1 : s.count;
+  for (int i = 0; i < 3; ++i) {
+    gr.args.seg[i] = s.seg[i];
+    if (i < count) end += (unsigned)((s.seg[i].N + rows - 1) / rows);
+    gr.args.tile_end[i] = end;
+  }
+  if (s.mode == Epilogue::kSwiGLU) gr.args.seg[1].N = s.seg[0].N;
+  gr.args.count = count;
+  gr.tiles = end;
   gr.splits = (unsigned)((KB + c.kslice - 1) / c.kslice);
   return gr;
 }
 
 template <int MT, int W, int KSL>
-hipError_t launch_t(const Grid& gr, const float* x, const uint8_t* w, const float* bias,
-                    float* y, int M, int N, int K, const SplitKWorkspace& ws,
-                    hipStream_t stream) {
-  hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KSL>), dim3(gr.tiles, gr.splits),
-                     dim3(64 * W), 0, stream, x, w, bias, y, M, N, K, ws.partials,
-                     ws.counters);
+hipError_t launch_t(const Grid& gr, Epilogue mode, const float* x, int M, int K,
+                    const SplitKWorkspace& ws, hipStream_t stream) {
+  if (mode == Epilogue::kSwiGLU) {
+    if constexpr (W % 2 == 0)
+      hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KSL, 1>), dim3(gr.tiles, gr.splits),
+                         dim3(64 * W), 0, stream, x, gr.args, M, K, ws.partials, ws.counters);
+  } else {
+    hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KSL, 0>), dim3(gr.tiles, gr.splits),
+                       dim3(64 * W), 0, stream, x, gr.args, M, K, ws.partials, ws.counters);
+  }
   return hipGetLastError();
 }
 
 template <int MT>
-hipError_t dispatch_shape(const DecodeMfmaConfig& c, const Grid& gr, const float* x,
-                          const uint8_t* w, const float* bias, float* y, int M, int N, int K,
-                          const SplitKWorkspace& ws, hipStream_t stream) {
+hipError_t dispatch_shape(const DecodeMfmaConfig& c, const Grid& gr, Epilogue mode,
+                          const float* x, int M, int K, const SplitKWorkspace& ws,
+                          hipStream_t stream) {
   if (c.kslice == 16) {
-    if (c.waves == 2) return launch_t<MT, 2, 16>(gr, x, w, bias, y, M, N, K, ws, stream);
-    if (c.waves == 4) return launch_t<MT, 4, 16>(gr, x, w, bias, y, M, N, K, ws, stream);
-    if (c.waves == 8) return launch_t<MT, 8, 16>(gr, x, w, bias, y, M, N, K, ws, stream);
+    if (c.waves == 2) return launch_t<MT, 2, 16>(gr, mode, x, M, K, ws, stream);
+    if (c.waves == 4) return launch_t<MT, 4, 16>(gr, mode, x, M, K, ws, stream);
+    if (c.waves == 8) return launch_t<MT, 8, 16>(gr, mode, x, M, K, ws, stream);
   }
   if constexpr (Cols<MT>::P <= 2) {
     if (c.kslice == 32) {
-      if (c.waves == 2) return launch_t<MT, 2, 32>(gr, x, w, bias, y, M, N, K, ws, stream);
-      if (c.waves == 4) return launch_t<MT, 4, 32>(gr, x, w, bias, y, M, N, K, ws, stream);
-      if (c.waves == 8) return launch_t<MT, 8, 32>(gr, x, w, bias, y, M, N, K, ws, stream);
+      if (c.waves == 2) return launch_t<MT, 2, 32>(gr, mode, x, M, K, ws, stream);
+      if (c.waves == 4) return launch_t<MT, 4, 32>(gr, mode, x, M, K, ws, stream);
+      if (c.waves == 8) return launch_t<MT, 8, 32>(gr, mode, x, M, K, ws, stream);
     }
   }
   return hipErrorInvalidValue;
+}
+
+LinearSegs single(const uint8_t* w, const float* bias, float* y, int N) {
+  LinearSegs s;
+  s.seg[0] = LinearSeg{w, bias, y, N};
+  return s;
 }
 
 }  // namespace
@@ -525,7 +599,11 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K) {
 }
 
 SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K) {
-  const Grid gr = grid_of(c, N, K);
+  return decode_mfma_workspace_segs(c, single(nullptr, nullptr, nullptr, N), K);
+}
+
+SplitKNeed decode_mfma_workspace_segs(const DecodeMfmaConfig& c, const LinearSegs& s, int K) {
+  const Grid gr = grid_of(c, s, K);
   SplitKNeed need;
   need.splits = (int)gr.splits;
   const size_t region = (size_t)16 * c.waves * c.mt;
@@ -546,15 +624,25 @@ bool decode_mfma_fits(const DecodeMfmaConfig& c, int M, int N, int K) {
 hipError_t launch_gemv_mfma(const DecodeMfmaConfig& c, const float* x, const uint8_t* w,
                             const float* bias, float* y, int M, int N, int K,
                             const SplitKWorkspace& ws, hipStream_t stream) {
-  if (!decode_mfma_fits(c, M, N, K)) return hipErrorInvalidValue;
-  const Grid gr = grid_of(c, N, K);
+  return launch_gemv_mfma_segs(c, x, single(w, bias, y, N), M, K, ws, stream);
+}
+
+hipError_t launch_gemv_mfma_segs(const DecodeMfmaConfig& c, const float* x,
+                                 const LinearSegs& s, int M, int K, const SplitKWorkspace& ws,
+                                 hipStream_t stream) {
+  const bool swi = s.mode == Epilogue::kSwiGLU;
+  if (s.count < 1 || s.count > 3 || (swi && (s.count != 2 || c.waves % 2 != 0)))
+    return hipErrorInvalidValue;
+  for (int i = 0; i < s.count; ++i)
+    if (!decode_mfma_fits(c, M, s.seg[i].N, K) || s.seg[i].N <= 0) return hipErrorInvalidValue;
+  const Grid gr = grid_of(c, s, K);
   switch (c.mt) {
-    case 1: return dispatch_shape<1>(c, gr, x, w, bias, y, M, N, K, ws, stream);
-    case 2: return dispatch_shape<2>(c, gr, x, w, bias, y, M, N, K, ws, stream);
-    case 4: return dispatch_shape<4>(c, gr, x, w, bias, y, M, N, K, ws, stream);
-    case 5: return dispatch_shape<5>(c, gr, x, w, bias, y, M, N, K, ws, stream);
-    case 8: return dispatch_shape<8>(c, gr, x, w, bias, y, M, N, K, ws, stream);
-    case 16: return dispatch_shape<16>(c, gr, x, w, bias, y, M, N, K, ws, stream);
+    case 1: return dispatch_shape<1>(c, gr, s.mode, x, M, K, ws, stream);
+    case 2: return dispatch_shape<2>(c, gr, s.mode, x, M, K, ws, stream);
+    case 4: return dispatch_shape<4>(c, gr, s.mode, x, M, K, ws, stream);
+    case 5: return dispatch_shape<5>(c, gr, s.mode, x, M, K, ws, stream);
+    case 8: return dispatch_shape<8>(c, gr, s.mode, x, M, K, ws, stream);
+    case 16: return dispatch_shape<16>(c, gr, s.mode, x, M, K, ws, stream);
   }
   return hipErrorInvalidValue;
 }

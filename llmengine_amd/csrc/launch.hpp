@@ -42,6 +42,26 @@ struct SplitKWorkspace {
   void* scratch = nullptr;       // 256-byte aligned, scratch_bytes long
 };
 int decode_mfma_tile(int M);
+// Output segments of one Linear launch: 1 to 3 weights read against the same
+// activations (a multi-output Linear: q/k/v), or, in kSwiGLU mode, exactly two
+// (gate, up) combined into y = silu(x.Wg^T) * (x.Wu^T) in seg[0].y.
+struct LinearSeg {
+  const uint8_t* w = nullptr;
+  const float* bias = nullptr;  // optional; not used in kSwiGLU mode
+  float* y = nullptr;
+  int N = 0;
+};
+enum class Epilogue { kPlain = 0, kSwiGLU = 1 };
+struct LinearSegs {
+  LinearSeg seg[3];
+  int count = 1;
+  Epilogue mode = Epilogue::kPlain;
+};
+
+// FP32 GEMV over segments (kSwiGLU only with a token tile of 1 and rw <= 4).
+hipError_t launch_gemv_segs(const GemvConfig& cfg, const float* x, const LinearSegs& s, int M,
+                            int K, hipStream_t stream);
+
 DecodeMfmaConfig decode_mfma_pick(int M, int N, int K);
 bool decode_mfma_config_valid(const DecodeMfmaConfig& c);
 SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K);
@@ -51,6 +71,12 @@ bool decode_mfma_fits(const DecodeMfmaConfig& c, int M, int N, int K);
 hipError_t launch_gemv_mfma(const DecodeMfmaConfig& c, const float* x, const uint8_t* w,
                             const float* bias, float* y, int M, int N, int K,
                             const SplitKWorkspace& ws, hipStream_t stream);
+// Segmented / fused form: `N` of the workspace and fits checks is the largest
+// segment N; kSwiGLU needs an even wave count.
+SplitKNeed decode_mfma_workspace_segs(const DecodeMfmaConfig& c, const LinearSegs& s, int K);
+hipError_t launch_gemv_mfma_segs(const DecodeMfmaConfig& c, const float* x,
+                                 const LinearSegs& s, int M, int K, const SplitKWorkspace& ws,
+                                 hipStream_t stream);
 
 // Linear GEMM on bf16 MFMA (prefill): same contract as launch_gemv, any M.
 // X is first converted to bf16 into the workspace scratch; `splits` K splits
@@ -67,6 +93,11 @@ bool gemm_mfma_fits(const GemmConfig& c, int M, int N, int K);
 hipError_t launch_gemm_mfma(const GemmConfig& c, const float* x, const uint8_t* w,
                             const float* bias, float* y, int M, int N, int K,
                             const SplitKWorkspace& ws, hipStream_t stream);
+// Segmented / fused form (kSwiGLU: BN/2 rows of each weight per tile).
+GemmConfig gemm_mfma_pick_segs(int M, const LinearSegs& s, int K);
+SplitKNeed gemm_mfma_workspace_segs(const GemmConfig& c, int M, const LinearSegs& s, int K);
+hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const LinearSegs& s,
+                                 int M, int K, const SplitKWorkspace& ws, hipStream_t stream);
 
 // MatMul C[M,N] = A[M,K] . B[K,N] with B in Q8_0 blocks along N.
 hipError_t launch_matmul(const float* a, const uint8_t* b, float* c, int M,

@@ -25,7 +25,7 @@ def declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     lib = capi.load()
-    assert lib.mle_q8_0_abi_version() == 2
+    assert lib.mle_q8_0_abi_version() == 3
     out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH],
                          stdout=subprocess.PIPE, text=True, check=True).stdout
     exported = set(re.findall(r" T (mle_\w+)", out))
@@ -62,6 +62,30 @@ def test_linear_validation_errors():
     assert code == 1 and "16-byte aligned" in msg
     code, msg = st(FAKE, FAKE + 1, None, FAKE, 1, 2, 32, stream=0)
     assert code == 1 and "aligned" in msg
+
+
+def test_fused_linear_validation_errors():
+    st = capi.linear_swiglu_status
+    code, msg = st(FAKE, FAKE, None, FAKE, 1, 64, 64, stream=0)
+    assert code == 1 and "up pointer must not be null" in msg
+    code, msg = st(FAKE, None, FAKE, FAKE, 1, 64, 64, stream=0)
+    assert code == 1 and "B pointer" in msg
+    code, msg = st(FAKE, FAKE, FAKE, FAKE, 1, 64, 48, stream=0)
+    assert code == 4 and "multiple of 32" in msg
+    code, msg = st(FAKE, FAKE, FAKE + 1, FAKE, 1, 64, 64, stream=0)
+    assert code == 1 and "up must be 2-byte aligned" in msg
+    mt = capi.linear_multi_status
+    for count in (0, 4):
+        code, msg = mt(FAKE, [FAKE] * count, None, [FAKE] * count, [64] * count, 1, 64, stream=0)
+        assert code == 1 and "count must be 1, 2 or 3" in msg
+    code, msg = mt(FAKE, [FAKE, FAKE], None, [FAKE, FAKE], [64, 0], 1, 64, stream=0)
+    assert code == 1 and "N must be positive" in msg
+    code, msg = mt(FAKE, [FAKE, None], None, [FAKE, FAKE], [64, 64], 1, 64, stream=0)
+    assert code == 1 and "B pointer" in msg
+    code, msg = mt(FAKE, [FAKE], [FAKE + 2], [FAKE], [64], 1, 64, stream=0)
+    assert code == 1 and "bias must be 4-byte aligned" in msg
+    rc = capi.load().mle_q8_0_linear_multi(FAKE, 2, None, None, None, None, 1, 64, None)
+    assert rc == 1 and "arrays must not be null" in capi.last_error()
 
 
 def test_linear_ex_rejects_bad_launch_shape():

@@ -1,0 +1,124 @@
+"""GPU parity of the fused Linear entry points against the CPU oracle.
+
+* ``mle_q8_0_linear_swiglu``: y = silu(x . Wg^T) * (x . Wu^T), silu(g) = g / (1 + e^-g)
+  (reference cpu_kernels.cpp:848-858 applied to two Linears, cpu_kernels.cpp:208-218).
+  The oracle side is the oracle's own two Linears followed by silu * up in float64.
+* ``mle_q8_0_linear_multi``: up to three Linears on one input in one launch; each output
+  against the oracle Linear (+ bias), and bit for bit against the single Linear entry
+  point for M < 64 (same kernels, same arithmetic).
+
+Bars: relative L2 <= 1e-5 for M < 64 (FP32-exact MFMA decode) and <= 1e-2 for M >= 64
+(bf16 MFMA GEMM), as for the plain Linear.
+"""
+import functools
+
+import numpy as np
+import pytest
+
+from helpers import empty_f32, note, rel_l2, to_dev, to_host
+from llmengine_amd import capi
+from llmengine_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+
+def tol(M):
+    return 1e-5 if M < 64 else 1e-2
+
+
+@functools.lru_cache(maxsize=None)
+def weight(seed, rows, cols):
+    return S.q8_0_weight(seed, rows, cols)[0]
+
+
+def silu_mul(g, u):
+    g = g.astype(np.float64)
+    return g / (1.0 + np.exp(-g)) * u.astype(np.float64)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 300, 512), (3, 333, 1024), (8, 1000, 4096),
+                                   (16, 256, 256), (17, 96, 992), (40, 130, 64),
+                                   (64, 192, 256), (100, 320, 1024), (129, 64, 512)])
+def test_swiglu_matches_oracle(dev, orc, M, N, K):
+    note(f"swiglu M={M} N={N} K={K}")
+    wg, wu = weight(60 + N, N, K), weight(61 + N, N, K)
+    x = S.activations(62 + K, (M, K))
+    want = silu_mul(orc.linear(x, wg, None, M, N, K), orc.linear(x, wu, None, M, N, K))
+    y = empty_f32((M, N), dev)
+    capi.linear_swiglu(to_dev(x, dev), to_dev(wg, dev), to_dev(wu, dev), y, M, N, K)
+    err = rel_l2(to_host(y), want)
+    assert err <= tol(M), err
+
+
+@pytest.mark.parametrize("M", [1, 8, 512])
+def test_swiglu_llama_ffn_full(dev, orc, M):
+    """Llama-7B gate/up [11008, 4096] at decode and prefill sizes: the whole output
+    against the separate Linears of the same entry points (silu * up in float64),
+    sampled rows against the oracle, and repeats bitwise equal."""
+    import torch
+    N, K = 11008, 4096
+    note(f"swiglu llama M={M}")
+    wg, wu = to_dev(weight(23, N, K), dev), to_dev(weight(24, N, K), dev)
+    xh = S.activations(25, (M, K))
+    x = to_dev(xh, dev)
+    y, y2 = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    g, u = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    capi.linear_swiglu(x, wg, wu, y, M, N, K)
+    capi.linear_swiglu(x, wg, wu, y2, M, N, K)
+    capi.linear(x, wg, None, g, M, N, K)
+    capi.linear(x, wu, None, u, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    got = to_host(y)
+    assert rel_l2(got, silu_mul(to_host(g), to_host(u))) <= tol(M)
+    rows = np.array([0, M // 2, M - 1])
+    wgh, wuh = weight(23, N, K), weight(24, N, K)
+    want_rows = silu_mul(orc.sgemm_nt(xh[rows], wgh, rows.size, N, K),
+                         orc.sgemm_nt(xh[rows], wuh, rows.size, N, K))
+    assert rel_l2(got[rows], want_rows) <= tol(M)
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 16, 40, 70])
+def test_multi_output_matches_oracle_and_single(dev, orc, M):
+    import torch
+    K = 512
+    Ns = (160, 96, 32)
+    ws = [weight(70 + i, n, K) for i, n in enumerate(Ns)]
+    biases = [S.activations(80, (Ns[0],), tag=S.TAG_BIAS), None,
+              S.activations(82, (Ns[2],), tag=S.TAG_BIAS)]
+    x = S.activations(83, (M, K))
+    note(f"multi M={M} Ns={Ns}")
+    dx = to_dev(x, dev)
+    dws = [to_dev(w, dev) for w in ws]
+    dbs = [to_dev(b, dev) if b is not None else None for b in biases]
+    ys = [empty_f32((M, n), dev) for n in Ns]
+    capi.linear_multi(dx, dws, dbs, ys, Ns, M, K)
+    torch.cuda.synchronize()
+    for i, n in enumerate(Ns):
+        want = orc.linear(x, ws[i], biases[i], M, n, K)
+        got = to_host(ys[i])
+        assert rel_l2(got, want) <= tol(M), i
+        if M < 64:
+            single = empty_f32((M, n), dev)
+            capi.linear(dx, dws[i], dbs[i], single, M, n, K)
+            torch.cuda.synchronize()
+            assert torch.equal(single, ys[i]), i
+
+
+@pytest.mark.parametrize("M,Ns", [(1, (4096, 1024, 1024)), (4, (4096, 1024, 1024)),
+                                  (8, (4096, 4096, 4096))])
+def test_multi_output_llama_qkv(dev, M, Ns):
+    """q/k/v of a grouped-query ([4096, 4096], [1024, 4096] x 2) and a multi-head
+    ([4096, 4096] x 3) layer: one launch equals three single Linears bit for bit
+    (at M=8 the fused launch uses 8-wave workgroups, the single ones 4-wave)."""
+    import torch
+    K = 4096
+    dws = [to_dev(weight(90 + i, n, K), dev) for i, n in enumerate(Ns)]
+    dx = to_dev(S.activations(93, (M, K)), dev)
+    ys = [empty_f32((M, n), dev) for n in Ns]
+    capi.linear_multi(dx, dws, None, ys, Ns, M, K)
+    for i, n in enumerate(Ns):
+        single = empty_f32((M, n), dev)
+        capi.linear(dx, dws[i], None, single, M, n, K)
+        torch.cuda.synchronize()
+        assert torch.equal(single, ys[i]), i
