@@ -130,6 +130,20 @@ int mle_q8_0_embedding(const uint8_t* table_q8_0, const int32_t* ids, float* out
                        int seq_len, int vocab, int hidden, hipStream_t stream);
 
 /*
+ * Greedy argmax of lm_head logits on the device: idx[r] = the first index of the
+ * largest value of logits[r*n : (r+1)*n] (ties -> lower index; -0 == +0; NaN
+ * entries ignored, a row of NaN only gives 0), val[r] = that value (val may be
+ * NULL).  Deterministic.  Replaces the device-to-host copy of every logits row
+ * that the reference's CUDA generator makes for its host-side greedy pick
+ * (examples/generate_cuda.cpp:81-94, 305-314; src/runtime/sampler.cpp:108-118):
+ * the caller copies back 4 (or 8) bytes per row instead.
+ * Errors: NULL logits / idx, rows or n <= 0 -> InvalidArgument; rows > 65535 ->
+ * Unsupported.  Uses the per-(device, stream) workspace of the Linear calls.
+ */
+int mle_argmax_f32(const float* logits, int rows, int n, int32_t* idx, float* val,
+                   hipStream_t stream);
+
+/*
  * Message of the last failed call on this thread ("" if none).  Stands in for
  * the message of the reference's Status return (status.h:34-59).  The pointer
  * stays valid until the next call on the same thread.

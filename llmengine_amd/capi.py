@@ -22,7 +22,8 @@ ERROR_NAMES = {0: "Ok", 1: "InvalidArgument", 2: "OutOfRange", 3: "ShapeMismatch
 
 EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_q8_0_linear_swiglu", "mle_q8_0_linear_multi", "mle_q8_0_matmul",
-            "mle_q8_0_embedding", "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode")
+            "mle_q8_0_embedding", "mle_argmax_f32", "mle_last_error", "mle_q8_0_bytes",
+            "mle_q8_0_f16_decode")
 
 
 class Q8_0Error(RuntimeError):
@@ -62,6 +63,8 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_matmul.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_q8_0_embedding.restype = _i
     lib.mle_q8_0_embedding.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_argmax_f32.restype = _i
+    lib.mle_argmax_f32.argtypes = [_vp, _i, _i, _vp, _vp, _vp]
     lib.mle_last_error.restype = ctypes.c_char_p
     lib.mle_last_error.argtypes = []
     lib.mle_q8_0_bytes.restype = ctypes.c_size_t
@@ -181,6 +184,16 @@ def embedding_status(w, ids, out, seq_len, vocab, hidden, stream=None):
 def embedding(w, ids, out, seq_len, vocab, hidden, stream=None) -> None:
     """out[s,h] = dequantised row ids[s] of a raw Q8_0 [vocab, hidden] table."""
     _raise(embedding_status(w, ids, out, seq_len, vocab, hidden, stream)[0])
+
+
+def argmax_status(logits, rows, n, idx, val=None, stream=None):
+    rc = load().mle_argmax_f32(_addr(logits), rows, n, _addr(idx), _addr(val), _stream(stream))
+    return _status(rc)
+
+
+def argmax(logits, rows, n, idx, val=None, stream=None) -> None:
+    """idx[r] (int32) = first index of the maximum of logits row r; val[r] its value."""
+    _raise(argmax_status(logits, rows, n, idx, val, stream)[0])
 
 
 def f16_decode(bits, out, n, stream=None) -> None:

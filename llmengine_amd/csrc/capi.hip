@@ -351,6 +351,26 @@ int mle_q8_0_linear_multi(const float* x, int count, const uint8_t* const* w,
   return run_segs(ctx, x, s, M, K, stream);
 }
 
+int mle_argmax_f32(const float* logits, int rows, int n, int32_t* idx, float* val,
+                   hipStream_t stream) {
+  const char* ctx = "argmax_f32";
+  MLE_TRY(check_ptrs(ctx, logits, "logits", idx, "idx", idx, "idx"));
+  MLE_TRY(check_positive(ctx, rows, "rows"));
+  MLE_TRY(check_positive(ctx, n, "n"));
+  if (rows > 65535)
+    return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": at most 65535 rows per call");
+  MLE_TRY(check_align(ctx, logits, 4, "logits"));
+  MLE_TRY(check_align(ctx, idx, 4, "idx"));
+  MLE_TRY(check_align(ctx, val, 4, "val"));
+  mle::SplitKNeed need;
+  need.partial_floats = (size_t)rows * mle::argmax_chunks(n) * 2;  // 64-bit keys
+  mle::SplitKWorkspace ws;
+  MLE_TRY(get_workspace(need, stream, &ws));
+  return check_launch(mle::launch_argmax(logits, rows, n, idx, val,
+                                         reinterpret_cast<uint64_t*>(ws.partials), stream),
+                      "hip argmax launch failed");
+}
+
 int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M, int N, int K,
                     hipStream_t stream) {
   const char* ctx = "sgemm_q8_0_weight";

@@ -103,6 +103,12 @@ hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const Line
 hipError_t launch_matmul(const float* a, const uint8_t* b, float* c, int M,
                          int N, int K, hipStream_t stream);
 
+// Greedy argmax of `rows` rows of n fp32 logits: idx (and val, if non-null) per
+// row; `keys` is a workspace of rows * argmax_chunks(n) 64-bit entries.
+int argmax_chunks(int64_t n);
+hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* idx, float* val,
+                         uint64_t* keys, hipStream_t stream);
+
 // Embedding gather-dequantise; ids outside [0, vocab) give rows of +0.0f.
 hipError_t launch_embedding(const uint8_t* w, const int32_t* ids, float* out,
                             int64_t seq_len, int vocab, int hidden,

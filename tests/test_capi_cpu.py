@@ -88,6 +88,22 @@ def test_fused_linear_validation_errors():
     assert rc == 1 and "arrays must not be null" in capi.last_error()
 
 
+def test_argmax_validation_errors():
+    st = capi.argmax_status
+    code, msg = st(None, 1, 10, FAKE, stream=0)
+    assert code == 1 and "logits pointer" in msg
+    code, msg = st(FAKE, 1, 10, None, stream=0)
+    assert code == 1 and "idx pointer" in msg
+    code, msg = st(FAKE, 0, 10, FAKE, stream=0)
+    assert code == 1 and "rows must be positive" in msg
+    code, msg = st(FAKE, 1, 0, FAKE, stream=0)
+    assert code == 1 and "n must be positive" in msg
+    code, msg = st(FAKE, 70000, 10, FAKE, stream=0)
+    assert code == 4 and "65535" in msg
+    code, msg = st(FAKE + 2, 1, 10, FAKE, stream=0)
+    assert code == 1 and "logits must be 4-byte aligned" in msg
+
+
 def test_linear_ex_rejects_bad_launch_shape():
     lib = capi.load()
     rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 1, 3, 32, 1, 0, None)

@@ -122,3 +122,80 @@ def test_multi_output_llama_qkv(dev, M, Ns):
         capi.linear(dx, dws[i], None, single, M, n, K)
         torch.cuda.synchronize()
         assert torch.equal(single, ys[i]), i
+
+
+# ----------------------------------------------------------------------------- argmax
+
+def first_argmax(x):
+    """Greedy pick of the reference (first maximum; NaN ignored; all-NaN -> 0)."""
+    out = []
+    for row in x:
+        ok = ~np.isnan(row)
+        if not ok.any():
+            out.append(0)
+            continue
+        best = np.max(row[ok])
+        out.append(int(np.flatnonzero(ok & (row == best))[0]))
+    return np.array(out, dtype=np.int32)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 1), (1, 7), (3, 2048), (2, 2049), (8, 151936),
+                                    (1, 151936), (5, 100_000)])
+def test_argmax_matches_first_maximum(dev, rows, n):
+    import torch
+    note(f"argmax rows={rows} n={n}")
+    x = S.activations(200 + n, (rows, n))
+    idx = torch.empty(rows, dtype=torch.int32, device=dev)
+    val = empty_f32((rows,), dev)
+    capi.argmax(to_dev(x, dev), rows, n, idx, val)
+    torch.cuda.synchronize()
+    want = first_argmax(x)
+    assert np.array_equal(idx.cpu().numpy(), want)
+    assert np.array_equal(val.cpu().numpy(), x[np.arange(rows), want])
+
+
+def test_argmax_ties_signed_zero_and_nan(dev):
+    import torch
+    n = 10_000
+    x = np.full((6, n), -1.0, dtype=np.float32)
+    x[0, [4000, 17, 9000]] = 3.0                    # tie -> lowest index 17
+    x[1, :] = 0.0
+    x[1, 5] = -0.0                                  # -0 == +0: index 0 wins
+    x[1, 0] = -0.0
+    x[2, :] = np.nan
+    x[2, 7777] = -5.0                               # only non-NaN value
+    x[3, :] = np.nan                                # NaN only -> 0
+    x[4, :] = -np.inf
+    x[4, 123] = np.float32(-3.4e38)                 # finite beats -inf
+    x[5, :] = np.inf                                # all +inf -> 0
+    idx = torch.empty(6, dtype=torch.int32, device=dev)
+    val = empty_f32((6,), dev)
+    capi.argmax(to_dev(x, dev), 6, n, idx, val)
+    torch.cuda.synchronize()
+    got = idx.cpu().numpy()
+    assert got.tolist() == [17, 0, 7777, 0, 123, 0]
+    v = val.cpu().numpy()
+    assert v[0] == 3.0 and v[2] == -5.0 and np.isnan(v[3]) and v[5] == np.inf
+    assert first_argmax(x).tolist() == got.tolist()
+
+
+def test_lm_head_then_argmax(dev, orc):
+    """Tied lm_head [151936, 896] Linear at M=1 and M=8 followed by the device argmax:
+    the picked token equals the first maximum of the oracle's logits wherever the
+    top two oracle logits are not within the Linear's error of each other."""
+    import torch
+    V, H = 151936, 896
+    w = weight(300, V, H)
+    dw = to_dev(w, dev)
+    for M in (1, 8):
+        x = S.activations(301 + M, (M, H))
+        logits = empty_f32((M, V), dev)
+        capi.linear(to_dev(x, dev), dw, None, logits, M, V, H)
+        idx = torch.empty(M, dtype=torch.int32, device=dev)
+        capi.argmax(logits, M, V, idx)
+        torch.cuda.synchronize()
+        assert np.array_equal(idx.cpu().numpy(), first_argmax(to_host(logits)))
+        want = orc.linear(x, w, None, M, V, H)
+        top2 = np.sort(want, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 1e-4 * np.abs(top2[:, 1])
+        assert np.array_equal(idx.cpu().numpy()[clear], first_argmax(want)[clear])
