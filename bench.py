@@ -17,7 +17,9 @@ algorithmic bytes per launch = N*(K/32)*34 + 4*M*K + 4*M*N.
 
 Also reported: per-launch kernel durations (HIP events on the launch stream, >= 100
 launches each), the roofline of the dominant launch, the prefill GEMM of configs[2]
-(M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding gather of configs[4], and the
+(M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding gather of configs[4], the fused
+Linear entry points (gate/up + SwiGLU, q/k/v multi-output) against their unfused launches,
+the device argmax of an lm_head logits row against copying the row to the host, and the
 reference's own CPU kernels timed on this host (cpu_baseline).
 """
 from __future__ import annotations
@@ -112,18 +114,20 @@ def cpu_baseline(weights_host, xs_host):
         lib, kind = oracle.reference(), "reference"
     else:
         lib, kind = oracle.oracle(), "port"
-    total_bytes, t0 = 0, time.perf_counter()
-    for M in (1, 4):
-        for name, N, K in LLAMA_SET:
-            lib.sgemm_nt(xs_host[(M, K)], weights_host[name], M, N, K)
-            total_bytes += gemv_bytes(M, N, K)
+    total_bytes, reps, t0 = 0, 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < 10.0:  # a ~10 s bounded sample
+        for M in (1, 4):
+            for name, N, K in LLAMA_SET:
+                lib.sgemm_nt(xs_host[(M, K)], weights_host[name], M, N, K)
+                total_bytes += gemv_bytes(M, N, K)
+        reps += 1
     dt = time.perf_counter() - t0
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(total_bytes / dt / 1e9, 4), "unit": "GB/s",
             "cores": min(4, threads), "kind": kind,
-            "sample": (f"M=1 and M=4 launches of one step (10 Q8_0 Linears, all rows) in "
-                       f"{dt:.1f} s; the reference parallelises over M only, so M=1 ran on 1 "
-                       f"thread and M=4 on 4 (OMP_NUM_THREADS={threads})")}
+            "sample": (f"M=1 and M=4 launches of one step (10 Q8_0 Linears, all rows), "
+                       f"{reps} times in {dt:.1f} s; the reference parallelises over M only, "
+                       f"so M=1 ran on 1 thread and M=4 on 4 (OMP_NUM_THREADS={threads})")}
 
 
 def main():
@@ -264,6 +268,70 @@ def main():
                                "GBps": round(eb / us / 1e3, 1),
                                "frac_hbm": round(eb / us / 1e3 / HBM_PEAK_GBS, 4)}
         del tbls
+
+        def timed(fn, iters):
+            for j in range(3):
+                fn(j)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for j in range(iters):
+                fn(j)
+            b.record(stream)
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) * 1e3 / iters
+
+        # ---- fused FFN front (gate/up + SwiGLU) and q/k/v multi-output, per call
+        fused = []
+        gw, uw = wdev["gate"], wdev["up"]
+        N, K = 11008, 4096
+        for M in (1, 4, 8, 512):
+            x = xdev[(M, K)] if (M, K) in xdev else torch.from_numpy(
+                S.activations(3000 + M, (M, K))).to(dev)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            g2 = torch.empty_like(y)
+            iters = 40 if M >= 64 else 100
+            tf = timed(lambda j: capi.linear_swiglu(x, gw[j % R], uw[j % R], y, M, N, K,
+                                                    stream=stream), iters)
+            ts = timed(lambda j: (capi.linear(x, gw[j % R], None, y, M, N, K, stream=stream),
+                                  capi.linear(x, uw[j % R], None, g2, M, N, K,
+                                              stream=stream)), iters)
+            nb = 2 * gemv_bytes(M, N, K) - 4 * M * K - 4 * M * N
+            fused.append({"op": "gate+up -> SwiGLU [2 x 11008x4096]", "M": M,
+                          "us_fused": round(tf, 2), "us_two_linears": round(ts, 2),
+                          "GBps_fused": round(nb / tf / 1e3, 1)})
+        qkv = [torch.from_numpy(S.q8_0_weight(40 + i, 4096, 4096)[0]).to(dev) for i in range(3)]
+        Rq = max(2, -(-ROTATE_BYTES // (3 * qkv[0].numel())) + 1)  # past the Infinity Cache
+        qkv_r = [qkv] + [[w.clone() for w in qkv] for _ in range(Rq - 1)]
+        for M in (1, 4, 8):
+            x = xdev[(M, 4096)]
+            ys = [torch.empty((M, 4096), dtype=torch.float32, device=dev) for _ in range(3)]
+            tf = timed(lambda j: capi.linear_multi(x, qkv_r[j % Rq], None, ys, (4096,) * 3, M,
+                                                   4096, stream=stream), 100)
+            ts = timed(lambda j: [capi.linear(x, qkv_r[j % Rq][i], None, ys[i], M, 4096, 4096,
+                                              stream=stream) for i in range(3)], 100)
+            nb = 3 * gemv_bytes(M, 4096, 4096) - 2 * 4 * M * 4096
+            fused.append({"op": "q,k,v multi-output [3 x 4096x4096]", "M": M,
+                          "us_fused": round(tf, 2), "us_three_linears": round(ts, 2),
+                          "GBps_fused": round(nb / tf / 1e3, 1)})
+        extras["fused"] = fused
+        del qkv, qkv_r
+
+        # ---- greedy pick over lm_head logits: device argmax vs copying the row back
+        V = 151936
+        logits = torch.from_numpy(S.activations(7, (1, V))).to(dev)
+        idx = torch.empty(1, dtype=torch.int32, device=dev)
+        t_arg = timed(lambda j: capi.argmax(logits, 1, V, idx, stream=stream), 200)
+        host = torch.empty((1, V), dtype=torch.float32).pin_memory()
+        for _ in range(3):
+            host.copy_(logits)
+        t0c = time.perf_counter()
+        for _ in range(200):
+            host.copy_(logits)
+        t_copy = (time.perf_counter() - t0c) / 200 * 1e6
+        extras["argmax"] = {"vocab": V, "rows": 1, "us_device_argmax": round(t_arg, 2),
+                            "us_copy_row_to_host": round(t_copy, 2),
+                            "note": "the reference copies the logits row to the host per token "
+                                    "and picks there; the device argmax returns 4 bytes"}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(weights_host, xs_host)
 

@@ -131,6 +131,19 @@ Status sgemm(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int 
              hipStream_t stream = nullptr);
 Status embedding(const uint8_t* weight_q8_0, const int* ids, float* out, int seq_len,
                  int vocab_size, int hidden, hipStream_t stream = nullptr);
+
+// Fused launchers with no counterpart among the reference's kernels (see
+// mle_q8_0.h): y = silu(x.Wg^T) * (x.Wu^T) in place of Linear + Linear +
+// SwiGLU (transformer_graph_builder.cpp:261-268); up to three Linears on one
+// input (q/k/v, :214-221); the greedy argmax of logits rows on the device
+// (generate_cuda.cpp:305-314 copies the whole row to the host instead).
+Status linear_swiglu(const float* x, const uint8_t* w_gate_q8_0, const uint8_t* w_up_q8_0,
+                     float* y, int M, int N, int K, hipStream_t stream = nullptr);
+Status linear_multi(const float* x, int count, const uint8_t* const* w_q8_0,
+                    const float* const* bias, float* const* y, const int* N, int M, int K,
+                    hipStream_t stream = nullptr);
+Status argmax(const float* logits, int rows, int n, int32_t* idx, float* val = nullptr,
+              hipStream_t stream = nullptr);
 }  // namespace hip
 
 }  // namespace minillm

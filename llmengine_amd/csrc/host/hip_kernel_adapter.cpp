@@ -249,6 +249,22 @@ Status embedding(const uint8_t* weight_q8_0, const int* ids, float* out, int seq
                                       seq_len, vocab_size, hidden, stream));
 }
 
+Status linear_swiglu(const float* x, const uint8_t* w_gate_q8_0, const uint8_t* w_up_q8_0,
+                     float* y, int M, int N, int K, hipStream_t stream) {
+  return from_capi(mle_q8_0_linear_swiglu(x, w_gate_q8_0, w_up_q8_0, y, M, N, K, stream));
+}
+
+Status linear_multi(const float* x, int count, const uint8_t* const* w_q8_0,
+                    const float* const* bias, float* const* y, const int* N, int M, int K,
+                    hipStream_t stream) {
+  return from_capi(mle_q8_0_linear_multi(x, count, w_q8_0, bias, y, N, M, K, stream));
+}
+
+Status argmax(const float* logits, int rows, int n, int32_t* idx, float* val,
+              hipStream_t stream) {
+  return from_capi(mle_argmax_f32(logits, rows, n, idx, val, stream));
+}
+
 }  // namespace hip
 
 void register_hip_kernels(KernelRegistry& registry) {

@@ -577,6 +577,63 @@ static void test_gguf_model_end_to_end() {
   std::printf("  PASS test_gguf_model_end_to_end\n");
 }
 
+static void test_fused_launchers() {
+  // M=3, N=40, K=64, scale 1.0, integer quants x dyadic activations: every
+  // Linear sum is exact, so gate/up are known exactly; silu in double.
+  const int M = 3, N = 40, K = 64;
+  std::vector<float> x(M * K);
+  for (int i = 0; i < M * K; ++i) x[i] = float((i * 7) % 9 - 4) * 0.125f;
+  std::vector<int8_t> qg(N * K), qu(N * K), qv(N * K);
+  for (int i = 0; i < N * K; ++i) {
+    qg[i] = int8_t((i * 5) % 11 - 5);
+    qu[i] = int8_t((i * 3) % 13 - 6);
+    qv[i] = int8_t((i * 11) % 7 - 3);
+  }
+  const auto pg = pack_q8_0(qg, 0x3c00), pu = pack_q8_0(qu, 0x3c00), pv = pack_q8_0(qv, 0x3c00);
+  DevBuf<float> dx(x.size()), dy(M * N), dy2(M * N), dy3(M * N);
+  DevBuf<uint8_t> dg(pg.size()), du(pu.size()), dv(pv.size());
+  dx.put(x);
+  dg.put(pg);
+  du.put(pu);
+  dv.put(pv);
+  auto dot = [&](const std::vector<int8_t>& q, int m, int n) {
+    double s = 0;
+    for (int k = 0; k < K; ++k) s += double(x[m * K + k]) * q[n * K + k];
+    return s;
+  };
+  check_status(hip::linear_swiglu(dx.p, dg.p, du.p, dy.p, M, N, K));
+  const uint8_t* ws[3] = {dg.p, du.p, dv.p};
+  float* ys[3] = {dy.p, dy2.p, dy3.p};
+  const int Ns[3] = {N, N, N};
+  const auto sw = dy.get();
+  check_status(hip::linear_multi(dx.p, 3, ws, nullptr, ys, Ns, M, K));
+  const auto g = dy.get(), u = dy2.get(), v = dy3.get();
+  for (int m = 0; m < M; ++m)
+    for (int n = 0; n < N; ++n) {
+      const double gg = dot(qg, m, n), uu = dot(qu, m, n);
+      CHECK(g[m * N + n] == float(gg) && u[m * N + n] == float(uu));
+      CHECK(v[m * N + n] == float(dot(qv, m, n)));
+      const double want = gg / (1.0 + std::exp(-gg)) * uu;
+      near(sw[m * N + n], float(want), 1e-5f * float(std::fabs(want)) + 1e-6f);
+    }
+  // Argmax of the gate outputs per row.
+  DevBuf<int32_t> di(M);
+  DevBuf<float> dval(M);
+  check_status(hip::argmax(dy.p, M, N, di.p, dval.p));
+  const auto ix = di.get();
+  const auto vx = dval.get();
+  for (int m = 0; m < M; ++m) {
+    int best = 0;
+    for (int n = 1; n < N; ++n)
+      if (g[m * N + n] > g[m * N + best]) best = n;
+    CHECK(ix[m] == best && vx[m] == g[m * N + best]);
+  }
+  CHECK(hip::argmax(dy.p, 0, N, di.p).code() == ErrorCode::InvalidArgument);
+  CHECK(hip::linear_swiglu(dx.p, dg.p, nullptr, dy.p, M, N, K).code() ==
+        ErrorCode::InvalidArgument);
+  std::printf("  PASS test_fused_launchers\n");
+}
+
 int main() {
   int count = 0;
   check_hip(hipGetDeviceCount(&count));
@@ -590,6 +647,7 @@ int main() {
   test_executor_rejects_invalid_inputs();
   test_executor_prefill_linear();
   test_gguf_model_end_to_end();
+  test_fused_launchers();
   std::printf("test_hip_q8_0: all passed\n");
   return 0;
 }
