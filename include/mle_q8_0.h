@@ -54,9 +54,10 @@ int mle_q8_0_abi_version(void);
  * minillm::cuda::add_bias(float*, const float*, int, int) (cuda_kernels.h:22),
  * which this entry point fuses when `bias` is non-NULL (NULL = no bias).
  *
- * Paths: M == 1 runs the FP32 decode GEMV; 2 <= M < 64 runs the MFMA decode
- * kernel in chunks of up to 16 tokens (FP32 activations split exactly into
- * three bf16 parts, so it matches FP32 to about 1e-7 relative L2);
+ * Paths: M == 1, and M <= 4 with K <= 1024, run the FP32 decode GEMV; other
+ * M < 64 run the MFMA decode kernel in chunks of up to 16 tokens (FP32
+ * activations split exactly into three bf16 parts, so it matches FP32 to about
+ * 1e-7 relative L2);
  * M >= 64 runs the bf16-MFMA prefill GEMM (relative L2 error vs FP32 about
  * 2e-3).  Both MFMA paths may split K over workgroups and reduce the partials
  * in a fixed order, so results are deterministic run to run.

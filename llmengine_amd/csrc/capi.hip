@@ -143,7 +143,13 @@ int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWo
 
 // Linear path numbers (mle_q8_0_linear_ex): 1 FP32 GEMV, 2 bf16-MFMA prefill GEMM,
 // 3 MFMA decode with FP32-exact activations.
-int pick_path(int M) { return M >= 64 ? 2 : M == 1 ? 1 : 3; }
+// The FP32 GEMV also wins for a few tokens on short rows (K <= 1024, e.g. the
+// 896-wide Qwen projections: 4.5-5.1 us vs 5.5-7.0 us at M = 2..4, MI355X).
+int pick_path(int M, int K) {
+  if (M >= 64) return 2;
+  if (M == 1 || (M <= 4 && K <= 1024)) return 1;
+  return 3;
+}
 
 struct Tune {
   mle::GemvConfig gemv{0, 0, 0};
@@ -154,7 +160,7 @@ struct Tune {
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
                int N, int K, int path, const Tune& tune, hipStream_t stream) {
   if (path == 0) {
-    path = pick_path(M);
+    path = pick_path(M, K);
     if (path == 3 && !mle::decode_mfma_fits(mle::decode_mfma_pick(M < 16 ? M : 16, N, K),
                                             M < 16 ? M : 16, N, K))
       path = 1;
@@ -215,9 +221,10 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
 }
 
 // One launch over 1-3 output segments (multi-output Linear) or a gate/up pair
-// (SwiGLU): the bf16 MFMA GEMM for M >= 64, the FP32 GEMV for M == 1, else the
-// MFMA decode kernel in chunks of up to 16 tokens (FP32-exact activations) --
-// the same path choice as a single Linear.
+// (SwiGLU): the same path choice as a single Linear (bf16 MFMA GEMM for
+// M >= 64, FP32 GEMV for M == 1 and for M <= 4 on short rows, else the MFMA
+// decode kernel in chunks of up to 16 tokens with FP32-exact activations);
+// SwiGLU takes the GEMV for M == 1 only.
 int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, int K,
              hipStream_t stream) {
   const bool swi = s.mode == mle::Epilogue::kSwiGLU;
@@ -232,9 +239,9 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
     return check_launch(mle::launch_gemm_mfma_segs(c, x, s, M, K, ws, stream),
                         "hip Q8_0 fused Linear launch failed");
   }
-  if (M == 1) {
-    const mle::GemvConfig c = mle::gemv_pick_config(1, total_n, K);
-    return check_launch(mle::launch_gemv_segs(c, x, s, 1, K, stream),
+  if (swi ? M == 1 : pick_path(M, K) == 1) {
+    const mle::GemvConfig c = mle::gemv_pick_config(M, total_n, K);
+    return check_launch(mle::launch_gemv_segs(c, x, s, M, K, stream),
                         "hip Q8_0 fused Linear launch failed");
   }
   for (int m0 = 0; m0 < M; m0 += 16) {

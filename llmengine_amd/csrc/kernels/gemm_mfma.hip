@@ -13,13 +13,16 @@
 //      memory (loading fragments from a row-major X spreads each load
 //      instruction over 32 rows, which halves the L2->CU throughput).
 //   2. the GEMM.  Workgroup tile BM x BN (BM = 128 MI, BN = 32 NJ), K step 64
-//      (two Q8_0 blocks per W row), 512 threads in two roles:
-//        * 4 consumer waves stacked along M: wave w owns rows
-//          [32 MI w, 32 MI (w+1)) of the tile and all BN columns as MI x NJ
-//          v_mfma_f32_32x32x16_bf16 accumulators;
+//      (two Q8_0 blocks per W row), waves in two roles:
+//        * CW consumer waves stacked along M: wave w owns rows
+//          [32 MW w, 32 MW (w+1)) of the tile and all BN columns as MW x NJ
+//          v_mfma_f32_32x32x16_bf16 accumulators.  128-row tiles: CW = 4,
+//          MW = 1; 256-row tiles: CW = 8, MW = 1 (two consumer waves per SIMD,
+//          so one's MFMAs cover the other's waits: 2-6% faster than 4 waves of
+//          64 rows);
 //        * 4 producer waves that load and dequantise W.
-//      Each SIMD runs one wave of each role, so the producers' vector ALU work
-//      overlaps the consumers' MFMAs.
+//      Each SIMD runs consumer and producer waves side by side, so the
+//      producers' vector ALU work overlaps the consumers' MFMAs.
 //
 // Operands:
 //   * A (X): each consumer wave loads its own rows' bf16 fragments straight from
@@ -28,7 +31,7 @@
 //   * B (W): per K step, producer thread t < 2 BN takes one 34-byte block (row
 //     t/2, block t%2 of the step), forms v = d * q in fp32 (exactly the
 //     reference's element value), rounds it once to bf16 and writes the 32
-//     values to an LDS tile that all four consumer waves read.  Each W element is
+//     values to an LDS tile that all consumer waves read.  Each W element is
 //     thus dequantised once per workgroup, and one dequantised element feeds
 //     2 BM flops.
 //   The per-block scale is folded into B rather than applied to the accumulator
@@ -124,7 +127,14 @@ struct XStage {
   u32x4 x[MI][4];
 };
 
-constexpr int kThreads = 512;  // 4 consumer (MFMA) waves + 4 producer (W) waves
+// Consumer (MFMA) waves: 8 for 256-row tiles (two per SIMD, 32 rows each), else
+// 4; plus 4 producer (W) waves.
+template <int MI>
+struct Roles {
+  static constexpr int CW = MI == 2 ? 8 : 4;
+  static constexpr int MW = MI * 4 / CW;
+  static constexpr int kThreads = 64 * (CW + 4);
+};
 
 // Output segments as the kernel sees them: segment i owns the column tiles
 // [tile_end[i-1], tile_end[i]) of the grid.
@@ -145,10 +155,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // each wave reads one weight; the epilogue writes silu(gate) * up for BN/2
 // output columns.
 template <int MI, int NJ, int MODE>
-__global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
+__global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
     const u32x4* __restrict__ xf, uint32_t xf_bytes, const GemmArgs args, int M, int K,
     int steps_per_split, float* __restrict__ partials, uint32_t* __restrict__ counters) {
   constexpr int BM = 128 * MI;
+  constexpr int CW = Roles<MI>::CW, MW = Roles<MI>::MW;  // consumer waves, 32-row blocks each
   constexpr int BN = 32 * NJ;
   constexpr bool kSwi = MODE == 1;
   constexpr int BNO = kSwi ? BN / 2 : BN;  // output columns per tile
@@ -157,7 +168,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
   constexpr int NBLK = 2 * BN;  // W blocks per K step (<= 256 producer threads)
   constexpr int TILE_ELEMS = BM * BN;
   constexpr int BUF = BN * LDS_STRIDE;
-  // X register stages per consumer lane (32 MI VGPRs each).
+  // X register stages per consumer lane (32 MW VGPRs each).
   constexpr int XS = 3;
   __shared__ __attribute__((aligned(16))) uint16_t Bs[4 * BUF];  // 2 buffers x 2 steps
   __shared__ uint32_t arrived;
@@ -165,9 +176,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const bool consumer = wave < 4;  // wave-uniform role
-  const int cw = wave & 3;         // consumer wave: rows 32 MI cw .. of the tile
-  const int pt = tid & 255;        // producer thread: W block pt of each step
+  const bool consumer = wave < CW;  // wave-uniform role
+  const int cw = wave;              // consumer wave: rows 32 MW cw .. of the tile
+  const int pt = tid - 64 * CW;     // producer thread: W block pt of each step
   const int64_t m0 = (int64_t)blockIdx.y * BM;
   // Segment of this column tile (uniform selects: no indexing into the argument).
   const unsigned tile = blockIdx.x;
@@ -191,17 +202,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
   // D[i][jj] of lane l holds rows 4 (l/32) + v%4 + 8 (v/4), column l%32, i.e.
   // four rows of one column per register quad: storing that directly takes one
   // 4-byte store per value.  Instead each consumer wave stages 16-row chunks of
-  // its 32 MI x BN tile in its own part of the (now idle) W buffers and writes
+  // its 32 MW x BN tile in its own part of the (now idle) W buffers and writes
   // them back as 16-byte pieces of contiguous rows (bias added on the way).
-  const int wm = cw * 32 * MI;
+  const int wm = cw * 32 * MW;
   constexpr int EP_STRIDE = BN + 4;  // floats per staged row: 16-byte rows, banks spread
-  static_assert(4 * 16 * EP_STRIDE * 4 <= 2 * BUF * 2, "epilogue staging exceeds LDS");
-  auto store_tile = [&](auto role, const f32x16 (&v)[MI][NJ]) {
+  static_assert(CW * 16 * EP_STRIDE * 4 <= 4 * BUF * 2, "epilogue staging exceeds LDS");
+  auto store_tile = [&](auto role, const f32x16 (&v)[MW][NJ]) {
     constexpr bool kConsumer = decltype(role)::value;
     float* ep = reinterpret_cast<float*>(Bs) + cw * 16 * EP_STRIDE;
     const bool vec = (N & 3) == 0;
 #pragma unroll
-    for (int c = 0; c < 2 * MI; ++c) {  // rows 16 c .. 16 c + 15 of this wave's rows
+    for (int c = 0; c < 2 * MW; ++c) {  // rows 16 c .. 16 c + 15 of this wave's rows
       const int i = c >> 1, h = c & 1;
       __syncthreads();  // the previous reads of this staging area are done
       if constexpr (kConsumer) {
@@ -243,7 +254,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
       }
     }
   };
-  auto finish = [&](auto role, f32x16 (&acc)[MI][NJ]) {
+  auto finish = [&](auto role, f32x16 (&acc)[MW][NJ]) {
   constexpr bool kConsumer = decltype(role)::value;
   if (gridDim.z == 1) {
     store_tile(role, acc);
@@ -259,11 +270,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
   const __amdgpu_buffer_rsrc_t prs =
       rsrc(partials + (int64_t)tile * gridDim.z * TILE_ELEMS, gridDim.z * TILE_ELEMS * 4u);
   auto slot = [&](int i, int jj, int q) {  // byte offset of 4 accumulators
-    return (uint32_t)((((i * NJ + jj) * 4 + q) * 256 + pt) * 16);
+    return (uint32_t)((((i * NJ + jj) * 4 + q) * (64 * CW) + tid) * 16);
   };
   if constexpr (kConsumer) {
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int i = 0; i < MW; ++i)
 #pragma unroll
       for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
@@ -287,7 +298,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
   if (arrived != gridDim.z - 1) return;
   if constexpr (kConsumer) {
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int i = 0; i < MW; ++i)
 #pragma unroll
       for (int jj = 0; jj < NJ; ++jj) {
         f32x4 sum[4];
@@ -313,9 +324,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
   // iteration t publishes the bf16 W tile of step t+1 (producers) and retires
   // the MFMAs of step t (consumers), which read LDS buffer (t - s_begin) % 2.
   if (consumer) {
-    f32x16 acc[MI][NJ];
+    f32x16 acc[MW][NJ];
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int i = 0; i < MW; ++i)
 #pragma unroll
       for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
@@ -323,21 +334,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
     // A: fragments of 32-row tile R at step s start at byte ((R n_steps + s) 4
     // + j) KB; tiles past the converted rows read as zero.
     const __amdgpu_buffer_rsrc_t xrs = rsrc(xf, xf_bytes);
-    uint32_t xoff[MI];
+    uint32_t xoff[MW];
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
-      xoff[i] = (uint32_t)((m0 / 32 + cw * MI + i) * n_steps) * 4096u + lane * 16u;
-    auto load_x = [&](int s, XStage<MI>& st) {
+    for (int i = 0; i < MW; ++i)
+      xoff[i] = (uint32_t)((m0 / 32 + cw * MW + i) * n_steps) * 4096u + lane * 16u;
+    auto load_x = [&](int s, XStage<MW>& st) {
       const uint32_t sx = (uint32_t)min(s, s_last) * 4096u;
 #pragma unroll
-      for (int i = 0; i < MI; ++i)
+      for (int i = 0; i < MW; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           st.x[i][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[i] + 1024 * j, sx, 0);
     };
     // B fragment of lane (c, h) for MFMA j: row 32 jj + c, K values 32 h + 8 j .. +7.
     const int boff_lds = (lane & 31) * LDS_STRIDE + 32 * (lane >> 5);
-    auto mfma_step = [&](const uint16_t* bs, const XStage<MI>& st) {
+    auto mfma_step = [&](const uint16_t* bs, const XStage<MW>& st) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         bf16x8 bf[NJ];
@@ -345,7 +356,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
         for (int jj = 0; jj < NJ; ++jj)
           bf[jj] = *reinterpret_cast<const bf16x8*>(bs + jj * 32 * LDS_STRIDE + boff_lds + 8 * j);
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
+        for (int i = 0; i < MW; ++i) {
           const bf16x8 a = __builtin_bit_cast(bf16x8, st.x[i][j]);
 #pragma unroll
           for (int jj = 0; jj < NJ; ++jj)
@@ -359,7 +370,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
     // One barrier per pair of K steps: buffer p holds the bf16 W of steps
     // (t, t + 1) of the current pair in its halves.
     static_assert(XS == 3, "pair loop unrolls by lcm(2, XS) = 6 steps");
-    XStage<MI> st[XS];
+    XStage<MW> st[XS];
 #pragma unroll
     for (int u = 0; u < XS - 1; ++u) load_x(s_begin + u, st[u]);
     __syncthreads();  // W of steps s_begin, s_begin + 1 are in buffer 0
@@ -391,7 +402,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
     // Item (row, block) of this thread within its weight.  Plain: items
     // pt < 2 BN.  SwiGLU: producer waves 0-1 take the gate items, 2-3 the up
     // items (tile rows BNO + row), so the weight is uniform per wave.
-    const int pwave = __builtin_amdgcn_readfirstlane(wave) - 4;
+    const int pwave = __builtin_amdgcn_readfirstlane(wave) - CW;
     const bool up_rows = kSwi && pwave >= 2;
     const int item = kSwi ? (pwave & 1) * 64 + lane : pt;
     const int prow = item >> 1, wn_h = item & 1;  // row within its weight, block of the step
@@ -460,7 +471,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q8_0_mfma_kernel(
 #pragma unroll
     for (int u = 0; u < RING; u += 2)
       if (t + u < s_end) pair(t + u, u);
-    f32x16 none[MI][NJ];  // never read: producers only join the barriers
+    f32x16 none[MW][NJ];  // never read: producers only join the barriers
     finish(std::false_type{}, none);
   }
 
@@ -506,10 +517,10 @@ void launch_tile(const GemmGrid& g, Epilogue mode, const u32x4* xf, uint32_t xf_
                  int K, const SplitKWorkspace& ws, hipStream_t stream) {
   const dim3 grid(g.tn, g.tm, g.splits);
   if (mode == Epilogue::kSwiGLU) {
-    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 1>), grid, dim3(kThreads), 0, stream, xf,
+    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 1>), grid, dim3(Roles<MI>::kThreads), 0, stream, xf,
                        xf_bytes, g.args, M, K, g.steps_per_split, ws.partials, ws.counters);
   } else {
-    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 0>), grid, dim3(kThreads), 0, stream, xf,
+    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 0>), grid, dim3(Roles<MI>::kThreads), 0, stream, xf,
                        xf_bytes, g.args, M, K, g.steps_per_split, ws.partials, ws.counters);
   }
 }

@@ -174,7 +174,8 @@ def test_linear_c2_llama_decode(dev, orc, M, N, K):
 
 
 @pytest.mark.parametrize("N,K,M", [(1152, 896, 1), (4864, 896, 1), (896, 4864, 1),
-                                   (151936, 896, 1), (151936, 896, 8)])
+                                   (151936, 896, 1), (151936, 896, 8), (1152, 896, 4),
+                                   (4864, 896, 2), (896, 4864, 3)])
 def test_linear_c4_qwen_decode(dev, orc, N, K, M):
     note(f"linear C4 M={M} N={N} K={K}")
     w, x = weight(4, N, K), acts(4 + M, M, K)
