@@ -540,17 +540,18 @@ bool gemm_mfma_config_valid(const GemmConfig& c) {
 }
 
 GemmConfig gemm_mfma_pick_segs(int M, const LinearSegs& s, int K) {
-  // Estimated time = rounds of workgroups over the 256 CUs x K steps per
-  // workgroup x the measured time of one K step of the tile shape (MI355X,
-  // microseconds), plus the split-K partial traffic (written and read once per
-  // split, at the ~2 TB/s it sustains).  Tile heights of 256 only once M
-  // exceeds 128.  A SwiGLU tile holds BN/2 rows of each weight.
+  // Estimated time = rounds of workgroups over the 256 CUs (one per CU) x K
+  // steps per workgroup x the measured time of one K step of the tile shape
+  // (MI355X, microseconds, fitted over M = 512 x {11008, 12288, 4096} x
+  // {4096, 11008} sweeps), plus the split-K partial traffic (written and read
+  // once per split; it mostly stays in cache, ~5.6 TB/s).  Tile heights of 256
+  // only once M exceeds 128.  A SwiGLU tile holds BN/2 rows of each weight.
   struct Shape {
     int bm, bn;
     double step_us;
   };
-  static const Shape shapes[] = {{256, 96, 0.98}, {256, 64, 0.73}, {128, 128, 0.71},
-                                 {128, 96, 0.67}, {128, 64, 0.55}};
+  static const Shape shapes[] = {{256, 96, 0.90}, {256, 64, 0.75}, {128, 128, 0.85},
+                                 {128, 96, 0.62}, {128, 64, 0.52}};
   const bool swi = s.mode == Epilogue::kSwiGLU;
   const int count = swi ? 1 : s.count;
   const int n_steps = padded_k(K) / BK;
@@ -570,7 +571,7 @@ GemmConfig gemm_mfma_pick_segs(int M, const LinearSegs& s, int K) {
       const int64_t rounds = (tiles * splits + 255) / 256;
       const int steps = (n_steps + splits - 1) / splits;
       const double split_us =
-          splits > 1 ? (double)splits * M * out_cols * (swi ? 2 : 1) * 8 / 2.1e6 : 0.0;
+          splits > 1 ? (double)splits * M * out_cols * (swi ? 2 : 1) * 8 / 5.6e6 : 0.0;
       const double us = (double)rounds * steps * sh.step_us + split_us;
       if (us < best_us) {
         best_us = us;
