@@ -130,6 +130,8 @@ class Graph {
 expected<Shape, Status> infer_matmul_shape(const Shape& a, const Shape& b);
 expected<Shape, Status> infer_linear_shape(const Shape& x, const Shape& weight);
 expected<Shape, Status> infer_embedding_shape(const Shape& input_ids, const Shape& weight);
+// Same rank, equal known dims (reference src/graph/shape_infer.cpp:48-63).
+expected<Shape, Status> infer_elementwise_shape(const Shape& a, const Shape& b);
 
 class GraphBuilder {
  public:
@@ -143,6 +145,8 @@ class GraphBuilder {
   expected<ValueId, Status> matmul(ValueId a, ValueId b, std::string name);
   expected<ValueId, Status> linear(ValueId x, ValueId weight, std::optional<ValueId> bias,
                                    std::string name);
+  // y = silu(gate) * up (reference src/graph/graph_builder.cpp:168-184).
+  expected<ValueId, Status> swiglu(ValueId gate, ValueId up, std::string name);
   expected<ValueId, Status> output(ValueId x, std::string name);
 
  private:

@@ -108,11 +108,35 @@ class HipExecutor final : public Executor {
   Status run(RuntimeContext& ctx) override;
   hipStream_t stream() const { return stream_; }
 
+  // Linear epilogue fusion (on by default; takes effect at the next compile):
+  //  * Linear(gate) + Linear(up) + SwiGLU, where both Linears read one input,
+  //    have no bias and feed only the SwiGLU, run as one fused launch at the
+  //    SwiGLU's place (the two Linear outputs are then not written);
+  //  * 2-3 other Linears reading one input (q/k/v) run as one multi-output
+  //    launch at the first one's place.
+  // A group whose bound tensors do not fit the fused kernels (e.g. non-Q8_0
+  // weights) runs node by node.  Off: one launch per node in topological
+  // order, exactly the reference executor's schedule.
+  void set_fusion(bool on) { fusion_ = on; }
+  bool fusion() const { return fusion_; }
+  // Fused groups in the compiled plan, and fused launches made by the last run.
+  size_t fused_groups() const;
+  size_t fused_launches() const { return fused_launches_; }
+
  private:
+  struct Step {
+    enum Kind { kNode, kSwiGLU, kMulti } kind;
+    std::vector<NodeId> nodes;  // kSwiGLU: gate, up, swiglu; kMulti: 2-3 Linears
+  };
+  Status run_nodes(const std::vector<NodeId>& ids, RuntimeContext& ctx);
+
   const Graph* graph_{nullptr};
   std::shared_ptr<Backend> backend_;
   KernelRegistry& registry_;
   std::vector<NodeId> execution_order_;
+  std::vector<Step> plan_;
+  bool fusion_{true};
+  size_t fused_launches_{0};
   hipStream_t stream_;
 };
 

@@ -131,6 +131,16 @@ int mle_q8_0_embedding(const uint8_t* table_q8_0, const int32_t* ids, float* out
                        int seq_len, int vocab, int hidden, hipStream_t stream);
 
 /*
+ * Unfused SwiGLU: y[i] = silu(gate[i]) * up[i] for i < n (n == 0: no-op),
+ * evaluated as the reference does ((g / (1 + exp(-g))) * u).  Replaces the
+ * reference's swiglu launcher (src/runtime/kernels/cuda_kernels.cu:245-248) for
+ * the HIP backend's SwiGLU op.
+ * Errors: NULL pointers or n < 0 -> InvalidArgument.
+ */
+int mle_swiglu_f32(const float* gate, const float* up, float* y, int64_t n,
+                   hipStream_t stream);
+
+/*
  * Greedy argmax of lm_head logits on the device: idx[r] = the first index of the
  * largest value of logits[r*n : (r+1)*n] (ties -> lower index; -0 == +0; NaN
  * entries ignored, a row of NaN only gives 0), val[r] = that value (val may be

@@ -22,8 +22,8 @@ ERROR_NAMES = {0: "Ok", 1: "InvalidArgument", 2: "OutOfRange", 3: "ShapeMismatch
 
 EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_q8_0_linear_swiglu", "mle_q8_0_linear_multi", "mle_q8_0_matmul",
-            "mle_q8_0_embedding", "mle_argmax_f32", "mle_last_error", "mle_q8_0_bytes",
-            "mle_q8_0_f16_decode")
+            "mle_q8_0_embedding", "mle_argmax_f32", "mle_swiglu_f32", "mle_last_error",
+            "mle_q8_0_bytes", "mle_q8_0_f16_decode")
 
 
 class Q8_0Error(RuntimeError):
@@ -63,6 +63,8 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_matmul.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_q8_0_embedding.restype = _i
     lib.mle_q8_0_embedding.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_swiglu_f32.restype = _i
+    lib.mle_swiglu_f32.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp]
     lib.mle_argmax_f32.restype = _i
     lib.mle_argmax_f32.argtypes = [_vp, _i, _i, _vp, _vp, _vp]
     lib.mle_last_error.restype = ctypes.c_char_p
@@ -184,6 +186,16 @@ def embedding_status(w, ids, out, seq_len, vocab, hidden, stream=None):
 def embedding(w, ids, out, seq_len, vocab, hidden, stream=None) -> None:
     """out[s,h] = dequantised row ids[s] of a raw Q8_0 [vocab, hidden] table."""
     _raise(embedding_status(w, ids, out, seq_len, vocab, hidden, stream)[0])
+
+
+def swiglu_status(gate, up, y, n, stream=None):
+    rc = load().mle_swiglu_f32(_addr(gate), _addr(up), _addr(y), n, _stream(stream))
+    return _status(rc)
+
+
+def swiglu(gate, up, y, n, stream=None) -> None:
+    """y[i] = silu(gate[i]) * up[i] for n fp32 elements."""
+    _raise(swiglu_status(gate, up, y, n, stream)[0])
 
 
 def argmax_status(logits, rows, n, idx, val=None, stream=None):

@@ -358,6 +358,17 @@ int mle_q8_0_linear_multi(const float* x, int count, const uint8_t* const* w,
   return run_segs(ctx, x, s, M, K, stream);
 }
 
+int mle_swiglu_f32(const float* gate, const float* up, float* y, int64_t n,
+                   hipStream_t stream) {
+  const char* ctx = "swiglu_f32";
+  MLE_TRY(check_ptrs(ctx, gate, "gate", up, "up", y, "output"));
+  if (n < 0) return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": n must be >= 0");
+  MLE_TRY(check_align(ctx, gate, 4, "gate"));
+  MLE_TRY(check_align(ctx, up, 4, "up"));
+  MLE_TRY(check_align(ctx, y, 4, "output"));
+  return check_launch(mle::launch_swiglu(gate, up, y, n, stream), "hip swiglu launch failed");
+}
+
 int mle_argmax_f32(const float* logits, int rows, int n, int32_t* idx, float* val,
                    hipStream_t stream) {
   const char* ctx = "argmax_f32";

@@ -206,6 +206,34 @@ expected<ValueId, Status> GraphBuilder::constant(std::string name, Shape shape, 
                           ValueKind::Constant);
 }
 
+expected<Shape, Status> infer_elementwise_shape(const Shape& a, const Shape& b) {
+  if (a.rank() != b.rank())
+    return unexpected(Status::shape_mismatch("Elementwise op requires same rank: " +
+                                             a.to_string() + " vs " + b.to_string()));
+  for (size_t i = 0; i < a.rank(); ++i) {
+    const int64_t da = a.dim(i), db = b.dim(i);
+    if (da >= 0 && db >= 0 && da != db)
+      return unexpected(Status::shape_mismatch("Elementwise dim mismatch at axis " +
+                                               std::to_string(i) + ": " + a.to_string() +
+                                               " vs " + b.to_string()));
+  }
+  return a;
+}
+
+expected<ValueId, Status> GraphBuilder::swiglu(ValueId gate, ValueId up, std::string name) {
+  auto gv = graph_.value(gate);
+  if (!gv) return unexpected(gv.error());
+  auto uv = graph_.value(up);
+  if (!uv) return unexpected(uv.error());
+  auto shape = infer_elementwise_shape((*gv)->shape, (*uv)->shape);
+  if (!shape) return unexpected(shape.error());
+  auto out = make_intermediate(name + ".out", std::move(*shape), (*gv)->dtype, (*gv)->device);
+  if (!out) return out;
+  auto nid = graph_.add_node(OpType::SwiGLU, std::move(name), {gate, up}, {*out});
+  if (!nid) return unexpected(nid.error());
+  return out;
+}
+
 expected<ValueId, Status> GraphBuilder::embedding(ValueId input_ids, ValueId weight,
                                                   std::string name) {
   auto iv = graph_.value(input_ids);

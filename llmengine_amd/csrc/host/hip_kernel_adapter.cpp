@@ -11,6 +11,7 @@
 #include <string>
 #include <string_view>
 
+#include "fusion.hpp"
 #include "mle_q8_0.h"
 #include "minillm_hip/runtime.h"
 
@@ -195,6 +196,93 @@ Status kernel_linear(const Node& node, RuntimeContext& ctx) {
                        static_cast<float*>((*ot)->data()), *M, *N, *K, bias, ctx.hip_stream());
 }
 
+Status kernel_swiglu(const Node& node, RuntimeContext& ctx) {
+  if (node.inputs().size() < 2 || node.outputs().empty())
+    return Status::invalid_argument("SwiGLU expects inputs [gate, up] and one output");
+  auto gt = get_tensor(node.inputs()[0], ctx, "gate");
+  if (!gt) return gt.error();
+  auto ut = get_tensor(node.inputs()[1], ctx, "up");
+  if (!ut) return ut.error();
+  auto ot = get_tensor(node.outputs()[0], ctx, "output");
+  if (!ot) return ot.error();
+  TRY(check_hip_float(*gt, "gate"));
+  TRY(check_hip_float(*ut, "up"));
+  TRY(check_hip_float(*ot, "output"));
+  auto n = (*ot)->numel();
+  if (!n) return n.error();
+  TRY(check_storage_bytes(*gt, *n * 4, "gate"));
+  TRY(check_storage_bytes(*ut, *n * 4, "up"));
+  TRY(check_storage_bytes(*ot, *n * 4, "output"));
+  return from_capi(mle_swiglu_f32(static_cast<const float*>((*gt)->data()),
+                                  static_cast<const float*>((*ut)->data()),
+                                  static_cast<float*>((*ot)->data()), (int64_t)*n,
+                                  ctx.hip_stream()));
+}
+
+// Operands of one Q8_0 Linear node, validated as kernel_linear validates them.
+struct LinearOperands {
+  const float* x = nullptr;
+  const uint8_t* w = nullptr;
+  const float* bias = nullptr;
+  float* y = nullptr;
+  int M = 0, N = 0, K = 0;
+  ValueId x_id;
+};
+
+expected<LinearOperands, Status> linear_operands(const Node& node, RuntimeContext& ctx) {
+  if (node.op_type() != OpType::Linear || node.inputs().size() < 2 || node.outputs().empty())
+    return unexpected(Status::invalid_argument("not a Linear node"));
+  auto xt = get_tensor(node.inputs()[0], ctx, "x");
+  if (!xt) return unexpected(xt.error());
+  auto wt = get_tensor(node.inputs()[1], ctx, "weight");
+  if (!wt) return unexpected(wt.error());
+  auto ot = get_tensor(node.outputs()[0], ctx, "output");
+  if (!ot) return unexpected(ot.error());
+  Status st = check_hip_float(*xt, "x");
+  if (st.ok()) st = check_hip_q8_weight(*wt, "weight");
+  if (st.ok()) st = check_hip_float(*ot, "output");
+  if (!st.ok()) return unexpected(st);
+  if ((*wt)->shape().rank() != 2 || (*xt)->shape().rank() == 0)
+    return unexpected(Status::shape_mismatch("Linear operand ranks"));
+  size_t rows = 1;
+  for (size_t i = 0; i + 1 < (*xt)->shape().rank(); ++i)
+    rows *= static_cast<size_t>((*xt)->shape().dim(i));
+  auto M = checked_count(rows, "linear x");
+  auto K = checked_dim((*xt)->shape().dim((*xt)->shape().rank() - 1), "linear x");
+  auto N = checked_dim((*wt)->shape().dim(0), "linear output");
+  auto wk = checked_dim((*wt)->shape().dim(1), "linear weight input");
+  if (!M || !K || !N || !wk || *wk != *K)
+    return unexpected(Status::shape_mismatch("Linear operand shapes"));
+  LinearOperands o;
+  if (node.inputs().size() >= 3) {
+    auto bt = get_tensor(node.inputs()[2], ctx, "bias");
+    if (!bt) return unexpected(bt.error());
+    st = check_hip_float(*bt, "bias");
+    if (!st.ok()) return unexpected(st);
+    if ((*bt)->shape().rank() != 1 || (*bt)->shape().dim(0) != *N)
+      return unexpected(Status::shape_mismatch("Linear bias shape must match output features"));
+    st = check_storage_bytes(*bt, static_cast<size_t>(*N) * 4, "bias");
+    if (!st.ok()) return unexpected(st);
+    o.bias = static_cast<const float*>((*bt)->data());
+  }
+  st = check_q8_block_aligned(*K, "linear");
+  if (st.ok()) st = check_q8_storage_bytes(*wt, "linear weight");
+  if (st.ok())
+    st = check_storage_bytes(*xt, static_cast<size_t>(*M) * static_cast<size_t>(*K) * 4, "x");
+  if (st.ok())
+    st = check_storage_bytes(*ot, static_cast<size_t>(*M) * static_cast<size_t>(*N) * 4,
+                             "output");
+  if (!st.ok()) return unexpected(st);
+  o.x = static_cast<const float*>((*xt)->data());
+  o.w = static_cast<const uint8_t*>((*wt)->data());
+  o.y = static_cast<float*>((*ot)->data());
+  o.M = *M;
+  o.N = *N;
+  o.K = *K;
+  o.x_id = node.inputs()[0];
+  return o;
+}
+
 Status kernel_matmul(const Node& node, RuntimeContext& ctx) {
   if (node.inputs().size() < 2 || node.outputs().empty())
     return Status::invalid_argument("MatMul expects inputs [a, b] and one output");
@@ -267,10 +355,56 @@ Status argmax(const float* logits, int rows, int n, int32_t* idx, float* val,
 
 }  // namespace hip
 
+namespace detail {
+
+expected<bool, Status> run_fused_swiglu(const Node& gate, const Node& up, const Node& sw,
+                                        RuntimeContext& ctx) {
+  auto g = linear_operands(gate, ctx);
+  auto u = linear_operands(up, ctx);
+  if (!g || !u || g->bias || u->bias || g->x != u->x || g->M != u->M || g->N != u->N ||
+      g->K != u->K || sw.outputs().empty())
+    return false;
+  Tensor* ot = ctx.get(sw.outputs()[0]);
+  if (!ot || !check_hip_float(ot, "output").ok() ||
+      !check_storage_bytes(ot, static_cast<size_t>(g->M) * g->N * 4, "output").ok())
+    return false;
+  const Status st = hip::linear_swiglu(g->x, g->w, u->w, static_cast<float*>(ot->data()), g->M,
+                                       g->N, g->K, ctx.hip_stream());
+  if (!st.ok()) return unexpected(st);
+  return true;
+}
+
+expected<bool, Status> run_fused_multi(const std::vector<const Node*>& nodes,
+                                       RuntimeContext& ctx) {
+  if (nodes.size() < 2 || nodes.size() > 3) return false;
+  const uint8_t* w[3];
+  const float* b[3];
+  float* y[3];
+  int N[3];
+  LinearOperands first;
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    auto o = linear_operands(*nodes[i], ctx);
+    if (!o) return false;
+    if (i == 0) first = *o;
+    else if (o->x != first.x || o->M != first.M || o->K != first.K) return false;
+    w[i] = o->w;
+    b[i] = o->bias;
+    y[i] = o->y;
+    N[i] = o->N;
+  }
+  const Status st = hip::linear_multi(first.x, static_cast<int>(nodes.size()), w, b, y, N,
+                                      first.M, first.K, ctx.hip_stream());
+  if (!st.ok()) return unexpected(st);
+  return true;
+}
+
+}  // namespace detail
+
 void register_hip_kernels(KernelRegistry& registry) {
   registry.register_kernel(DeviceType::HIP, OpType::Embedding, kernel_embedding);
   registry.register_kernel(DeviceType::HIP, OpType::Linear, kernel_linear);
   registry.register_kernel(DeviceType::HIP, OpType::MatMul, kernel_matmul);
+  registry.register_kernel(DeviceType::HIP, OpType::SwiGLU, kernel_swiglu);
 }
 
 }  // namespace minillm

@@ -2,6 +2,12 @@
 // (see include/minillm_hip/runtime.h).
 #include "minillm_hip/runtime.h"
 
+#include <map>
+#include <unordered_map>
+#include <unordered_set>
+
+#include "fusion.hpp"
+
 namespace minillm {
 
 // ---------------------------------------------------------------- registry
@@ -51,7 +57,7 @@ bool Backend::supports(OpType op) const {
 
 bool HipBackend::supports(OpType op) const {
   return op == OpType::Embedding || op == OpType::MatMul || op == OpType::Linear ||
-         op == OpType::Output;
+         op == OpType::SwiGLU || op == OpType::Output;
 }
 
 // ---------------------------------------------------------------- context
@@ -126,13 +132,87 @@ Status HipExecutor::compile(const Graph& graph) {
   }
   graph_ = &graph;
   execution_order_ = std::move(*order);
+
+  // Fusion plan over the topological order.
+  plan_.clear();
+  std::unordered_map<size_t, int> uses;          // value -> consuming nodes
+  std::unordered_map<size_t, size_t> producer;   // value -> node index
+  for (const Node& n : graph.nodes()) {
+    for (const ValueId& v : n.inputs()) ++uses[v.value];
+    for (const ValueId& v : n.outputs()) producer[v.value] = n.id().value;
+  }
+  auto node_of = [&](size_t id) -> const Node* {
+    auto nd = graph.node(NodeId{id});
+    return nd ? *nd : nullptr;
+  };
+  auto value_kind = [&](ValueId v) {
+    auto val = graph.value(v);
+    return val ? (*val)->kind : ValueKind::Intermediate;
+  };
+  std::unordered_set<size_t> taken;
+  std::unordered_map<size_t, std::vector<NodeId>> anchor;  // node -> fused group it starts
+  std::unordered_map<size_t, Step::Kind> anchor_kind;
+  if (fusion_) {
+    for (const NodeId& nid : execution_order_) {
+      const Node* sw = node_of(nid.value);
+      if (!sw || sw->op_type() != OpType::SwiGLU || sw->inputs().size() != 2) continue;
+      const ValueId g = sw->inputs()[0], u = sw->inputs()[1];
+      if (!producer.count(g.value) || !producer.count(u.value)) continue;
+      const Node* pg = node_of(producer[g.value]);
+      const Node* pu = node_of(producer[u.value]);
+      if (!pg || !pu || pg == pu || pg->op_type() != OpType::Linear ||
+          pu->op_type() != OpType::Linear || pg->inputs().size() != 2 ||
+          pu->inputs().size() != 2 || !(pg->inputs()[0] == pu->inputs()[0]))
+        continue;
+      if (uses[g.value] != 1 || uses[u.value] != 1 || value_kind(g) == ValueKind::Output ||
+          value_kind(u) == ValueKind::Output)
+        continue;
+      if (taken.count(pg->id().value) || taken.count(pu->id().value)) continue;
+      taken.insert({pg->id().value, pu->id().value, nid.value});
+      anchor[nid.value] = {pg->id(), pu->id(), nid};
+      anchor_kind[nid.value] = Step::kSwiGLU;
+    }
+    // Sibling Linears on one input whose other inputs are constants / inputs.
+    std::map<size_t, std::vector<NodeId>> by_input;
+    for (const NodeId& nid : execution_order_) {
+      const Node* n = node_of(nid.value);
+      if (!n || n->op_type() != OpType::Linear || taken.count(nid.value)) continue;
+      bool ok = true;
+      for (size_t i = 1; i < n->inputs().size(); ++i) {
+        const ValueKind k = value_kind(n->inputs()[i]);
+        ok = ok && (k == ValueKind::Constant || k == ValueKind::Input);
+      }
+      if (ok) by_input[n->inputs()[0].value].push_back(nid);
+    }
+    for (auto& [x, ids] : by_input) {
+      (void)x;
+      for (size_t i = 0; i + 1 < ids.size(); i += 3) {
+        std::vector<NodeId> group(ids.begin() + i, ids.begin() + std::min(ids.size(), i + 3));
+        for (const NodeId& m : group) taken.insert(m.value);
+        anchor[group[0].value] = group;
+        anchor_kind[group[0].value] = Step::kMulti;
+      }
+    }
+  }
+  for (const NodeId& nid : execution_order_) {
+    auto a = anchor.find(nid.value);
+    if (a != anchor.end()) {
+      plan_.push_back(Step{anchor_kind[nid.value], a->second});
+    } else if (!taken.count(nid.value)) {
+      plan_.push_back(Step{Step::kNode, {nid}});
+    }
+  }
   return Status::make_ok();
 }
 
-Status HipExecutor::run(RuntimeContext& ctx) {
-  if (!graph_) return Status::runtime_error("executor not compiled");
-  ctx.set_hip_stream(stream_);
-  for (const NodeId& nid : execution_order_) {
+size_t HipExecutor::fused_groups() const {
+  size_t n = 0;
+  for (const Step& s : plan_) n += s.kind != Step::kNode;
+  return n;
+}
+
+Status HipExecutor::run_nodes(const std::vector<NodeId>& ids, RuntimeContext& ctx) {
+  for (const NodeId& nid : ids) {
     auto nd = graph_->node(nid);
     if (!nd) return nd.error();
     const OpType op = (*nd)->op_type();
@@ -144,6 +224,42 @@ Status HipExecutor::run(RuntimeContext& ctx) {
       return Status::runtime_error("HIP kernel " + std::string(op_type_name(op)) +
                                    " failed for node #" + std::to_string(nid.value) + " (" +
                                    std::string((*nd)->name()) + "): " + st.to_string());
+  }
+  return Status::make_ok();
+}
+
+Status HipExecutor::run(RuntimeContext& ctx) {
+  if (!graph_) return Status::runtime_error("executor not compiled");
+  ctx.set_hip_stream(stream_);
+  fused_launches_ = 0;
+  for (const Step& step : plan_) {
+    if (step.kind != Step::kNode) {
+      std::vector<const Node*> nodes;
+      for (const NodeId& nid : step.nodes) {
+        auto nd = graph_->node(nid);
+        if (!nd) return nd.error();
+        nodes.push_back(*nd);
+      }
+      auto done = step.kind == Step::kSwiGLU
+                      ? detail::run_fused_swiglu(*nodes[0], *nodes[1], *nodes[2], ctx)
+                      : detail::run_fused_multi(nodes, ctx);
+      if (!done) {
+        std::string ids;
+        for (const Node* n : nodes)
+          ids += (ids.empty() ? "#" : ", #") + std::to_string(n->id().value) + " (" +
+                 std::string(n->name()) + ")";
+        return Status::runtime_error(std::string("HIP fused ") +
+                                     (step.kind == Step::kSwiGLU ? "Linear+Linear+SwiGLU"
+                                                                 : "multi-output Linear") +
+                                     " failed for nodes " + ids + ": " +
+                                     done.error().to_string());
+      }
+      if (*done) {
+        ++fused_launches_;
+        continue;
+      }
+    }
+    TRY(run_nodes(step.nodes, ctx));
   }
   const Status st = ctx.advance_kv_cache_step();
   if (!st.ok()) return Status::runtime_error("KV cache advance failed: " + st.to_string());

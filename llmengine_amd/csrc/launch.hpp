@@ -109,6 +109,10 @@ int argmax_chunks(int64_t n);
 hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* idx, float* val,
                          uint64_t* keys, hipStream_t stream);
 
+// y = silu(g) * u over n fp32 elements.
+hipError_t launch_swiglu(const float* g, const float* u, float* y, int64_t n,
+                         hipStream_t stream);
+
 // Embedding gather-dequantise; ids outside [0, vocab) give rows of +0.0f.
 hipError_t launch_embedding(const uint8_t* w, const int32_t* ids, float* out,
                             int64_t seq_len, int vocab, int hidden,

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "gguf_writer.h"
+#include "mle_q8_0.h"
 #include "minillm_hip/io.h"
 #include "minillm_hip/runtime.h"
 
@@ -39,6 +40,10 @@ static void check_hip(hipError_t e) {
     std::fprintf(stderr, "HIP error: %s\n", hipGetErrorString(e));
     std::abort();
   }
+}
+
+static Status from_hip(int rc) {
+  return rc == 0 ? Status::make_ok() : Status::runtime_error(mle_last_error());
 }
 
 static void check_status(const Status& st) {
@@ -634,6 +639,102 @@ static void test_fused_launchers() {
   std::printf("  PASS test_fused_launchers\n");
 }
 
+static void test_executor_fusion_end_to_end() {
+  // x -> {gate, up} -> SwiGLU -> down, plus q / k / v on x; the fused executor
+  // against the unfused one (bitwise for M < 64, the same kernels' arithmetic;
+  // within 1e-5 of each other at M = 70, where split choices may differ).
+  const int K = 128, I = 96, Q = 64, KV = 32;
+  std::vector<std::vector<uint8_t>> w;
+  const int rows[6] = {I, I, K, Q, KV, KV};
+  const int cols[6] = {K, K, I, K, K, K};
+  for (int i = 0; i < 6; ++i) w.push_back(synth_q8(rows[i], cols[i], 40 + i));
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  for (int M : {5, 70}) {
+    std::vector<float> hx(size_t(M) * K);
+    for (size_t i = 0; i < hx.size(); ++i) hx[i] = float(int(i * 37 % 101) - 50) * 0.02f;
+    std::vector<std::vector<float>> outs[2];
+    for (int fuse = 0; fuse < 2; ++fuse) {
+      Graph g;
+      GraphBuilder gb(g);
+      const Device dev = Device::hip(0);
+      auto x = gb.input("x", Shape({M, K}), DType::Float32, dev);
+      CHECK(x);
+      std::vector<ValueId> cw;
+      const char* names[6] = {"wg", "wu", "wd", "wq", "wk", "wv"};
+      for (int i = 0; i < 6; ++i) {
+        auto c = gb.constant(names[i], Shape({rows[i], cols[i]}), DType::Float32, dev);
+        CHECK(c);
+        cw.push_back(*c);
+      }
+      auto gate = gb.linear(*x, cw[0], std::nullopt, "gate");
+      auto up = gb.linear(*x, cw[1], std::nullopt, "up");
+      CHECK(gate && up);
+      auto act = gb.swiglu(*gate, *up, "swiglu");
+      CHECK(act);
+      auto down = gb.linear(*act, cw[2], std::nullopt, "down");
+      auto q = gb.linear(*x, cw[3], std::nullopt, "q");
+      auto k = gb.linear(*x, cw[4], std::nullopt, "k");
+      auto v = gb.linear(*x, cw[5], std::nullopt, "v");
+      CHECK(down && q && k && v);
+      CHECK(gb.output(*down, "o_down") && gb.output(*q, "o_q") && gb.output(*k, "o_k") &&
+            gb.output(*v, "o_v"));
+      std::vector<std::unique_ptr<Tensor>> tw;
+      RuntimeContext ctx;
+      for (int i = 0; i < 6; ++i) {
+        tw.push_back(std::make_unique<Tensor>(names[i], Shape({rows[i], cols[i]}), DType::Q8_0,
+                                              dev));
+        check_status(tw.back()->allocate_hip_bytes(w[i].size()));
+        upload(*tw.back(), w[i].data(), w[i].size());
+        check_status(ctx.bind(cw[i], tw.back().get()));
+      }
+      Tensor tx("x", Shape({M, K}), DType::Float32, dev);
+      check_status(tx.allocate_hip());
+      upload(tx, hx.data(), hx.size() * 4);
+      check_status(ctx.bind(*x, &tx));
+      check_status(ctx.allocate_intermediates(g));
+      HipExecutor ex(std::make_shared<HipBackend>(), registry);
+      ex.set_fusion(fuse == 1);
+      check_status(ex.compile(g));
+      check_status(ex.run(ctx));
+      check_hip(hipDeviceSynchronize());
+      CHECK(ex.fused_launches() == (fuse ? 2u : 0u));
+      outs[fuse] = {download(ctx.get(*down), size_t(M) * K), download(ctx.get(*q), size_t(M) * Q),
+                    download(ctx.get(*k), size_t(M) * KV), download(ctx.get(*v), size_t(M) * KV)};
+    }
+    for (int o = 0; o < 4; ++o) {
+      const auto& a = outs[0][o];
+      const auto& b = outs[1][o];
+      double num = 0, den = 0;
+      for (size_t i = 0; i < a.size(); ++i) {
+        num += double(a[i] - b[i]) * (a[i] - b[i]);
+        den += double(a[i]) * a[i];
+      }
+      if (M < 64) CHECK(std::memcmp(a.data(), b.data(), a.size() * 4) == 0);
+      else CHECK(std::sqrt(num / den) <= 1e-5);
+    }
+  }
+  // The unfused SwiGLU op on its own: silu(g) * u in the reference's order.
+  {
+    const int n = 1001;
+    std::vector<float> hg(n), hu(n);
+    for (int i = 0; i < n; ++i) {
+      hg[i] = float(i - 500) * 0.013f;
+      hu[i] = float((i * 7) % 23 - 11) * 0.25f;
+    }
+    DevBuf<float> dg(n), du(n), dy(n);
+    dg.put(hg);
+    du.put(hu);
+    check_status(from_hip(mle_swiglu_f32(dg.p, du.p, dy.p, n, nullptr)));
+    const auto hy = dy.get();
+    for (int i = 0; i < n; ++i) {
+      const double want = double(hg[i]) / (1.0 + std::exp(-double(hg[i]))) * hu[i];
+      near(hy[i], float(want), 2e-6f * float(std::fabs(want)) + 1e-7f);
+    }
+  }
+  std::printf("  PASS test_executor_fusion_end_to_end\n");
+}
+
 int main() {
   int count = 0;
   check_hip(hipGetDeviceCount(&count));
@@ -648,6 +749,7 @@ int main() {
   test_executor_prefill_linear();
   test_gguf_model_end_to_end();
   test_fused_launchers();
+  test_executor_fusion_end_to_end();
   std::printf("test_hip_q8_0: all passed\n");
   return 0;
 }

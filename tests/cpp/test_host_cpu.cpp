@@ -424,6 +424,56 @@ static void test_gguf_parse_and_host_load() {
   std::printf("  PASS test_gguf_parse_and_host_load\n");
 }
 
+static void test_executor_fusion_plan() {
+  // x -> {gate, up} -> SwiGLU -> down, and q / k / v on x: one fused SwiGLU
+  // group and one multi-output group; with the gate value also a graph output
+  // the SwiGLU cannot fuse and the five sibling Linears group as 3 + 2.
+  for (int variant = 0; variant < 3; ++variant) {
+    Graph g;
+    GraphBuilder gb(g);
+    const Device dev = Device::hip(0);
+    auto x = gb.input("x", Shape({4, 64}), DType::Float32, dev);
+    auto wg = gb.constant("wg", Shape({96, 64}), DType::Float32, dev);
+    auto wu = gb.constant("wu", Shape({96, 64}), DType::Float32, dev);
+    auto wd = gb.constant("wd", Shape({64, 96}), DType::Float32, dev);
+    auto wq = gb.constant("wq", Shape({64, 64}), DType::Float32, dev);
+    auto wk = gb.constant("wk", Shape({32, 64}), DType::Float32, dev);
+    auto wv = gb.constant("wv", Shape({32, 64}), DType::Float32, dev);
+    CHECK(x && wg && wu && wd && wq && wk && wv);
+    auto gate = gb.linear(*x, *wg, std::nullopt, "gate");
+    auto up = gb.linear(*x, *wu, std::nullopt, "up");
+    CHECK(gate && up);
+    auto act = gb.swiglu(*gate, *up, "swiglu");
+    CHECK(act);
+    auto down = gb.linear(*act, *wd, std::nullopt, "down");
+    auto q = gb.linear(*x, *wq, std::nullopt, "q");
+    auto k = gb.linear(*x, *wk, std::nullopt, "k");
+    auto v = gb.linear(*x, *wv, std::nullopt, "v");
+    CHECK(down && q && k && v);
+    CHECK(gb.output(*down, "o1") && gb.output(*q, "o2") && gb.output(*k, "o3") &&
+          gb.output(*v, "o4"));
+    if (variant == 1) CHECK(gb.output(*gate, "o5"));
+    KernelRegistry reg;
+    register_hip_kernels(reg);
+    HipExecutor ex(std::make_shared<HipBackend>(), reg);
+    if (variant == 2) ex.set_fusion(false);
+    CHECK(ex.compile(g).ok());
+    if (variant == 0) CHECK(ex.fused_groups() == 2);
+    if (variant == 1) CHECK(ex.fused_groups() == 2);  // {gate, up, q}, {k, v}: no SwiGLU group
+    if (variant == 2) CHECK(ex.fused_groups() == 0);
+  }
+  {  // shape rule of the SwiGLU builder
+    Graph g;
+    GraphBuilder gb(g);
+    auto a = gb.input("a", Shape({2, 8}), DType::Float32);
+    auto b = gb.input("b", Shape({2, 9}), DType::Float32);
+    CHECK(a && b);
+    auto r = gb.swiglu(*a, *b, "bad");
+    CHECK(!r && r.error().code() == ErrorCode::ShapeMismatch);
+  }
+  std::printf("  PASS test_executor_fusion_plan\n");
+}
+
 int main() {
   std::printf("test_host_cpu:\n");
   test_core_types();
@@ -432,6 +482,7 @@ int main() {
   test_linear_validation();
   test_matmul_and_embedding_validation();
   test_gguf_parse_and_host_load();
+  test_executor_fusion_plan();
   std::printf("test_host_cpu: all passed\n");
   return 0;
 }

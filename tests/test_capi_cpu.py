@@ -88,6 +88,16 @@ def test_fused_linear_validation_errors():
     assert rc == 1 and "arrays must not be null" in capi.last_error()
 
 
+def test_swiglu_validation_errors():
+    st = capi.swiglu_status
+    code, msg = st(None, FAKE, FAKE, 8, stream=0)
+    assert code == 1 and "gate pointer" in msg
+    code, msg = st(FAKE, FAKE, FAKE, -1, stream=0)
+    assert code == 1 and "n must be >= 0" in msg
+    code, msg = st(FAKE, FAKE + 2, FAKE, 8, stream=0)
+    assert code == 1 and "up must be 4-byte aligned" in msg
+
+
 def test_argmax_validation_errors():
     st = capi.argmax_status
     code, msg = st(None, 1, 10, FAKE, stream=0)
