@@ -144,10 +144,12 @@ int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWo
 // Linear path numbers (mle_q8_0_linear_ex): 1 FP32 GEMV, 2 bf16-MFMA prefill GEMM,
 // 3 MFMA decode with FP32-exact activations.
 // The FP32 GEMV also wins for a few tokens on short rows (K <= 1024, e.g. the
-// 896-wide Qwen projections: 4.5-5.1 us vs 5.5-7.0 us at M = 2..4, MI355X).
-int pick_path(int M, int K) {
+// 896-wide Qwen projections: 4.5-5.1 us vs 5.5-7.0 us at M = 2..4, MI355X),
+// but not on a vocabulary-sized weight (the [151936, 896] lm_head at M = 4:
+// 50.9 us vs 34.5 us for the MFMA decode).
+int pick_path(int M, int N, int K) {
   if (M >= 64) return 2;
-  if (M == 1 || (M <= 4 && K <= 1024)) return 1;
+  if (M == 1 || (M <= 4 && K <= 1024 && N <= 32768)) return 1;
   return 3;
 }
 
@@ -160,7 +162,7 @@ struct Tune {
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
                int N, int K, int path, const Tune& tune, hipStream_t stream) {
   if (path == 0) {
-    path = pick_path(M, K);
+    path = pick_path(M, N, K);
     if (path == 3 && !mle::decode_mfma_fits(mle::decode_mfma_pick(M < 16 ? M : 16, N, K),
                                             M < 16 ? M : 16, N, K))
       path = 1;
@@ -239,7 +241,7 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
     return check_launch(mle::launch_gemm_mfma_segs(c, x, s, M, K, ws, stream),
                         "hip Q8_0 fused Linear launch failed");
   }
-  if (swi ? M == 1 : pick_path(M, K) == 1) {
+  if (swi ? M == 1 : pick_path(M, total_n, K) == 1) {
     const mle::GemvConfig c = mle::gemv_pick_config(M, total_n, K);
     return check_launch(mle::launch_gemv_segs(c, x, s, M, K, stream),
                         "hip Q8_0 fused Linear launch failed");
