@@ -19,8 +19,9 @@ Also reported: per-launch kernel durations (HIP events on the launch stream, >= 
 launches each), the roofline of the dominant launch, the prefill GEMM of configs[2]
 (M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding gather of configs[4], the fused
 Linear entry points (gate/up + SwiGLU, q/k/v multi-output) against their unfused launches,
-the device argmax of an lm_head logits row against copying the row to the host, and the
-reference's own CPU kernels timed on this host (cpu_baseline).
+the device argmax of an lm_head logits row against copying the row to the host, the
+device top-n tokens with softmax probabilities (sampling candidates), and the reference's
+own CPU kernels timed on this host (cpu_baseline).
 """
 from __future__ import annotations
 
@@ -332,6 +333,18 @@ def main():
                             "us_copy_row_to_host": round(t_copy, 2),
                             "note": "the reference copies the logits row to the host per token "
                                     "and picks there; the device argmax returns 4 bytes"}
+        # ---- sampling candidates: device top-n tokens with softmax probabilities
+        tk = []
+        for rows, top_n in ((1, 40), (8, 40), (1, 128)):
+            lg = torch.from_numpy(S.activations(8, (rows, V))).to(dev)
+            tid = torch.empty((rows, top_n), dtype=torch.int32, device=dev)
+            tpr = torch.empty((rows, top_n), dtype=torch.float32, device=dev)
+            t_top = timed(lambda j: capi.top_tokens(lg, rows, V, top_n, tid, tpr, 0.8,
+                                                    stream=stream), 200)
+            tk.append({"rows": rows, "top_n": top_n, "us_device": round(t_top, 2)})
+        extras["top_tokens"] = {"vocab": V, "temperature": 0.8, "runs": tk,
+                                "note": "Sampler::get_top_tokens on the device (softmax + "
+                                        "top-n); the reference sorts the copied row on the host"}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(weights_host, xs_host)
 

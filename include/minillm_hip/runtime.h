@@ -168,6 +168,10 @@ Status linear_multi(const float* x, int count, const uint8_t* const* w_q8_0,
                     hipStream_t stream = nullptr);
 Status argmax(const float* logits, int rows, int n, int32_t* idx, float* val = nullptr,
               hipStream_t stream = nullptr);
+// Sampler::get_top_tokens (sampler.cpp:141-197) on the device: ids / probs
+// [rows][min(top_n, n)] of each logits row, largest probability first.
+Status top_tokens(const float* logits, int rows, int n, int top_n, float temperature,
+                  int32_t* ids, float* probs, hipStream_t stream = nullptr);
 }  // namespace hip
 
 }  // namespace minillm

@@ -155,6 +155,25 @@ int mle_argmax_f32(const float* logits, int rows, int n, int32_t* idx, float* va
                    hipStream_t stream);
 
 /*
+ * The top_n tokens of each logits row with their softmax probabilities, on the
+ * device: Sampler::get_top_tokens (src/runtime/sampler.cpp:141-197).  Row r of
+ * n logits is scaled by 1 / temperature when temperature > 0 and != 1, then
+ * p = exp(v - max) * (1 / sum); ids[r*k + j], probs[r*k + j] (k = min(top_n, n))
+ * are the top k tokens, largest probability first, ties to the lower index.  A
+ * row with a NaN, a non-finite maximum or a non-finite or zero sum gives the
+ * uniform 1/n (ids 0, 1, ...), as the reference does.  With the k candidates
+ * on the host, Sampler::sample's top-k / top-p / draw (:65-138) runs on k
+ * values instead of the whole row the reference's generator copies back
+ * (examples/generate_cuda.cpp:81-94).  Deterministic.
+ * Errors: NULL logits / ids / probs, rows or n <= 0 -> InvalidArgument;
+ * top_n <= 0 -> nothing written (the reference's empty list); rows > 65535,
+ * top_n > 128, or n > (16384 / k) * 2048 -> Unsupported.  Uses the
+ * per-(device, stream) workspace of the Linear calls.
+ */
+int mle_top_tokens_f32(const float* logits, int rows, int n, int top_n, float temperature,
+                       int32_t* ids, float* probs, hipStream_t stream);
+
+/*
  * Message of the last failed call on this thread ("" if none).  Stands in for
  * the message of the reference's Status return (status.h:34-59).  The pointer
  * stays valid until the next call on the same thread.

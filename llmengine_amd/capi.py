@@ -22,8 +22,8 @@ ERROR_NAMES = {0: "Ok", 1: "InvalidArgument", 2: "OutOfRange", 3: "ShapeMismatch
 
 EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_q8_0_linear_swiglu", "mle_q8_0_linear_multi", "mle_q8_0_matmul",
-            "mle_q8_0_embedding", "mle_argmax_f32", "mle_swiglu_f32", "mle_last_error",
-            "mle_q8_0_bytes", "mle_q8_0_f16_decode")
+            "mle_q8_0_embedding", "mle_argmax_f32", "mle_top_tokens_f32", "mle_swiglu_f32",
+            "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode")
 
 
 class Q8_0Error(RuntimeError):
@@ -67,6 +67,8 @@ def load() -> ctypes.CDLL:
     lib.mle_swiglu_f32.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp]
     lib.mle_argmax_f32.restype = _i
     lib.mle_argmax_f32.argtypes = [_vp, _i, _i, _vp, _vp, _vp]
+    lib.mle_top_tokens_f32.restype = _i
+    lib.mle_top_tokens_f32.argtypes = [_vp, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp]
     lib.mle_last_error.restype = ctypes.c_char_p
     lib.mle_last_error.argtypes = []
     lib.mle_q8_0_bytes.restype = ctypes.c_size_t
@@ -206,6 +208,18 @@ def argmax_status(logits, rows, n, idx, val=None, stream=None):
 def argmax(logits, rows, n, idx, val=None, stream=None) -> None:
     """idx[r] (int32) = first index of the maximum of logits row r; val[r] its value."""
     _raise(argmax_status(logits, rows, n, idx, val, stream)[0])
+
+
+def top_tokens_status(logits, rows, n, top_n, ids, probs, temperature=1.0, stream=None):
+    rc = load().mle_top_tokens_f32(_addr(logits), rows, n, top_n, float(temperature),
+                                   _addr(ids), _addr(probs), _stream(stream))
+    return _status(rc)
+
+
+def top_tokens(logits, rows, n, top_n, ids, probs, temperature=1.0, stream=None) -> None:
+    """ids/probs [rows, min(top_n, n)]: the top tokens of each logits row by softmax
+    probability (after 1/temperature), largest first (Sampler::get_top_tokens)."""
+    _raise(top_tokens_status(logits, rows, n, top_n, ids, probs, temperature, stream)[0])
 
 
 def f16_decode(bits, out, n, stream=None) -> None:

@@ -269,7 +269,7 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
 
 extern "C" {
 
-int mle_q8_0_abi_version(void) { return 3; }
+int mle_q8_0_abi_version(void) { return 4; }
 
 const char* mle_last_error(void) { return g_last_error.c_str(); }
 
@@ -389,6 +389,36 @@ int mle_argmax_f32(const float* logits, int rows, int n, int32_t* idx, float* va
   return check_launch(mle::launch_argmax(logits, rows, n, idx, val,
                                          reinterpret_cast<uint64_t*>(ws.partials), stream),
                       "hip argmax launch failed");
+}
+
+int mle_top_tokens_f32(const float* logits, int rows, int n, int top_n, float temperature,
+                       int32_t* ids, float* probs, hipStream_t stream) {
+  const char* ctx = "top_tokens_f32";
+  MLE_TRY(check_ptrs(ctx, logits, "logits", ids, "ids", probs, "probs"));
+  MLE_TRY(check_positive(ctx, rows, "rows"));
+  MLE_TRY(check_positive(ctx, n, "n"));
+  if (top_n <= 0) return ok();  // an empty list, as Sampler::get_top_tokens returns
+  if (rows > 65535)
+    return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": at most 65535 rows per call");
+  if (top_n > mle::kTopTokensMax)
+    return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": top_n must be at most " +
+                                     std::to_string(mle::kTopTokensMax) + ", got " +
+                                     std::to_string(top_n));
+  const int kk = top_n < n ? top_n : n;
+  if (n > mle::topk_max_n(kk))
+    return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": n must be at most " +
+                                     std::to_string(mle::topk_max_n(kk)) + " for top_n " +
+                                     std::to_string(kk));
+  MLE_TRY(check_align(ctx, logits, 4, "logits"));
+  MLE_TRY(check_align(ctx, ids, 4, "ids"));
+  MLE_TRY(check_align(ctx, probs, 4, "probs"));
+  mle::SplitKNeed need;
+  need.partial_floats = mle::top_tokens_workspace_floats(rows, n, top_n);
+  mle::SplitKWorkspace ws;
+  MLE_TRY(get_workspace(need, stream, &ws));
+  return check_launch(mle::launch_top_tokens(logits, rows, n, top_n, temperature, ids, probs,
+                                             ws.partials, stream),
+                      "hip top_tokens launch failed");
 }
 
 int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M, int N, int K,

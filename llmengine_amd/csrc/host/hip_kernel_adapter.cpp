@@ -353,6 +353,11 @@ Status argmax(const float* logits, int rows, int n, int32_t* idx, float* val,
   return from_capi(mle_argmax_f32(logits, rows, n, idx, val, stream));
 }
 
+Status top_tokens(const float* logits, int rows, int n, int top_n, float temperature,
+                  int32_t* ids, float* probs, hipStream_t stream) {
+  return from_capi(mle_top_tokens_f32(logits, rows, n, top_n, temperature, ids, probs, stream));
+}
+
 }  // namespace hip
 
 namespace detail {

@@ -109,6 +109,18 @@ int argmax_chunks(int64_t n);
 hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* idx, float* val,
                          uint64_t* keys, hipStream_t stream);
 
+// Top-n tokens of `rows` rows of n fp32 logits with their softmax
+// probabilities (temperature applied when > 0 and != 1): ids / probs are
+// [rows][min(top_n, n)], largest probability first, ties to the lower index;
+// `workspace` holds top_tokens_workspace_floats() floats.  Needs
+// 1 <= top_n <= kTopTokensMax and n <= topk_max_n(min(top_n, n)).
+constexpr int kTopTokensMax = 128;
+int topk_chunks(int64_t n);
+int topk_max_n(int k);
+size_t top_tokens_workspace_floats(int rows, int64_t n, int top_n);
+hipError_t launch_top_tokens(const float* x, int rows, int64_t n, int top_n, float temperature,
+                             int32_t* ids, float* probs, float* workspace, hipStream_t stream);
+
 // y = silu(g) * u over n fp32 elements.
 hipError_t launch_swiglu(const float* g, const float* u, float* y, int64_t n,
                          hipStream_t stream);

@@ -25,7 +25,7 @@ def declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     lib = capi.load()
-    assert lib.mle_q8_0_abi_version() == 3
+    assert lib.mle_q8_0_abi_version() == 4
     out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH],
                          stdout=subprocess.PIPE, text=True, check=True).stdout
     exported = set(re.findall(r" T (mle_\w+)", out))
@@ -96,6 +96,32 @@ def test_swiglu_validation_errors():
     assert code == 1 and "n must be >= 0" in msg
     code, msg = st(FAKE, FAKE + 2, FAKE, 8, stream=0)
     assert code == 1 and "up must be 4-byte aligned" in msg
+
+
+def test_top_tokens_validation_errors():
+    st = capi.top_tokens_status
+    code, msg = st(None, 1, 10, 5, FAKE, FAKE, stream=0)
+    assert code == 1 and "logits pointer" in msg
+    code, msg = st(FAKE, 1, 10, 5, None, FAKE, stream=0)
+    assert code == 1 and "ids pointer" in msg
+    code, msg = st(FAKE, 1, 10, 5, FAKE, None, stream=0)
+    assert code == 1 and "probs pointer" in msg
+    code, msg = st(FAKE, 0, 10, 5, FAKE, FAKE, stream=0)
+    assert code == 1 and "rows must be positive" in msg
+    code, msg = st(FAKE, 1, 0, 5, FAKE, FAKE, stream=0)
+    assert code == 1 and "n must be positive" in msg
+    # top_n <= 0: the reference returns an empty list; nothing is launched
+    assert st(FAKE, 1, 10, 0, FAKE, FAKE, stream=0)[0] == 0
+    assert st(FAKE, 1, 10, -3, FAKE, FAKE, stream=0)[0] == 0
+    code, msg = st(FAKE, 70000, 10, 5, FAKE, FAKE, stream=0)
+    assert code == 4 and "65535" in msg
+    code, msg = st(FAKE, 1, 1000, 129, FAKE, FAKE, stream=0)
+    assert code == 4 and "at most 128" in msg
+    # candidates of a row must fit one workgroup: n <= (16384 / k) * 2048
+    code, msg = st(FAKE, 1, 262145, 128, FAKE, FAKE, stream=0)
+    assert code == 4 and "at most 262144" in msg
+    code, msg = st(FAKE + 2, 1, 10, 5, FAKE, FAKE, stream=0)
+    assert code == 1 and "logits must be 4-byte aligned" in msg
 
 
 def test_argmax_validation_errors():
