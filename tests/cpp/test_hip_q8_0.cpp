@@ -12,6 +12,7 @@
 // to end: Embedding -> Linear -> Linear -> tied lm_head Linear.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -634,6 +635,39 @@ static void test_fused_launchers() {
     CHECK(ix[m] == best && vx[m] == g[m * N + best]);
   }
   CHECK(hip::argmax(dy.p, 0, N, di.p).code() == ErrorCode::InvalidArgument);
+  // Top tokens of the gate outputs (Sampler::get_top_tokens restated on the host:
+  // softmax after 1/temperature, probability order, ties to the lower index).
+  {
+    const int top = 7;
+    const float temp = 0.5f;
+    DevBuf<int32_t> tid(M * top);
+    DevBuf<float> tpr(M * top);
+    check_status(hip::top_tokens(dy.p, M, N, top, temp, tid.p, tpr.p));
+    const auto ti = tid.get();
+    const auto tp = tpr.get();
+    for (int m = 0; m < M; ++m) {
+      std::vector<float> v(N);
+      float mx = -INFINITY;
+      for (int n = 0; n < N; ++n) {
+        v[n] = g[m * N + n] * (1.0f / temp);
+        mx = std::max(mx, v[n]);
+      }
+      double sum = 0;
+      for (int n = 0; n < N; ++n) sum += std::exp(double(v[n] - mx));
+      std::vector<int> order(N);
+      for (int n = 0; n < N; ++n) order[n] = n;
+      std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return v[a] > v[b]; });
+      for (int j = 0; j < top; ++j) {
+        CHECK(ti[m * top + j] == order[j]);
+        const float want = float(std::exp(double(v[order[j]] - mx)) / sum);
+        near(tp[m * top + j], want, 1e-5f * want + 1e-7f);
+      }
+    }
+    CHECK(hip::top_tokens(dy.p, M, N, top, temp, nullptr, tpr.p).code() ==
+          ErrorCode::InvalidArgument);
+    CHECK(hip::top_tokens(dy.p, M, N, 129, temp, tid.p, tpr.p).code() ==
+          ErrorCode::Unsupported);
+  }
   CHECK(hip::linear_swiglu(dx.p, dg.p, nullptr, dy.p, M, N, K).code() ==
         ErrorCode::InvalidArgument);
   std::printf("  PASS test_fused_launchers\n");
