@@ -17,7 +17,8 @@ algorithmic bytes per launch = N*(K/32)*34 + 4*M*K + 4*M*N.
 
 Also reported: per-launch kernel durations (HIP events on the launch stream, >= 100
 launches each), the roofline of the dominant launch, the prefill GEMM of configs[2]
-(M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding gather of configs[4], the fused
+(M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding gather of configs[4], the
+Qwen-shaped decode Linears and lm_head of configs[3] (per launch), the fused
 Linear entry points (gate/up + SwiGLU, q/k/v multi-output) against their unfused launches,
 the device argmax of an lm_head logits row against copying the row to the host, the
 device top-n tokens with softmax probabilities (sampling candidates), and the reference's
@@ -269,6 +270,34 @@ def main():
                                "GBps": round(eb / us / 1e3, 1),
                                "frac_hbm": round(eb / us / 1e3 / HBM_PEAK_GBS, 4)}
         del tbls
+        # ---- Qwen2.5-0.5B-shaped decode Linears at M = 1 and the tied
+        # lm_head at M = 1 and 8 (weights rotated over >= 1 GiB; small ones are
+        # latency-bound, so wall-clock per launch is the figure)
+        qwen = []
+        for name, N, K, Ms in (("qkv", 1152, 896, (1,)), ("gate", 4864, 896, (1,)),
+                               ("up", 4864, 896, (1,)), ("down", 896, 4864, (1,)),
+                               ("lm_head", 151936, 896, (1, 8))):
+            wq = torch.from_numpy(S.q8_0_weight(3000 + N, N, K)[0]).to(dev)
+            Rq = max(2, -(-ROTATE_BYTES // wq.numel()) + 1)
+            wqs = [wq] + [wq.clone() for _ in range(Rq - 1)]
+            for M in Ms:
+                x = torch.from_numpy(S.activations(3100 + K, (M, K))).to(dev)
+                y = torch.empty((M, N), dtype=torch.float32, device=dev)
+                for j in range(3):
+                    capi.linear(x, wqs[j % Rq], None, y, M, N, K, stream=stream)
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                iters = 100
+                a.record(stream)
+                for j in range(iters):
+                    capi.linear(x, wqs[j % Rq], None, y, M, N, K, stream=stream)
+                b.record(stream)
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / iters
+                gb = gemv_bytes(M, N, K) / us / 1e3
+                qwen.append({"op": name, "M": M, "N": N, "K": K, "us": round(us, 2),
+                             "GBps": round(gb, 1), "frac_hbm": round(gb / HBM_PEAK_GBS, 4)})
+            del wqs
+        extras["qwen_lm_head"] = qwen
 
         def timed(fn, iters):
             for j in range(3):
