@@ -588,13 +588,14 @@ int decode_mfma_tile(int M) {
 DecodeMfmaConfig decode_mfma_pick(int M, int N, int K) {
   // Measured on MI355X over the BASELINE decode shapes: 16-block K slices
   // (one-shot workgroups of ~35 KB) beat 32 unless K fits one 32-block slice
-  // (no split-K hand-off at all); 8 waves per workgroup pay off for 8+ tokens
-  // on wide weights, 4 otherwise.
+  // (no split-K hand-off at all); 8 waves per workgroup pay off for 4+ tokens
+  // on wide weights (qkv / gate at M = 4: 16.9 / 16.4 us vs 18.4 / 17.6 with 4
+  // waves), 4 otherwise.
   DecodeMfmaConfig c;
   c.mt = decode_mfma_tile(M);
   const int KB = K / kBlockElems;
   c.kslice = (c.mt <= 8 && KB <= 32) ? 32 : 16;
-  c.waves = (c.mt >= 8 && N >= 8192) ? 8 : 4;
+  c.waves = (c.mt >= 4 && N >= 8192) ? 8 : 4;
   return c;
 }
 
