@@ -48,8 +48,9 @@ SEED_W = {"qkv": 21, "o_proj": 22, "gate": 23, "up": 24, "down": 25}
 
 # HBM bytes per dispatch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on
 # `bench.py --profile-kernel M,N,K` (FETCH_SIZE scaled by a device copy's read/write
-# ratio), keyed by (M, N, K); see profiles/gemv_q8_0_mfma_m8_4096x11008_traffic.txt.
-MEASURED_TRAFFIC = {(8, 4096, 11008): 57.230e6}
+# ratio), keyed by (M, N, K); see profiles/gemv_q8_0_mfma_m8_4096x11008_traffic.txt and
+# profiles/gemv_q8_0_mfma_m8_12288x4096_traffic.txt.
+MEASURED_TRAFFIC = {(8, 4096, 11008): 57.236e6, (8, 12288, 4096): 61.745e6}
 
 
 def gemv_bytes(M, N, K):
