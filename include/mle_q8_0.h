@@ -174,6 +174,45 @@ int mle_top_tokens_f32(const float* logits, int rows, int n, int top_n, float te
                        int32_t* ids, float* probs, hipStream_t stream);
 
 /*
+ * Q8_0 16-row tiles: the bytes of a raw Q8_0 weight [N,K] reordered once, at
+ * weight-load time, for the MI355X matrix cores.  No counterpart in the
+ * reference: its loader copies GGUF bytes to the device as they are
+ * (src/io/gguf_weight_loader.cpp:102-116); a loader that calls
+ * mle_q8_0_tile after that copy keeps the same bytes per block (34) and gets
+ * decode launches whose weight loads are contiguous 1 KB pieces per wave.
+ *
+ * Layout, with KB = K/32 blocks, KP = ceil(KB/2) block pairs, G = ceil(N/16)
+ * row groups: G*KP quant pieces of 1024 bytes ((g, p) at (g*KP + p)*1024),
+ * then G*KP scale pieces of 64 bytes ((g, p) at G*KP*1024 + (g*KP + p)*64).
+ * Bytes 16l .. 16l+7 of quant piece (g, p) (l = 0..63) are quants
+ * 8(l/16) .. 8(l/16)+7 of block 2p of row 16g + l%16, bytes 16l+8 .. 16l+15
+ * the same quants of block 2p+1; dword r of scale piece (g, p) is the binary16
+ * scale of block 2p (low half) and 2p+1 (high half) of row 16g + r.  Rows past
+ * N and the block past an odd KB are zero.
+ *
+ * mle_q8_0_tiled_bytes: G*KP*1088; 0 for N <= 0, K <= 0 or K % 32 != 0.
+ * mle_q8_0_tile: raw -> tiled on `stream`.  w_tiled is 16-byte aligned, holds
+ *   mle_q8_0_tiled_bytes(N, K) bytes and does not overlap w_q8_0.
+ *   Errors: NULL pointers, N or K <= 0, misalignment, overlap ->
+ *   InvalidArgument; K % 32 != 0 -> Unsupported.
+ * mle_q8_0_linear_tiled / _swiglu_tiled / _multi_tiled: mle_q8_0_linear /
+ *   _swiglu / _multi on tiled weights (16-byte aligned), same errors.  M >= 64
+ *   runs the bf16-MFMA GEMM and M < 64 the MFMA decode with FP32-exact
+ *   activations, each bit-identical to the raw entry point on the same path
+ *   (the raw entry point's FP32 GEMV cases, M == 1 and short rows at M <= 4,
+ *   agree with it to about 1e-7 relative L2).
+ */
+size_t mle_q8_0_tiled_bytes(int N, int K);
+int mle_q8_0_tile(const uint8_t* w_q8_0, uint8_t* w_tiled, int N, int K, hipStream_t stream);
+int mle_q8_0_linear_tiled(const float* x, const uint8_t* w_tiled, const float* bias, float* y,
+                          int M, int N, int K, hipStream_t stream);
+int mle_q8_0_linear_swiglu_tiled(const float* x, const uint8_t* w_gate, const uint8_t* w_up,
+                                 float* y, int M, int N, int K, hipStream_t stream);
+int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const* w,
+                                const float* const* bias, float* const* y, const int* N, int M,
+                                int K, hipStream_t stream);
+
+/*
  * Message of the last failed call on this thread ("" if none).  Stands in for
  * the message of the reference's Status return (status.h:34-59).  The pointer
  * stays valid until the next call on the same thread.

@@ -23,7 +23,9 @@ ERROR_NAMES = {0: "Ok", 1: "InvalidArgument", 2: "OutOfRange", 3: "ShapeMismatch
 EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_q8_0_linear_swiglu", "mle_q8_0_linear_multi", "mle_q8_0_matmul",
             "mle_q8_0_embedding", "mle_argmax_f32", "mle_top_tokens_f32", "mle_swiglu_f32",
-            "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode")
+            "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode", "mle_q8_0_tiled_bytes",
+            "mle_q8_0_tile", "mle_q8_0_linear_tiled", "mle_q8_0_linear_swiglu_tiled",
+            "mle_q8_0_linear_multi_tiled")
 
 
 class Q8_0Error(RuntimeError):
@@ -75,6 +77,16 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_bytes.argtypes = [ctypes.c_int64]
     lib.mle_q8_0_f16_decode.restype = _i
     lib.mle_q8_0_f16_decode.argtypes = [_vp, _vp, ctypes.c_int64, _vp]
+    lib.mle_q8_0_tiled_bytes.restype = ctypes.c_size_t
+    lib.mle_q8_0_tiled_bytes.argtypes = [_i, _i]
+    lib.mle_q8_0_tile.restype = _i
+    lib.mle_q8_0_tile.argtypes = [_vp, _vp, _i, _i, _vp]
+    lib.mle_q8_0_linear_tiled.restype = _i
+    lib.mle_q8_0_linear_tiled.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_q8_0_linear_swiglu_tiled.restype = _i
+    lib.mle_q8_0_linear_swiglu_tiled.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_q8_0_linear_multi_tiled.restype = _i
+    lib.mle_q8_0_linear_multi_tiled.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp]
     _lib = lib
     return lib
 
@@ -148,19 +160,20 @@ def linear_swiglu(x, w_gate, w_up, y, M, N, K, stream=None) -> None:
     _raise(linear_swiglu_status(x, w_gate, w_up, y, M, N, K, stream)[0])
 
 
-def linear_multi_status(x, ws, biases, ys, Ns, M, K, stream=None):
+def linear_multi_status(x, ws, biases, ys, Ns, M, K, stream=None, tiled=False):
     count = len(ws)
     vp_arr = _vp * max(count, 1)
     w_arr = vp_arr(*[_addr(w) for w in ws]) if ws is not None else None
     y_arr = vp_arr(*[_addr(y) for y in ys]) if ys is not None else None
     b_arr = vp_arr(*[_addr(b) for b in biases]) if biases is not None else None
     n_arr = (_i * max(count, 1))(*Ns) if Ns is not None else None
-    rc = load().mle_q8_0_linear_multi(_addr(x), count,
-                                      ctypes.cast(w_arr, _vp) if w_arr else None,
-                                      ctypes.cast(b_arr, _vp) if b_arr else None,
-                                      ctypes.cast(y_arr, _vp) if y_arr else None,
-                                      ctypes.cast(n_arr, _vp) if n_arr else None,
-                                      M, K, _stream(stream))
+    fn = load().mle_q8_0_linear_multi_tiled if tiled else load().mle_q8_0_linear_multi
+    rc = fn(_addr(x), count,
+            ctypes.cast(w_arr, _vp) if w_arr else None,
+            ctypes.cast(b_arr, _vp) if b_arr else None,
+            ctypes.cast(y_arr, _vp) if y_arr else None,
+            ctypes.cast(n_arr, _vp) if n_arr else None,
+            M, K, _stream(stream))
     return _status(rc)
 
 
@@ -228,3 +241,47 @@ def f16_decode(bits, out, n, stream=None) -> None:
 
 def q8_0_bytes(numel: int) -> int:
     return load().mle_q8_0_bytes(numel)
+
+
+# Q8_0 16-row tiles: the raw bytes reordered once at load time (layout in
+# include/mle_q8_0.h); the *_tiled entry points take weights in that layout.
+
+def tiled_bytes(N: int, K: int) -> int:
+    return load().mle_q8_0_tiled_bytes(N, K)
+
+
+def tile_status(w, w_tiled, N, K, stream=None):
+    rc = load().mle_q8_0_tile(_addr(w), _addr(w_tiled), N, K, _stream(stream))
+    return _status(rc)
+
+
+def tile(w, w_tiled, N, K, stream=None) -> None:
+    """w_tiled = the 16-row tiled form of the raw Q8_0 weight w [N,K]."""
+    _raise(tile_status(w, w_tiled, N, K, stream)[0])
+
+
+def linear_tiled_status(x, w_tiled, bias, y, M, N, K, stream=None):
+    rc = load().mle_q8_0_linear_tiled(_addr(x), _addr(w_tiled), _addr(bias), _addr(y), M, N,
+                                      K, _stream(stream))
+    return _status(rc)
+
+
+def linear_tiled(x, w_tiled, bias, y, M, N, K, stream=None) -> None:
+    """linear() on a tiled weight."""
+    _raise(linear_tiled_status(x, w_tiled, bias, y, M, N, K, stream)[0])
+
+
+def linear_swiglu_tiled_status(x, w_gate, w_up, y, M, N, K, stream=None):
+    rc = load().mle_q8_0_linear_swiglu_tiled(_addr(x), _addr(w_gate), _addr(w_up), _addr(y),
+                                             M, N, K, _stream(stream))
+    return _status(rc)
+
+
+def linear_swiglu_tiled(x, w_gate, w_up, y, M, N, K, stream=None) -> None:
+    """linear_swiglu() on tiled weights."""
+    _raise(linear_swiglu_tiled_status(x, w_gate, w_up, y, M, N, K, stream)[0])
+
+
+def linear_multi_tiled(x, ws, biases, ys, Ns, M, K, stream=None) -> None:
+    """linear_multi() on tiled weights."""
+    _raise(linear_multi_status(x, ws, biases, ys, Ns, M, K, stream, tiled=True)[0])

@@ -159,14 +159,24 @@ struct Tune {
   mle::GemmConfig gemm{0, 0, 0};  // 0 fields = automatic
 };
 
+// Tiled weights (mle::WeightLayout::kTiled) take the MFMA decode for every
+// M < 64 (there is no tiled FP32 GEMV) and the MFMA GEMM from 64 tokens.
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
-               int N, int K, int path, const Tune& tune, hipStream_t stream) {
+               int N, int K, int path, const Tune& tune, hipStream_t stream,
+               mle::WeightLayout layout = mle::WeightLayout::kRaw) {
+  const bool tiled = layout == mle::WeightLayout::kTiled;
   if (path == 0) {
-    path = pick_path(M, N, K);
-    if (path == 3 && !mle::decode_mfma_fits(mle::decode_mfma_pick(M < 16 ? M : 16, N, K),
-                                            M < 16 ? M : 16, N, K))
+    path = tiled ? (M >= 64 ? 2 : 3) : pick_path(M, N, K);
+    const int mc = M < 16 ? M : 16;
+    if (path == 3 && !mle::decode_mfma_fits(mle::decode_mfma_pick(mc, N, K, layout), mc, N, K)) {
+      if (tiled)
+        return fail(MLE_UNSUPPORTED, "hip sgemm_nt Q8_0: K too large for the MFMA decode");
       path = 1;
+    }
   }
+  mle::LinearSegs one;
+  one.seg[0] = mle::LinearSeg{w, bias, y, N};
+  one.layout = layout;
   if (path == 2) {
     mle::GemmConfig c = mle::gemm_mfma_pick(M, N, K);
     if (tune.gemm.bm) c.bm = tune.gemm.bm;
@@ -183,7 +193,7 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
       return fail(MLE_UNSUPPORTED, "hip sgemm_nt Q8_0: K too large for the MFMA GEMM");
     mle::SplitKWorkspace ws;
     MLE_TRY(get_workspace(mle::gemm_mfma_workspace(c, M, N, K), stream, &ws));
-    return check_launch(mle::launch_gemm_mfma(c, x, w, bias, y, M, N, K, ws, stream),
+    return check_launch(mle::launch_gemm_mfma_segs(c, x, one, M, K, ws, stream),
                         "hip sgemm_nt Q8_0 launch failed");
   }
   if (path == 3) {
@@ -192,15 +202,17 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
       const int mc = M - m0 < 16 ? M - m0 : 16;
       mle::DecodeMfmaConfig c = tune.dec;
       if (c.mt == 0) {
-        c = mle::decode_mfma_pick(mc, N, K);
+        c = mle::decode_mfma_pick(mc, N, K, layout);
       } else if (c.mt < mc) {
         return fail(MLE_INVALID_ARGUMENT, "hip sgemm_nt_q8_0_weight: MFMA token tile " +
                                               std::to_string(c.mt) + " is smaller than M");
       }
+      mle::LinearSegs chunk = one;
+      chunk.seg[0].y = y + (int64_t)m0 * N;
       mle::SplitKWorkspace ws;
-      MLE_TRY(get_workspace(mle::decode_mfma_workspace(c, N, K), stream, &ws));
-      const hipError_t err = mle::launch_gemv_mfma(c, x + (int64_t)m0 * K, w, bias,
-                                                   y + (int64_t)m0 * N, mc, N, K, ws, stream);
+      MLE_TRY(get_workspace(mle::decode_mfma_workspace_segs(c, chunk, K), stream, &ws));
+      const hipError_t err =
+          mle::launch_gemv_mfma_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ws, stream);
       if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 launch failed");
     }
     return ok();
@@ -241,14 +253,15 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
     return check_launch(mle::launch_gemm_mfma_segs(c, x, s, M, K, ws, stream),
                         "hip Q8_0 fused Linear launch failed");
   }
-  if (swi ? M == 1 : pick_path(M, total_n, K) == 1) {
+  const bool tiled = s.layout == mle::WeightLayout::kTiled;
+  if (!tiled && (swi ? M == 1 : pick_path(M, total_n, K) == 1)) {
     const mle::GemvConfig c = mle::gemv_pick_config(M, total_n, K);
     return check_launch(mle::launch_gemv_segs(c, x, s, M, K, stream),
                         "hip Q8_0 fused Linear launch failed");
   }
   for (int m0 = 0; m0 < M; m0 += 16) {
     const int mc = M - m0 < 16 ? M - m0 : 16;
-    const mle::DecodeMfmaConfig c = mle::decode_mfma_pick(mc, total_n, K);
+    const mle::DecodeMfmaConfig c = mle::decode_mfma_pick(mc, total_n, K, s.layout);
     if (!mle::decode_mfma_fits(c, mc, 1, K))
       return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": K too large for the MFMA decode");
     mle::LinearSegs chunk = s;
@@ -267,9 +280,53 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
 
 }  // namespace
 
+namespace {
+
+int linear_swiglu(const float* x, const uint8_t* w_gate, const uint8_t* w_up, float* y, int M,
+                  int N, int K, hipStream_t stream, mle::WeightLayout layout) {
+  const bool tiled = layout == mle::WeightLayout::kTiled;
+  const char* ctx = tiled ? "linear_swiglu_q8_0_tiled" : "linear_swiglu_q8_0";
+  MLE_TRY(validate_linear(x, w_gate, nullptr, y, M, N, K));
+  if (w_up == nullptr)
+    return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": up pointer must not be null");
+  MLE_TRY(check_align(ctx, w_gate, tiled ? 16 : 2, "gate"));
+  MLE_TRY(check_align(ctx, w_up, tiled ? 16 : 2, "up"));
+  mle::LinearSegs s;
+  s.layout = layout;
+  s.mode = mle::Epilogue::kSwiGLU;
+  s.count = 2;
+  s.seg[0] = mle::LinearSeg{w_gate, nullptr, y, N};
+  s.seg[1] = mle::LinearSeg{w_up, nullptr, y, N};
+  return run_segs(ctx, x, s, M, K, stream);
+}
+
+int linear_multi(const float* x, int count, const uint8_t* const* w, const float* const* bias,
+                 float* const* y, const int* N, int M, int K, hipStream_t stream,
+                 mle::WeightLayout layout) {
+  const bool tiled = layout == mle::WeightLayout::kTiled;
+  const char* ctx = tiled ? "linear_multi_q8_0_tiled" : "linear_multi_q8_0";
+  if (count < 1 || count > 3)
+    return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": count must be 1, 2 or 3");
+  if (w == nullptr || y == nullptr || N == nullptr)
+    return fail(MLE_INVALID_ARGUMENT,
+                std::string("hip ") + ctx + ": weight, output and N arrays must not be null");
+  mle::LinearSegs s;
+  s.count = count;
+  s.layout = layout;
+  for (int i = 0; i < count; ++i) {
+    const float* b = bias ? bias[i] : nullptr;
+    MLE_TRY(validate_linear(x, w[i], b, y[i], M, N[i], K));
+    if (tiled) MLE_TRY(check_align(ctx, w[i], 16, "B"));
+    s.seg[i] = mle::LinearSeg{w[i], b, y[i], N[i]};
+  }
+  return run_segs(ctx, x, s, M, K, stream);
+}
+
+}  // namespace
+
 extern "C" {
 
-int mle_q8_0_abi_version(void) { return 4; }
+int mle_q8_0_abi_version(void) { return 5; }
 
 const char* mle_last_error(void) { return g_last_error.c_str(); }
 
@@ -326,38 +383,58 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
   return run_linear(x, w_q8_0, bias, y, M, N, K, path, tune, stream);
 }
 
+
 int mle_q8_0_linear_swiglu(const float* x, const uint8_t* w_gate, const uint8_t* w_up,
                            float* y, int M, int N, int K, hipStream_t stream) {
-  const char* ctx = "linear_swiglu_q8_0";
-  MLE_TRY(validate_linear(x, w_gate, nullptr, y, M, N, K));
-  if (w_up == nullptr)
-    return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": up pointer must not be null");
-  MLE_TRY(check_align(ctx, w_up, 2, "up"));
-  mle::LinearSegs s;
-  s.mode = mle::Epilogue::kSwiGLU;
-  s.count = 2;
-  s.seg[0] = mle::LinearSeg{w_gate, nullptr, y, N};
-  s.seg[1] = mle::LinearSeg{w_up, nullptr, y, N};
-  return run_segs(ctx, x, s, M, K, stream);
+  return linear_swiglu(x, w_gate, w_up, y, M, N, K, stream, mle::WeightLayout::kRaw);
 }
 
 int mle_q8_0_linear_multi(const float* x, int count, const uint8_t* const* w,
                           const float* const* bias, float* const* y, const int* N, int M, int K,
                           hipStream_t stream) {
-  const char* ctx = "linear_multi_q8_0";
-  if (count < 1 || count > 3)
-    return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": count must be 1, 2 or 3");
-  if (w == nullptr || y == nullptr || N == nullptr)
+  return linear_multi(x, count, w, bias, y, N, M, K, stream, mle::WeightLayout::kRaw);
+}
+
+size_t mle_q8_0_tiled_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 32 != 0) return 0;
+  return mle::tiled_bytes(N, K);
+}
+
+int mle_q8_0_tile(const uint8_t* w_q8_0, uint8_t* w_tiled, int N, int K, hipStream_t stream) {
+  const char* ctx = "tile_q8_0";
+  MLE_TRY(check_ptrs(ctx, w_q8_0, "w_q8_0", w_tiled, "w_tiled", w_tiled, "w_tiled"));
+  MLE_TRY(check_positive(ctx, N, "N"));
+  MLE_TRY(check_positive(ctx, K, "K"));
+  if (K % 32 != 0)
+    return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + " requires K to be a multiple of 32");
+  MLE_TRY(check_align(ctx, w_q8_0, 2, "w_q8_0"));
+  MLE_TRY(check_align(ctx, w_tiled, 16, "w_tiled"));
+  const uintptr_t r0 = (uintptr_t)w_q8_0, r1 = r0 + (uintptr_t)N * (K / 32) * 34;
+  const uintptr_t t0 = (uintptr_t)w_tiled, t1 = t0 + mle::tiled_bytes(N, K);
+  if (r0 < t1 && t0 < r1)
     return fail(MLE_INVALID_ARGUMENT,
-                std::string("hip ") + ctx + ": weight, output and N arrays must not be null");
-  mle::LinearSegs s;
-  s.count = count;
-  for (int i = 0; i < count; ++i) {
-    const float* b = bias ? bias[i] : nullptr;
-    MLE_TRY(validate_linear(x, w[i], b, y[i], M, N[i], K));
-    s.seg[i] = mle::LinearSeg{w[i], b, y[i], N[i]};
-  }
-  return run_segs(ctx, x, s, M, K, stream);
+                std::string("hip ") + ctx + ": w_q8_0 and w_tiled must not overlap");
+  return check_launch(mle::launch_tile_q8_0(w_q8_0, w_tiled, N, K, stream),
+                      "hip tile_q8_0 launch failed");
+}
+
+int mle_q8_0_linear_tiled(const float* x, const uint8_t* w_tiled, const float* bias, float* y,
+                          int M, int N, int K, hipStream_t stream) {
+  MLE_TRY(validate_linear(x, w_tiled, bias, y, M, N, K));
+  MLE_TRY(check_align("sgemm_nt_q8_0_tiled", w_tiled, 16, "B"));
+  return run_linear(x, w_tiled, bias, y, M, N, K, 0, Tune{}, stream,
+                    mle::WeightLayout::kTiled);
+}
+
+int mle_q8_0_linear_swiglu_tiled(const float* x, const uint8_t* w_gate, const uint8_t* w_up,
+                                 float* y, int M, int N, int K, hipStream_t stream) {
+  return linear_swiglu(x, w_gate, w_up, y, M, N, K, stream, mle::WeightLayout::kTiled);
+}
+
+int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const* w,
+                                const float* const* bias, float* const* y, const int* N, int M,
+                                int K, hipStream_t stream) {
+  return linear_multi(x, count, w, bias, y, N, M, K, stream, mle::WeightLayout::kTiled);
 }
 
 int mle_swiglu_f32(const float* gate, const float* up, float* y, int64_t n,

@@ -154,7 +154,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // weight; producer waves 0-1 dequantise the gate rows and 2-3 the up rows, so
 // each wave reads one weight; the epilogue writes silu(gate) * up for BN/2
 // output columns.
-template <int MI, int NJ, int MODE>
+template <int MI, int NJ, int MODE, int LAYOUT>
 __global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
     const u32x4* __restrict__ xf, uint32_t xf_bytes, const GemmArgs args, int M, int K,
     int steps_per_split, float* __restrict__ partials, uint32_t* __restrict__ counters) {
@@ -416,39 +416,82 @@ __global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
     const uint32_t wmis = (uint32_t)(((uintptr_t)wtile + boff) & 2u);
     const uint32_t wv8 = boff + wmis;
     const uint32_t wv2 = boff + (wmis ? 0u : 32u);
+    // Tiled weights (LAYOUT 1): the tile's rows are whole 16-row groups
+    // [n0/16, n0/16 + BNO/16) of quant pieces (1 KB per group and K step) and
+    // scale pieces (64 B).  Item (row, half j) reads the quant slots of lanes
+    // 32 j + r and 32 j + 16 + r (r = row % 16): quants 16 j .. 16 j + 15 of
+    // both blocks of the step, and the row's scale dword of the pair.
+    constexpr bool kTiled = LAYOUT == int(WeightLayout::kTiled);
+    const int KP = (KB + 1) >> 1;
+    const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
+    const int64_t g0 = n0 / kTileRows;
+    const int64_t ngr = min((int64_t)(BNO / kTileRows), G - g0);
+    const uint8_t* tq_base = wsrc + g0 * KP * kTilePieceBytes;
+    const uint8_t* ts_base = wsrc + G * KP * kTilePieceBytes + g0 * KP * kTileScaleBytes;
+    const __amdgpu_buffer_rsrc_t tqrs = rsrc(tq_base, (uint32_t)(ngr * KP * kTilePieceBytes));
+    const __amdgpu_buffer_rsrc_t tsrs = rsrc(ts_base, (uint32_t)(ngr * KP * kTileScaleBytes));
+    const uint32_t tqv = (uint32_t)(prow / kTileRows) * KP * kTilePieceBytes +
+                         (uint32_t)(32 * wn_h + prow % kTileRows) * 16;
+    const uint32_t tsv = (uint32_t)(prow / kTileRows) * KP * kTileScaleBytes +
+                         (uint32_t)(prow % kTileRows) * 4;
     // Steps s with block 2 s + h < KB (none for threads without a W block,
-    // whose loads are then all masked).
-    const int w_steps = w_thread ? (KB - wn_h + 1) >> 1 : 0;
-    auto load_w = [&](int s, RawBlock& r) {
+    // whose loads are then all masked); tiled: every pair (the block past an
+    // odd K/32 is zero in the tiled tensor).
+    const int w_steps = w_thread ? (kTiled ? KP : (KB - wn_h + 1) >> 1) : 0;
+    struct TiledW {
+      u32x4 a, b;  // quant slots 32 j + r, 32 j + 16 + r
+      uint32_t sc;  // scales of both blocks
+    };
+    using WItem = std::conditional_t<kTiled, TiledW, RawBlock>;
+    auto load_w = [&](int s, WItem& r) {
       s = min(s, s_last);
       const bool live = s < w_steps;
-      const uint32_t so = (uint32_t)s * (2 * kBlockBytes);
-      const uint32_t v8 = live ? wv8 : 0x80000000u;
-      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, so, 0);
-      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, so, 0);
-      r.v0 = u32x4_a4{a.x, a.y, a.z, a.w};
-      r.v1 = u32x4_a4{b.x, b.y, b.z, b.w};
-      r.u = __builtin_amdgcn_raw_buffer_load_b16(wrs, live ? wv2 : 0x80000000u, so, 0);
-      r.mis = wmis;
+      if constexpr (kTiled) {
+        const uint32_t sq = (uint32_t)s * kTilePieceBytes;
+        r.a = __builtin_amdgcn_raw_buffer_load_b128(tqrs, live ? tqv : 0x80000000u, sq, 0);
+        r.b = __builtin_amdgcn_raw_buffer_load_b128(tqrs, live ? tqv + 256 : 0x80000000u, sq, 0);
+        r.sc = __builtin_amdgcn_raw_buffer_load_b32(tsrs, live ? tsv : 0x80000000u,
+                                                    (uint32_t)s * kTileScaleBytes, 0);
+      } else {
+        const uint32_t so = (uint32_t)s * (2 * kBlockBytes);
+        const uint32_t v8 = live ? wv8 : 0x80000000u;
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, so, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, so, 0);
+        r.v0 = u32x4_a4{a.x, a.y, a.z, a.w};
+        r.v1 = u32x4_a4{b.x, b.y, b.z, b.w};
+        r.u = __builtin_amdgcn_raw_buffer_load_b16(wrs, live ? wv2 : 0x80000000u, so, 0);
+        r.mis = wmis;
+      }
     };
-    auto dequant = [&](const RawBlock& r, uint16_t* bs) {
+    auto dq8 = [](float d, uint32_t q0, uint32_t q1) {
+      return u32x4{cvt_bf16x2(d * q_at(q0, 0), d * q_at(q0, 1)),
+                   cvt_bf16x2(d * q_at(q0, 2), d * q_at(q0, 3)),
+                   cvt_bf16x2(d * q_at(q1, 0), d * q_at(q1, 1)),
+                   cvt_bf16x2(d * q_at(q1, 2), d * q_at(q1, 3))};
+    };
+    auto dequant = [&](const WItem& r, uint16_t* bs) {
       if (!w_thread) return;
-      const Block b = finish_block(r);
-      const float d = scale_to_f32_fast(b.scale_bits);
-      u32x4* dst = reinterpret_cast<u32x4*>(bs + wn_row * LDS_STRIDE + wn_h * kBlockElems);
+      if constexpr (kTiled) {
+        // Quants 16 j .. 16 j + 15 of block h go to elements 32 h + 16 j ..
+        const float d0 = scale_to_f32_fast(r.sc & 0xffffu);
+        const float d1 = scale_to_f32_fast(r.sc >> 16);
+        u32x4* dst = reinterpret_cast<u32x4*>(bs + wn_row * LDS_STRIDE + 16 * wn_h);
+        dst[0] = dq8(d0, r.a.x, r.a.y);
+        dst[1] = dq8(d0, r.b.x, r.b.y);
+        dst[4] = dq8(d1, r.a.z, r.a.w);
+        dst[5] = dq8(d1, r.b.z, r.b.w);
+      } else {
+        const Block b = finish_block(r);
+        const float d = scale_to_f32_fast(b.scale_bits);
+        u32x4* dst = reinterpret_cast<u32x4*>(bs + wn_row * LDS_STRIDE + wn_h * kBlockElems);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t q0 = b.q[2 * i], q1 = b.q[2 * i + 1];
-        dst[i] = u32x4{cvt_bf16x2(d * q_at(q0, 0), d * q_at(q0, 1)),
-                       cvt_bf16x2(d * q_at(q0, 2), d * q_at(q0, 3)),
-                       cvt_bf16x2(d * q_at(q1, 0), d * q_at(q1, 1)),
-                       cvt_bf16x2(d * q_at(q1, 2), d * q_at(q1, 3))};
+        for (int i = 0; i < 4; ++i) dst[i] = dq8(d, b.q[2 * i], b.q[2 * i + 1]);
       }
     };
     // Ring of 8 raw blocks: slot (s - s_begin) % 8 holds W of step s.  The pair
     // starting at step t dequantises W(t + 2), W(t + 3) into the other buffer.
     constexpr int RING = 8;
-    RawBlock r[RING];
+    WItem r[RING];
 #pragma unroll
     for (int u = 0; u < RING; ++u) load_w(s_begin + u, r[u]);
     dequant(r[0], Bs);
@@ -512,17 +555,29 @@ GemmGrid gemm_grid(const GemmConfig& c, int M, const LinearSegs& s, int K) {
   return g;
 }
 
-template <int MI, int NJ>
-void launch_tile(const GemmGrid& g, Epilogue mode, const u32x4* xf, uint32_t xf_bytes, int M,
-                 int K, const SplitKWorkspace& ws, hipStream_t stream) {
+template <int MI, int NJ, int L>
+void launch_tile_l(const GemmGrid& g, Epilogue mode, const u32x4* xf, uint32_t xf_bytes, int M,
+                   int K, const SplitKWorkspace& ws, hipStream_t stream) {
   const dim3 grid(g.tn, g.tm, g.splits);
   if (mode == Epilogue::kSwiGLU) {
-    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 1>), grid, dim3(Roles<MI>::kThreads), 0, stream, xf,
-                       xf_bytes, g.args, M, K, g.steps_per_split, ws.partials, ws.counters);
+    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 1, L>), grid, dim3(Roles<MI>::kThreads), 0,
+                       stream, xf, xf_bytes, g.args, M, K, g.steps_per_split, ws.partials,
+                       ws.counters);
   } else {
-    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 0>), grid, dim3(Roles<MI>::kThreads), 0, stream, xf,
-                       xf_bytes, g.args, M, K, g.steps_per_split, ws.partials, ws.counters);
+    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 0, L>), grid, dim3(Roles<MI>::kThreads), 0,
+                       stream, xf, xf_bytes, g.args, M, K, g.steps_per_split, ws.partials,
+                       ws.counters);
   }
+}
+
+template <int MI, int NJ>
+void launch_tile(const GemmGrid& g, Epilogue mode, WeightLayout layout, const u32x4* xf,
+                 uint32_t xf_bytes, int M, int K, const SplitKWorkspace& ws,
+                 hipStream_t stream) {
+  if (layout == WeightLayout::kTiled)
+    launch_tile_l<MI, NJ, int(WeightLayout::kTiled)>(g, mode, xf, xf_bytes, M, K, ws, stream);
+  else
+    launch_tile_l<MI, NJ, int(WeightLayout::kRaw)>(g, mode, xf, xf_bytes, M, K, ws, stream);
 }
 
 // Bytes of the fragment-ordered bf16 copy of X: rows rounded up to 32, K to 64.
@@ -631,11 +686,11 @@ hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const Line
   if (err != hipSuccess) return err;
   const int mi = c.bm / 128;
   switch (mi * 1000 + c.bn) {
-    case 1064: launch_tile<1, 2>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
-    case 1096: launch_tile<1, 3>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
-    case 1128: launch_tile<1, 4>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
-    case 2064: launch_tile<2, 2>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
-    case 2096: launch_tile<2, 3>(g, s.mode, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 1064: launch_tile<1, 2>(g, s.mode, s.layout, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 1096: launch_tile<1, 3>(g, s.mode, s.layout, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 1128: launch_tile<1, 4>(g, s.mode, s.layout, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 2064: launch_tile<2, 2>(g, s.mode, s.layout, xf, (uint32_t)xfb, M, K, ws, stream); break;
+    case 2096: launch_tile<2, 3>(g, s.mode, s.layout, xf, (uint32_t)xfb, M, K, ws, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -222,7 +222,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // MODE 0: plain / multi-output Linear.  MODE 1 (SwiGLU): waves [0, W/2) take
 // rows of the gate weight, waves [W/2, W) the same rows of the up weight, and
 // the epilogue writes silu(gate) * up.
-template <int MT, int W, int KSL, int MODE>
+template <int MT, int W, int KSL, int MODE, int LAYOUT>
 __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
     const float* __restrict__ x, const DecodeArgs args, int M, int K,
     float* __restrict__ partials, uint32_t* __restrict__ counters) {
@@ -304,23 +304,60 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   //    Blocks past the slice's end read as zeros: their per-lane offset is put
   //    past the buffer (the range check applies to the per-lane offset), so no
   //    lane ever addresses a byte outside its slice of the weight tensor.
-  RawBlock wr[NCH][NL];
+  constexpr bool kTiled = LAYOUT == int(WeightLayout::kTiled);
+  RawBlock wr[kTiled ? 1 : NCH][NL];
+  u32x4 tq[kTiled ? NCH : 1][4];  // tiled: the chunk's 4 block pairs
+  uint32_t ts[kTiled ? NCH : 1];  // tiled: one scale dword per chunk
+  if constexpr (!kTiled) {
 #pragma unroll
-  for (int c = 0; c < NCH; ++c)
+    for (int c = 0; c < NCH; ++c)
 #pragma unroll
-    for (int u = 0; u < NL; ++u) {
-      const int b = KS * c + 4 * u;  // first block of the load set (lane adds g)
-      const bool live = b + g < nblk;
-      const uint32_t soff = b < nblk ? (uint32_t)b * kBlockBytes : 0u;  // uniform
-      const uint32_t v8 = live ? voff : 0x80000000u;
-      const uint32_t v2 = live ? uoff : 0x80000000u;
-      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, soff, 0);
-      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, soff, 0);
-      wr[c][u].v0 = u32x4_a4{v0.x, v0.y, v0.z, v0.w};
-      wr[c][u].v1 = u32x4_a4{v1.x, v1.y, v1.z, v1.w};
-      wr[c][u].u = __builtin_amdgcn_raw_buffer_load_b16(wrs, v2, soff, 0);
-      wr[c][u].mis = mis;
+      for (int u = 0; u < NL; ++u) {
+        const int b = KS * c + 4 * u;  // first block of the load set (lane adds g)
+        const bool live = b + g < nblk;
+        const uint32_t soff = b < nblk ? (uint32_t)b * kBlockBytes : 0u;  // uniform
+        const uint32_t v8 = live ? voff : 0x80000000u;
+        const uint32_t v2 = live ? uoff : 0x80000000u;
+        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, soff, 0);
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, soff, 0);
+        wr[c][u].v0 = u32x4_a4{v0.x, v0.y, v0.z, v0.w};
+        wr[c][u].v1 = u32x4_a4{v1.x, v1.y, v1.z, v1.w};
+        wr[c][u].u = __builtin_amdgcn_raw_buffer_load_b16(wrs, v2, soff, 0);
+        wr[c][u].mis = mis;
+      }
+  } else {
+    // Tiled weights: the wave's row group streams its quant pieces (1 KB per
+    // block pair, one 16-byte slot per lane: rows l % 16, quants 8 (l/16) .. +7
+    // of both blocks) and scale pieces (lane l reads dword l of the chunk's four
+    // 64-byte pieces: pair l/16, row l % 16).  Pairs past the slice read as zero.
+    const int KP = (KB + 1) >> 1;
+    const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
+    const int64_t rg = n0 / kTileRows + wrow;
+    const int64_t rgc = rg < G ? rg : 0;
+    const uint8_t* qb = w + rgc * KP * kTilePieceBytes;
+    const uint8_t* sb = w + G * KP * kTilePieceBytes + rgc * KP * kTileScaleBytes;
+    const __amdgpu_buffer_rsrc_t qrs =
+        make_rsrc(qb, rg < G ? (uint32_t)KP * kTilePieceBytes : 0u);
+    const __amdgpu_buffer_rsrc_t srs =
+        make_rsrc(sb, rg < G ? (uint32_t)KP * kTileScaleBytes : 0u);
+    const int p0 = kb0 >> 1;  // KSL is even
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int pr = (KS / 2) * c + u;  // pair within the slice
+        const uint32_t off = 2 * pr < nblk
+                                 ? (uint32_t)(p0 + pr) * kTilePieceBytes + (uint32_t)lane * 16
+                                 : 0x80000000u;
+        tq[c][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0);
+      }
+      const int ps = (KS / 2) * c + g;  // scale pair of this lane
+      ts[c] = __builtin_amdgcn_raw_buffer_load_b32(
+          srs, 2 * ps < nblk ? (uint32_t)(p0 + (KS / 2) * c) * kTileScaleBytes + (uint32_t)lane * 4
+                             : 0x80000000u,
+          0, 0);
     }
+  }
 
   // 2. B fragments of the whole K slice (activations split into bf16 parts),
   //    shared by the workgroup's waves.  B fragment (block kb, MFMA p): lane l
@@ -373,41 +410,56 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   //    scales to (wave-private) LDS, in-register transpose into A fragments,
   //    P chained MFMAs per block, fp32 scale FMA.  No barrier.
   f32x4 accs[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  // Block kc of chunk (kb = block within the slice): P chained MFMAs against
+  // the token columns, then the fp32 scale FMA into an accumulator that takes
+  // every other block (even blocks in accs[0], odd in accs[1], in K order).
+  auto block_mma = [&](int kc, int kb, const bf16x8_t a, f32x4& a4) {
+    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, W, P>(kb, 0, g, r16)),
+        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+    for (int p = 1; p < P; ++p)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, W, P>(kb, p, g, r16)), d, 0,
+          0, 0);
+    // D layout: lane l holds rows 4 (l/16) + v (v = 0..3), virtual column l % 16.
+    const f32x4 sc = *reinterpret_cast<const f32x4*>(&scl[wave][kc][4 * g]);
+    a4.x = __builtin_fmaf(sc.x, d.x, a4.x);
+    a4.y = __builtin_fmaf(sc.y, d.y, a4.y);
+    a4.z = __builtin_fmaf(sc.z, d.z, a4.z);
+    a4.w = __builtin_fmaf(sc.w, d.w, a4.w);
+  };
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    Block blk[NL];
+    if constexpr (kTiled) {
+      // Scales of pair g (blocks 2g, 2g+1 of the chunk) for row r16; the quant
+      // slots are A fragments already.
+      scl[wave][2 * g][r16] = scale_to_f32_fast(ts[c] & 0xffffu);
+      scl[wave][2 * g + 1][r16] = scale_to_f32_fast(ts[c] >> 16);
 #pragma unroll
-    for (int u = 0; u < NL; ++u) {
-      blk[u] = finish_block(wr[c][u]);
-      const bool valid = KS * c + 4 * u + g < nblk;
-      scl[wave][4 * u + g][r16] = valid ? scale_to_f32_fast(blk[u].scale_bits) : 0.0f;
-    }
+      for (int u = 0; u < 4; ++u) {
+        const u32x4 q = tq[c][u];
+        block_mma(2 * u, KS * c + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
+        block_mma(2 * u + 1, KS * c + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
+      }
+    } else {
+      Block blk[NL];
 #pragma unroll
-    for (int u = 0; u < NL; ++u) {
-      uint32_t q[8];
+      for (int u = 0; u < NL; ++u) {
+        blk[u] = finish_block(wr[c][u]);
+        const bool valid = KS * c + 4 * u + g < nblk;
+        scl[wave][4 * u + g][r16] = valid ? scale_to_f32_fast(blk[u].scale_bits) : 0.0f;
+      }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) q[i] = blk[u].q[i];
-      transpose_chunks(q);
+      for (int u = 0; u < NL; ++u) {
+        uint32_t q[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int kc = 4 * u + j;        // block within the chunk
-        const int kb = KS * c + kc;      // block within the slice
-        const bf16x8_t a = quants_to_bf16(q[2 * j], q[2 * j + 1]);
-        f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, W, P>(kb, 0, g, r16)),
-            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        for (int i = 0; i < 8; ++i) q[i] = blk[u].q[i];
+        transpose_chunks(q);
 #pragma unroll
-        for (int p = 1; p < P; ++p)
-          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, W, P>(kb, p, g, r16)), d, 0,
-              0, 0);
-        // D layout: lane l holds rows 4 (l/16) + v (v = 0..3), virtual column l % 16.
-        const f32x4 sc = *reinterpret_cast<const f32x4*>(&scl[wave][kc][4 * g]);
-        f32x4& a4 = accs[j & 1];
-        a4.x = __builtin_fmaf(sc.x, d.x, a4.x);
-        a4.y = __builtin_fmaf(sc.y, d.y, a4.y);
-        a4.z = __builtin_fmaf(sc.z, d.z, a4.z);
-        a4.w = __builtin_fmaf(sc.w, d.w, a4.w);
+        for (int j = 0; j < 4; ++j)
+          block_mma(4 * u + j, KS * c + 4 * u + j, quants_to_bf16(q[2 * j], q[2 * j + 1]),
+                    accs[j & 1]);
       }
     }
   }
@@ -532,34 +584,42 @@ Grid grid_of(const DecodeMfmaConfig& c, const LinearSegs& s, int K) {
   return gr;
 }
 
-template <int MT, int W, int KSL>
-hipError_t launch_t(const Grid& gr, Epilogue mode, const float* x, int M, int K,
+template <int MT, int W, int KSL, int L>
+hipError_t launch_l(const Grid& gr, Epilogue mode, const float* x, int M, int K,
                     const SplitKWorkspace& ws, hipStream_t stream) {
   if (mode == Epilogue::kSwiGLU) {
     if constexpr (W % 2 == 0)
-      hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KSL, 1>), dim3(gr.tiles, gr.splits),
+      hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KSL, 1, L>), dim3(gr.tiles, gr.splits),
                          dim3(64 * W), 0, stream, x, gr.args, M, K, ws.partials, ws.counters);
   } else {
-    hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KSL, 0>), dim3(gr.tiles, gr.splits),
+    hipLaunchKernelGGL((gemv_q8_0_mfma_kernel<MT, W, KSL, 0, L>), dim3(gr.tiles, gr.splits),
                        dim3(64 * W), 0, stream, x, gr.args, M, K, ws.partials, ws.counters);
   }
   return hipGetLastError();
 }
 
+template <int MT, int W, int KSL>
+hipError_t launch_t(const Grid& gr, Epilogue mode, WeightLayout layout, const float* x, int M,
+                    int K, const SplitKWorkspace& ws, hipStream_t stream) {
+  if (layout == WeightLayout::kTiled)
+    return launch_l<MT, W, KSL, int(WeightLayout::kTiled)>(gr, mode, x, M, K, ws, stream);
+  return launch_l<MT, W, KSL, int(WeightLayout::kRaw)>(gr, mode, x, M, K, ws, stream);
+}
+
 template <int MT>
 hipError_t dispatch_shape(const DecodeMfmaConfig& c, const Grid& gr, Epilogue mode,
-                          const float* x, int M, int K, const SplitKWorkspace& ws,
-                          hipStream_t stream) {
+                          WeightLayout layout, const float* x, int M, int K,
+                          const SplitKWorkspace& ws, hipStream_t stream) {
   if (c.kslice == 16) {
-    if (c.waves == 2) return launch_t<MT, 2, 16>(gr, mode, x, M, K, ws, stream);
-    if (c.waves == 4) return launch_t<MT, 4, 16>(gr, mode, x, M, K, ws, stream);
-    if (c.waves == 8) return launch_t<MT, 8, 16>(gr, mode, x, M, K, ws, stream);
+    if (c.waves == 2) return launch_t<MT, 2, 16>(gr, mode, layout, x, M, K, ws, stream);
+    if (c.waves == 4) return launch_t<MT, 4, 16>(gr, mode, layout, x, M, K, ws, stream);
+    if (c.waves == 8) return launch_t<MT, 8, 16>(gr, mode, layout, x, M, K, ws, stream);
   }
   if constexpr (Cols<MT>::P <= 2) {
     if (c.kslice == 32) {
-      if (c.waves == 2) return launch_t<MT, 2, 32>(gr, mode, x, M, K, ws, stream);
-      if (c.waves == 4) return launch_t<MT, 4, 32>(gr, mode, x, M, K, ws, stream);
-      if (c.waves == 8) return launch_t<MT, 8, 32>(gr, mode, x, M, K, ws, stream);
+      if (c.waves == 2) return launch_t<MT, 2, 32>(gr, mode, layout, x, M, K, ws, stream);
+      if (c.waves == 4) return launch_t<MT, 4, 32>(gr, mode, layout, x, M, K, ws, stream);
+      if (c.waves == 8) return launch_t<MT, 8, 32>(gr, mode, layout, x, M, K, ws, stream);
     }
   }
   return hipErrorInvalidValue;
@@ -585,7 +645,7 @@ int decode_mfma_tile(int M) {
   return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 5 ? 5 : M <= 8 ? 8 : 16;
 }
 
-DecodeMfmaConfig decode_mfma_pick(int M, int N, int K) {
+DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
   // Measured on MI355X over the BASELINE decode shapes: 16-block K slices
   // (one-shot workgroups of ~35 KB) beat 32 unless K fits one 32-block slice
   // (no split-K hand-off at all); 8 waves per workgroup pay off for 4+ tokens
@@ -595,6 +655,10 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K) {
   c.mt = decode_mfma_tile(M);
   const int KB = K / kBlockElems;
   c.kslice = (c.mt <= 8 && KB <= 32) ? 32 : 16;
+  if (layout == WeightLayout::kTiled) {
+    c.waves = N >= 4096 ? 8 : N >= 2048 ? 4 : 2;
+    return c;
+  }
   c.waves = (c.mt >= 4 && N >= 8192) ? 8 : 4;
   return c;
 }
@@ -638,12 +702,12 @@ hipError_t launch_gemv_mfma_segs(const DecodeMfmaConfig& c, const float* x,
     if (!decode_mfma_fits(c, M, s.seg[i].N, K) || s.seg[i].N <= 0) return hipErrorInvalidValue;
   const Grid gr = grid_of(c, s, K);
   switch (c.mt) {
-    case 1: return dispatch_shape<1>(c, gr, s.mode, x, M, K, ws, stream);
-    case 2: return dispatch_shape<2>(c, gr, s.mode, x, M, K, ws, stream);
-    case 4: return dispatch_shape<4>(c, gr, s.mode, x, M, K, ws, stream);
-    case 5: return dispatch_shape<5>(c, gr, s.mode, x, M, K, ws, stream);
-    case 8: return dispatch_shape<8>(c, gr, s.mode, x, M, K, ws, stream);
-    case 16: return dispatch_shape<16>(c, gr, s.mode, x, M, K, ws, stream);
+    case 1: return dispatch_shape<1>(c, gr, s.mode, s.layout, x, M, K, ws, stream);
+    case 2: return dispatch_shape<2>(c, gr, s.mode, s.layout, x, M, K, ws, stream);
+    case 4: return dispatch_shape<4>(c, gr, s.mode, s.layout, x, M, K, ws, stream);
+    case 5: return dispatch_shape<5>(c, gr, s.mode, s.layout, x, M, K, ws, stream);
+    case 8: return dispatch_shape<8>(c, gr, s.mode, s.layout, x, M, K, ws, stream);
+    case 16: return dispatch_shape<16>(c, gr, s.mode, s.layout, x, M, K, ws, stream);
   }
   return hipErrorInvalidValue;
 }

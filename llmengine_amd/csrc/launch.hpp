@@ -52,17 +52,44 @@ struct LinearSeg {
   int N = 0;
 };
 enum class Epilogue { kPlain = 0, kSwiGLU = 1 };
+// Byte layout of the weights of a launch.
+//   kRaw: GGUF Q8_0, row n at byte n*(K/32)*34, 34-byte blocks along K.
+//   kTiled: Q8_0 16-row tiles.  With KB = K/32 blocks, KP = ceil(KB/2) block
+//     pairs and G = ceil(N/16) row groups, the tensor is
+//       quant pieces  [G][KP] x 1024 B, then
+//       scale pieces  [G][KP] x 64 B   (at byte G*KP*1024),
+//     G*KP*1088 bytes in all (34 per block, as raw, plus zero padding of rows
+//     past N and of the block past KB when KB is odd).  Slot l (0..63) of quant
+//     piece (g, p) holds, at bytes 16l .. 16l+7, quants 8(l/16) .. +7 of block
+//     2p of row 16g + l%16, and at bytes 16l+8 .. +15 the same quants of block
+//     2p+1: the bf16 MFMA A-fragment order, so one 16-byte load per lane feeds
+//     two 16x16x32 MFMAs.  Dword r of scale piece (g, p) holds the binary16
+//     scale of block 2p (low half) and 2p+1 (high half) of row 16g + r.
+enum class WeightLayout { kRaw = 0, kTiled = 1 };
+constexpr int kTileRows = 16;
+constexpr int kTilePieceBytes = 1024;
+constexpr int kTileScaleBytes = 64;
+// Bytes of a kTiled tensor of N rows and K columns (K % 32 == 0).
+inline size_t tiled_bytes(int64_t N, int64_t K) {
+  const int64_t KP = (K / 32 + 1) / 2, G = (N + kTileRows - 1) / kTileRows;
+  return (size_t)(G * KP * (kTilePieceBytes + kTileScaleBytes));
+}
 struct LinearSegs {
   LinearSeg seg[3];
   int count = 1;
   Epilogue mode = Epilogue::kPlain;
+  WeightLayout layout = WeightLayout::kRaw;
 };
+// Raw Q8_0 [N, K] -> kTiled (one pass; `tiled` holds tiled_bytes(N, K)).
+hipError_t launch_tile_q8_0(const uint8_t* raw, uint8_t* tiled, int N, int K,
+                            hipStream_t stream);
 
 // FP32 GEMV over segments (kSwiGLU only with a token tile of 1 and rw <= 4).
 hipError_t launch_gemv_segs(const GemvConfig& cfg, const float* x, const LinearSegs& s, int M,
                             int K, hipStream_t stream);
 
-DecodeMfmaConfig decode_mfma_pick(int M, int N, int K);
+DecodeMfmaConfig decode_mfma_pick(int M, int N, int K,
+                                  WeightLayout layout = WeightLayout::kRaw);
 bool decode_mfma_config_valid(const DecodeMfmaConfig& c);
 SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K);
 // False when the shape's buffer offsets would not fit 32 bits (the caller then

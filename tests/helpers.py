@@ -53,3 +53,38 @@ def assert_bitexact(got, want, what=""):
     assert np.array_equal(gn, wn), f"{what}: NaN positions differ"
     diff = np.nonzero(bits(got)[~wn] != bits(want)[~wn])[0]
     assert diff.size == 0, f"{what}: {diff.size} values differ, first at {diff[:5]}"
+
+
+# ---------------------------------------------------------------------------
+# Q8_0 16-row tiles (layout of mle_q8_0_tile, include/mle_q8_0.h), restated in
+# numpy as the checker of the device repack.
+
+def tiled_shape(N: int, K: int):
+    KB = K // 32
+    return KB, (KB + 1) // 2, (N + 15) // 16
+
+
+def tile_ref(raw: np.ndarray, N: int, K: int) -> np.ndarray:
+    """Raw Q8_0 bytes of W[N,K] -> tiled bytes (quant pieces, then scale pieces)."""
+    KB, KP, G = tiled_shape(N, K)
+    blocks = np.asarray(raw, np.uint8).reshape(N, KB, 34)
+    q = np.zeros((G * 16, 2 * KP, 32), np.uint8)
+    d = np.zeros((G * 16, 2 * KP, 2), np.uint8)
+    q[:N, :KB] = blocks[:, :, 2:]
+    d[:N, :KB] = blocks[:, :, :2]
+    # piece (g, p), slot 16 sub + r, half h: quants 8 sub .. of block 2p+h, row 16g+r
+    qt = q.reshape(G, 16, KP, 2, 4, 8).transpose(0, 2, 4, 1, 3, 5).reshape(-1)
+    # piece (g, p), dword r: scale bytes of block 2p, then 2p+1, of row 16g+r
+    dt = d.reshape(G, 16, KP, 2, 2).transpose(0, 2, 1, 3, 4).reshape(-1)
+    return np.concatenate([qt, dt])
+
+
+def untile_ref(tiled: np.ndarray, N: int, K: int) -> np.ndarray:
+    """Inverse of tile_ref (drops the zero padding)."""
+    KB, KP, G = tiled_shape(N, K)
+    t = np.asarray(tiled, np.uint8)
+    nq = G * KP * 1024
+    q = t[:nq].reshape(G, KP, 4, 16, 2, 8).transpose(0, 3, 1, 4, 2, 5).reshape(G * 16, 2 * KP, 32)
+    d = t[nq:].reshape(G, KP, 16, 2, 2).transpose(0, 2, 1, 3, 4).reshape(G * 16, 2 * KP, 2)
+    out = np.concatenate([d[:N, :KB], q[:N, :KB]], axis=2)
+    return out.reshape(-1)

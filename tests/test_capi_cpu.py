@@ -6,6 +6,7 @@ import os
 import re
 import subprocess
 
+import numpy as np
 import pytest
 
 from llmengine_amd import capi
@@ -25,7 +26,7 @@ def declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     lib = capi.load()
-    assert lib.mle_q8_0_abi_version() == 4
+    assert lib.mle_q8_0_abi_version() == 5
     out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH],
                          stdout=subprocess.PIPE, text=True, check=True).stdout
     exported = set(re.findall(r" T (mle_\w+)", out))
@@ -199,3 +200,78 @@ def test_product_package_does_not_import_oracle():
             text = open(path).read()
             assert not re.search(r"^\s*(import|from)\s+oracle\b", text, re.M), path
             assert "q8_0_oracle" not in text and "liboracle" not in text, path
+
+
+def test_tiled_bytes_rule():
+    # G*KP*1088 with G = ceil(N/16) row groups and KP = ceil(K/64) block pairs
+    assert capi.tiled_bytes(4096, 11008) == 4096 * 344 * 34  # no padding
+    assert capi.tiled_bytes(17, 96) == 2 * 2 * 1088          # rows and a block padded
+    assert capi.tiled_bytes(1, 32) == 1088
+    assert capi.tiled_bytes(151936, 896) == 151936 * 28 * 34
+    for bad in [(0, 32), (16, 0), (16, 48), (-1, 32)]:
+        assert capi.tiled_bytes(*bad) == 0
+
+
+@pytest.mark.parametrize("N,K", [(1, 32), (17, 96), (33, 4128), (100, 992)])
+def test_tile_reference_layout(N, K):
+    """The numpy tiler that checks the device repack: a permutation of the raw
+    bytes plus zero padding (round trip), and each slot where the layout puts it
+    (explicit loops over the formula of include/mle_q8_0.h)."""
+    from helpers import tile_ref, tiled_shape, untile_ref
+    from llmengine_amd import synthetic as S
+    raw = S.q8_0_weight(5 + N, N, K)[0]
+    t = tile_ref(raw, N, K)
+    assert t.size == capi.tiled_bytes(N, K)
+    assert np.array_equal(untile_ref(t, N, K), raw)
+    KB, KP, G = tiled_shape(N, K)
+    blk = raw.reshape(N, KB, 34)
+    zero8, zero2 = np.zeros(8, np.uint8), np.zeros(2, np.uint8)
+    for g in range(G):
+        for p in range(KP):
+            for l in range(64):
+                sub, r = l // 16, l % 16
+                for h in range(2):
+                    row, b = 16 * g + r, 2 * p + h
+                    want = blk[row, b, 2 + 8 * sub:10 + 8 * sub] if row < N and b < KB else zero8
+                    off = (g * KP + p) * 1024 + 16 * l + 8 * h
+                    assert np.array_equal(t[off:off + 8], want), (g, p, l, h)
+            for r in range(16):
+                for h in range(2):
+                    row, b = 16 * g + r, 2 * p + h
+                    want = blk[row, b, 0:2] if row < N and b < KB else zero2
+                    off = G * KP * 1024 + (g * KP + p) * 64 + 4 * r + 2 * h
+                    assert np.array_equal(t[off:off + 2], want), (g, p, r, h)
+    # a dropped or duplicated slot would break the round trip; a swapped pair of
+    # halves would break the loop check
+    bad = t.copy()
+    bad[8:16], bad[0:8] = t[0:8], t[8:16]
+    if not np.array_equal(t[0:8], t[8:16]):
+        assert not np.array_equal(untile_ref(bad, N, K), raw)
+
+
+def test_tile_validation_errors():
+    st = capi.tile_status
+    code, msg = st(None, FAKE, 16, 32, stream=0)
+    assert code == 1 and "w_q8_0 pointer" in msg
+    code, msg = st(FAKE, None, 16, 32, stream=0)
+    assert code == 1 and "w_tiled pointer" in msg
+    code, msg = st(FAKE, FAKE + 0x100000, 0, 32, stream=0)
+    assert code == 1 and "N must be positive" in msg
+    code, msg = st(FAKE, FAKE + 0x100000, 16, 48, stream=0)
+    assert code == 4 and "multiple of 32" in msg
+    code, msg = st(FAKE + 1, FAKE + 0x100000, 16, 32, stream=0)
+    assert code == 1 and "2-byte aligned" in msg
+    code, msg = st(FAKE, FAKE + 0x100008, 16, 32, stream=0)
+    assert code == 1 and "16-byte aligned" in msg
+    # 16 rows x 1 block: raw [FAKE, FAKE + 544), tiled 1088 bytes
+    code, msg = st(FAKE, FAKE + 512, 16, 32, stream=0)
+    assert code == 1 and "overlap" in msg
+    code, msg = capi.linear_tiled_status(FAKE, FAKE + 2, None, FAKE, 1, 16, 32, stream=0)
+    assert code == 1 and "16-byte aligned" in msg
+    code, msg = capi.linear_tiled_status(FAKE, FAKE, None, FAKE, 1, 16, 48, stream=0)
+    assert code == 4 and "multiple of 32" in msg
+    code, msg = capi.linear_swiglu_tiled_status(FAKE, FAKE, FAKE + 2, FAKE, 1, 16, 32, stream=0)
+    assert code == 1 and "16-byte aligned" in msg
+    code, msg = capi.linear_multi_status(FAKE, [FAKE, FAKE + 4], None, [FAKE, FAKE], [16, 16],
+                                         1, 32, stream=0, tiled=True)
+    assert code == 1 and "16-byte aligned" in msg
