@@ -12,8 +12,14 @@ M in {1, 4, 8}, the five Q8_0 Linears [4096->12288] QKV, [4096->4096] o_proj,
 timing.  Weights rotate over R copies of the set (R * 215 MB >= 1 GiB) so that no
 launch finds its weights in the 256 MB Infinity Cache.
 
+Weights in Q8_0 16-row tiles: each weight is repacked once at load time
+(mle_q8_0_tile, outside the timed region) into the tiled layout of include/mle_q8_0.h --
+the same 34 bytes per block, ordered so that every wave's weight load is one contiguous
+1 KB piece -- and the step runs mle_q8_0_linear_tiled.  The same step on the raw GGUF
+bytes (mle_q8_0_linear) is timed too and reported as raw_value / per_launch_raw.
+
 value = algorithmic bytes of all launches / wall time of the timed steps (GB/s), with
-algorithmic bytes per launch = N*(K/32)*34 + 4*M*K + 4*M*N.
+algorithmic bytes per launch = N*(K/32)*34 + 4*M*K + 4*M*N (either layout).
 
 Also reported: per-launch kernel durations (HIP events on the launch stream, >= 100
 launches each), the roofline of the dominant launch, the prefill GEMM of configs[2]
@@ -50,20 +56,33 @@ SEED_W = {"qkv": 21, "o_proj": 22, "gate": 23, "up": 24, "down": 25}
 # `bench.py --profile-kernel M,N,K` (FETCH_SIZE scaled by a device copy's read/write
 # ratio), keyed by (M, N, K); see profiles/gemv_q8_0_mfma_m8_4096x11008_traffic.txt and
 # profiles/gemv_q8_0_mfma_m8_12288x4096_traffic.txt.
-MEASURED_TRAFFIC = {(8, 4096, 11008): 57.236e6, (8, 12288, 4096): 61.745e6}
+MEASURED_TRAFFIC = {("raw", 8, 4096, 11008): 57.236e6, ("raw", 8, 12288, 4096): 61.745e6}
 
 
 def gemv_bytes(M, N, K):
     return N * (K // 32) * 34 + 4 * M * K + 4 * M * N
 
 
-def decode_kernel_name(M):
-    """Kernel the C ABI runs for an M-token Linear (mle_q8_0_linear's path choice)."""
-    if M == 1:
+def decode_kernel_name(M, layout="raw"):
+    """Kernel the C ABI runs for an M-token Linear (mle_q8_0_linear[_tiled] path choice)."""
+    if M == 1 and layout == "raw":
         return "gemv_q8_0_kernel (FP32 GEMV)"
     if M < 64:
-        return "gemv_q8_0_mfma_kernel (MFMA decode, exact bf16 activation split)"
+        return ("gemv_q8_0_mfma_kernel (MFMA decode, exact bf16 activation split"
+                + (", tiled weights)" if layout == "tiled" else ")"))
     return "gemm_q8_0_mfma_kernel (bf16 MFMA GEMM)"
+
+
+def tiled_copy(capi, w, N, K, stream):
+    """Device repack of a raw Q8_0 weight [N,K] into 16-row tiles."""
+    import torch
+    t = torch.empty(capi.tiled_bytes(N, K), dtype=torch.uint8, device=w.device)
+    capi.tile(w, t, N, K, stream=stream)
+    return t
+
+
+def linear_fn(capi, layout):
+    return capi.linear_tiled if layout == "tiled" else capi.linear
 
 
 def parse():
@@ -76,10 +95,11 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true",
                    help="skip the prefill and embedding figures")
-    p.add_argument("--profile-kernel", default=None, metavar="M,N,K",
+    p.add_argument("--profile-kernel", default=None, metavar="M,N,K[,tiled]",
                    help="counter-collection mode: run only the decode Linear of this shape "
-                        "200 times (rotating weight copies) and a 256 MiB device copy used "
-                        "to calibrate FETCH_SIZE / WRITE_SIZE, then exit")
+                        "(raw weights, or tiled with a 4th field 'tiled') 200 times (rotating "
+                        "weight copies) and a 256 MiB device copy used to calibrate "
+                        "FETCH_SIZE / WRITE_SIZE, then exit")
     return p.parse_args()
 
 
@@ -88,23 +108,28 @@ def profile_kernel(spec):
     import torch
     from llmengine_amd import capi
     from llmengine_amd import synthetic as S
-    M, N, K = (int(v) for v in spec.split(","))
+    fields = spec.split(",")
+    M, N, K = (int(v) for v in fields[:3])
+    layout = "tiled" if len(fields) > 3 and fields[3] == "tiled" else "raw"
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     w = torch.from_numpy(S.q8_0_weight(7, N, K)[0]).to(dev)
+    if layout == "tiled":
+        w = tiled_copy(capi, w, N, K, stream)
     R = max(2, -(-ROTATE_BYTES // w.numel()) + 1)
     ws = [w] + [w.clone() for _ in range(R - 1)]
     x = torch.from_numpy(S.activations(8, (M, K))).to(dev)
     y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    lin = linear_fn(capi, layout)
     for j in range(200):
-        capi.linear(x, ws[j % R], None, y, M, N, K, stream=stream)
+        lin(x, ws[j % R], None, y, M, N, K, stream=stream)
     torch.cuda.synchronize()
     src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(10):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"profiled": {"M": M, "N": N, "K": K, "launches": 200,
+    print(json.dumps({"profiled": {"M": M, "N": N, "K": K, "layout": layout, "launches": 200,
                                    "bytes_per_launch": gemv_bytes(M, N, K),
                                    "calibration_copy_bytes": src.numel() * 4}}), flush=True)
 
@@ -154,12 +179,14 @@ def main():
     # ---- inputs, resident in HBM before timing
     set_bytes = sum(S.weight_bytes(N, K) for _, N, K in LLAMA_SET)
     R = max(2, -(-ROTATE_BYTES // set_bytes) + 1)
-    weights_host, wdev = {}, {}
+    weights_host, wdev, tdev = {}, {}, {}
     for name, N, K in LLAMA_SET:
         w, _, _ = S.q8_0_weight(SEED_W[name], N, K)
         weights_host[name] = w
         base = torch.from_numpy(w).to(dev)
         wdev[name] = [base] + [base.clone() for _ in range(R - 1)]
+        tdev[name] = [tiled_copy(capi, c, N, K, stream) for c in wdev[name]]
+    wsets = {"tiled": tdev, "raw": wdev}
     xs_host, xdev, ydev = {}, {}, {}
     for M in MS:
         for K in (4096, 11008):
@@ -171,57 +198,67 @@ def main():
 
     step_bytes = sum(gemv_bytes(M, N, K) for M in MS for _, N, K in LLAMA_SET)
 
-    def step(i):
+    def step(i, layout):
+        lin, ws = linear_fn(capi, layout), wsets[layout]
         for mi, M in enumerate(MS):
             c = (i * len(MS) + mi) % R
             for name, N, K in LLAMA_SET:
-                capi.linear(xdev[(M, K)], wdev[name][c], None, ydev[(M, name)], M, N, K,
-                            stream=stream)
+                lin(xdev[(M, K)], ws[name][c], None, ydev[(M, name)], M, N, K, stream=stream)
 
-    # ---- timed steps
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for i in range(args.steps):
-        step(args.warmup + i)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = ev0.elapsed_time(ev1)
-    elapsed = max(wall, gpu_ms / 1e3)
-    value = step_bytes * args.steps / elapsed / 1e9
+    # ---- timed steps (tiled weights: the headline value; raw GGUF bytes beside it)
+    timing = {}
+    for layout in ("tiled", "raw"):
+        for i in range(args.warmup):
+            step(i, layout)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for i in range(args.steps):
+            step(args.warmup + i, layout)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        gpu_ms = ev0.elapsed_time(ev1)
+        elapsed_l = max(wall, gpu_ms / 1e3)
+        timing[layout] = (elapsed_l, step_bytes * args.steps / elapsed_l / 1e9)
+    elapsed, value = timing["tiled"]
+    raw_elapsed, raw_value = timing["raw"]
 
     # ---- per-launch kernel durations (events around back-to-back launches)
-    per_launch = []
-    for M in MS:
-        for name, N, K in LLAMA_SET:
-            for j in range(3):  # warm
-                capi.linear(xdev[(M, K)], wdev[name][j % R], None, ydev[(M, name)], M, N, K,
-                            stream=stream)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for j in range(args.launch_iters):
-                capi.linear(xdev[(M, K)], wdev[name][j % R], None, ydev[(M, name)], M, N, K,
-                            stream=stream)
-            b.record(stream)
-            torch.cuda.synchronize()
-            us = a.elapsed_time(b) * 1e3 / args.launch_iters
-            nbytes = gemv_bytes(M, N, K)
-            per_launch.append({"M": M, "op": name, "N": N, "K": K, "us": round(us, 3),
-                               "GBps": round(nbytes / us / 1e3, 1),
-                               "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+    def launches(layout):
+        lin, ws = linear_fn(capi, layout), wsets[layout]
+        rows = []
+        for M in MS:
+            for name, N, K in LLAMA_SET:
+                for j in range(3):  # warm
+                    lin(xdev[(M, K)], ws[name][j % R], None, ydev[(M, name)], M, N, K,
+                        stream=stream)
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                for j in range(args.launch_iters):
+                    lin(xdev[(M, K)], ws[name][j % R], None, ydev[(M, name)], M, N, K,
+                        stream=stream)
+                b.record(stream)
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / args.launch_iters
+                nbytes = gemv_bytes(M, N, K)
+                rows.append({"M": M, "op": name, "N": N, "K": K, "us": round(us, 3),
+                             "GBps": round(nbytes / us / 1e3, 1),
+                             "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+        return rows
+
+    per_launch = launches("tiled")
+    per_launch_raw = launches("raw")
     dom = max(per_launch, key=lambda r: r["us"])
     dom_bytes = gemv_bytes(dom["M"], dom["N"], dom["K"])
     achieved = dom_bytes / dom["us"] / 1e3
-    traffic = MEASURED_TRAFFIC.get((dom["M"], dom["N"], dom["K"]))
+    traffic = MEASURED_TRAFFIC.get(("tiled", dom["M"], dom["N"], dom["K"]))
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": int(traffic) if traffic else None,
                 "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE)",
-                "kernel": f"{decode_kernel_name(dom['M'])} M={dom['M']} {dom['op']} "
+                "kernel": f"{decode_kernel_name(dom['M'], 'tiled')} M={dom['M']} {dom['op']} "
                           f"[{dom['N']}x{dom['K']}]",
                 "bytes_per_launch": dom_bytes, "us_per_launch": dom["us"]}
 
@@ -229,25 +266,27 @@ def main():
     if not args.no_extras:
         # ---- prefill GEMM, configs[2]: M=512 on the bf16 MFMA path
         pre = []
-        for name, N, K in (("gate", 11008, 4096), ("down", 4096, 11008)):
-            M = 512
-            x = torch.from_numpy(S.activations(2000 + K, (M, K))).to(dev)
-            y = torch.empty((M, N), dtype=torch.float32, device=dev)
-            for j in range(3):
-                capi.linear(x, wdev[name][j % R], None, y, M, N, K, stream=stream)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            iters = 40
-            a.record(stream)
-            for j in range(iters):
-                capi.linear(x, wdev[name][j % R], None, y, M, N, K, stream=stream)
-            b.record(stream)
-            torch.cuda.synchronize()
-            us = a.elapsed_time(b) * 1e3 / iters
-            tflops = 2.0 * M * N * K / us / 1e6
-            pre.append({"M": M, "N": N, "K": K, "us": round(us, 2),
-                        "TFLOPs": round(tflops, 1),
-                        "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                        "note": "per call: X->bf16 fragment pre-pass + GEMM kernel"})
+        for layout in ("tiled", "raw"):
+            lin, ws = linear_fn(capi, layout), wsets[layout]
+            for name, N, K in (("gate", 11008, 4096), ("down", 4096, 11008)):
+                M = 512
+                x = torch.from_numpy(S.activations(2000 + K, (M, K))).to(dev)
+                y = torch.empty((M, N), dtype=torch.float32, device=dev)
+                for j in range(3):
+                    lin(x, ws[name][j % R], None, y, M, N, K, stream=stream)
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                iters = 40
+                a.record(stream)
+                for j in range(iters):
+                    lin(x, ws[name][j % R], None, y, M, N, K, stream=stream)
+                b.record(stream)
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / iters
+                tflops = 2.0 * M * N * K / us / 1e6
+                pre.append({"M": M, "N": N, "K": K, "layout": layout, "us": round(us, 2),
+                            "TFLOPs": round(tflops, 1),
+                            "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                            "note": "per call: X->bf16 fragment pre-pass + GEMM kernel"})
         extras["prefill"] = pre
         # ---- embedding gather, configs[4]
         V, H, T = 151936, 896, 8 * 512
@@ -280,23 +319,30 @@ def main():
                                ("lm_head", 151936, 896, (1, 8))):
             wq = torch.from_numpy(S.q8_0_weight(3000 + N, N, K)[0]).to(dev)
             Rq = max(2, -(-ROTATE_BYTES // wq.numel()) + 1)
-            wqs = [wq] + [wq.clone() for _ in range(Rq - 1)]
+            wqs = {"raw": [wq] + [wq.clone() for _ in range(Rq - 1)]}
+            wqs["tiled"] = [tiled_copy(capi, c, N, K, stream) for c in wqs["raw"]]
             for M in Ms:
                 x = torch.from_numpy(S.activations(3100 + K, (M, K))).to(dev)
                 y = torch.empty((M, N), dtype=torch.float32, device=dev)
-                for j in range(Rq):  # touch every copy once (first-use page mapping)
-                    capi.linear(x, wqs[j], None, y, M, N, K, stream=stream)
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                iters = 100
-                a.record(stream)
-                for j in range(iters):
-                    capi.linear(x, wqs[j % Rq], None, y, M, N, K, stream=stream)
-                b.record(stream)
-                torch.cuda.synchronize()
-                us = a.elapsed_time(b) * 1e3 / iters
-                gb = gemv_bytes(M, N, K) / us / 1e3
-                qwen.append({"op": name, "M": M, "N": N, "K": K, "us": round(us, 2),
-                             "GBps": round(gb, 1), "frac_hbm": round(gb / HBM_PEAK_GBS, 4)})
+                row = {"op": name, "M": M, "N": N, "K": K}
+                for layout in ("tiled", "raw"):
+                    lin = linear_fn(capi, layout)
+                    for j in range(Rq):  # touch every copy once (first-use page mapping)
+                        lin(x, wqs[layout][j], None, y, M, N, K, stream=stream)
+                    a, b = (torch.cuda.Event(enable_timing=True),
+                            torch.cuda.Event(enable_timing=True))
+                    iters = 100
+                    a.record(stream)
+                    for j in range(iters):
+                        lin(x, wqs[layout][j % Rq], None, y, M, N, K, stream=stream)
+                    b.record(stream)
+                    torch.cuda.synchronize()
+                    us = a.elapsed_time(b) * 1e3 / iters
+                    gb = gemv_bytes(M, N, K) / us / 1e3
+                    sfx = "" if layout == "tiled" else "_raw"
+                    row.update({"us" + sfx: round(us, 2), "GBps" + sfx: round(gb, 1),
+                                "frac_hbm" + sfx: round(gb / HBM_PEAK_GBS, 4)})
+                qwen.append(row)
             del wqs
         extras["qwen_lm_head"] = qwen
 
@@ -323,16 +369,22 @@ def main():
             iters = 40 if M >= 64 else 100
             tf = timed(lambda j: capi.linear_swiglu(x, gw[j % R], uw[j % R], y, M, N, K,
                                                     stream=stream), iters)
+            tgw, tuw = tdev["gate"], tdev["up"]
+            tft = timed(lambda j: capi.linear_swiglu_tiled(x, tgw[j % R], tuw[j % R], y, M, N,
+                                                           K, stream=stream), iters)
             ts = timed(lambda j: (capi.linear(x, gw[j % R], None, y, M, N, K, stream=stream),
                                   capi.linear(x, uw[j % R], None, g2, M, N, K,
                                               stream=stream)), iters)
             nb = 2 * gemv_bytes(M, N, K) - 4 * M * K - 4 * M * N
             fused.append({"op": "gate+up -> SwiGLU [2 x 11008x4096]", "M": M,
                           "us_fused": round(tf, 2), "us_two_linears": round(ts, 2),
-                          "GBps_fused": round(nb / tf / 1e3, 1)})
+                          "GBps_fused": round(nb / tf / 1e3, 1),
+                          "us_fused_tiled": round(tft, 2),
+                          "GBps_fused_tiled": round(nb / tft / 1e3, 1)})
         qkv = [torch.from_numpy(S.q8_0_weight(40 + i, 4096, 4096)[0]).to(dev) for i in range(3)]
         Rq = max(2, -(-ROTATE_BYTES // (3 * qkv[0].numel())) + 1)  # past the Infinity Cache
         qkv_r = [qkv] + [[w.clone() for w in qkv] for _ in range(Rq - 1)]
+        qkv_t = [[tiled_copy(capi, w, 4096, 4096, stream) for w in ws3] for ws3 in qkv_r]
         for M in (1, 4, 8):
             x = xdev[(M, 4096)]
             ys = [torch.empty((M, 4096), dtype=torch.float32, device=dev) for _ in range(3)]
@@ -340,12 +392,17 @@ def main():
                                                    4096, stream=stream), 100)
             ts = timed(lambda j: [capi.linear(x, qkv_r[j % Rq][i], None, ys[i], M, 4096, 4096,
                                               stream=stream) for i in range(3)], 100)
+            tft = timed(lambda j: capi.linear_multi_tiled(x, qkv_t[j % Rq], None, ys,
+                                                          (4096,) * 3, M, 4096, stream=stream),
+                        100)
             nb = 3 * gemv_bytes(M, 4096, 4096) - 2 * 4 * M * 4096
             fused.append({"op": "q,k,v multi-output [3 x 4096x4096]", "M": M,
                           "us_fused": round(tf, 2), "us_three_linears": round(ts, 2),
-                          "GBps_fused": round(nb / tf / 1e3, 1)})
+                          "GBps_fused": round(nb / tf / 1e3, 1),
+                          "us_fused_tiled": round(tft, 2),
+                          "GBps_fused_tiled": round(nb / tft / 1e3, 1)})
         extras["fused"] = fused
-        del qkv, qkv_r
+        del qkv, qkv_r, qkv_t
 
         # ---- greedy pick over lm_head logits: device argmax vs copying the row back
         V = 151936
@@ -387,11 +444,16 @@ def main():
         "config": {"workload": "configs[1]: Llama-7B decode Q8_0 Linear set, M in {1,4,8} x "
                                "{QKV 4096->12288, o_proj 4096->4096, gate/up 4096->11008, "
                                "down 11008->4096}, 15 launches per step",
+                   "weights": "Q8_0 16-row tiles (repacked once at load, 34 B per block as "
+                              "raw); raw GGUF layout in raw_value / per_launch_raw",
                    "rotated_weight_copies": R, "bytes_per_step": step_bytes,
                    "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "raw_value": round(raw_value, 1),
+        "raw_ms_per_step": round(raw_elapsed * 1e3 / args.steps, 4),
         "per_launch": per_launch,
+        "per_launch_raw": per_launch_raw,
     }
     line.update(extras)
     print(json.dumps(line), flush=True)

@@ -656,7 +656,17 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
   const int KB = K / kBlockElems;
   c.kslice = (c.mt <= 8 && KB <= 32) ? 32 : 16;
   if (layout == WeightLayout::kTiled) {
-    c.waves = N >= 4096 ? 8 : N >= 2048 ? 4 : 2;
+    // Tiled weights (MI355X sweep over the Llama-7B and Qwen2.5-0.5B projections
+    // and the Qwen lm_head, M = 1..16): short rows (one 32-block slice) run best
+    // in 4-wave workgroups, except at 16 tokens and for a vocabulary-sized
+    // weight from 8 tokens (lm_head M = 8: 33.0 us vs 38.4); long rows in 8-wave
+    // workgroups, except 4 for 12288+ outputs at 8 tokens (fused q/k/v 15.9 us
+    // vs 16.6, gate/up 24.1 vs 24.3).  The K slice follows the raw rule, so raw
+    // and tiled launches accumulate in the same order.
+    if (KB <= 32)
+      c.waves = (c.mt >= 16 || (c.mt >= 8 && N >= 65536)) ? 8 : 4;
+    else
+      c.waves = (c.mt == 8 && N >= 12288) ? 4 : 8;
     return c;
   }
   c.waves = (c.mt >= 4 && N >= 8192) ? 8 : 4;
