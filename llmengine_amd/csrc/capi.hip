@@ -159,8 +159,10 @@ struct Tune {
   mle::GemmConfig gemm{0, 0, 0};  // 0 fields = automatic
 };
 
-// Tiled weights (mle::WeightLayout::kTiled) take the MFMA decode for every
-// M < 64 (there is no tiled FP32 GEMV) and the MFMA GEMM from 64 tokens.
+// Tiled weights (mle::WeightLayout::kTiled): the tiled FP32 GEMV where
+// mle::gemv_tiled_wins (one token; two below vocabulary-sized outputs; up to
+// four on short rows), else the MFMA decode below 64 tokens and the MFMA GEMM
+// from 64.
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
                int N, int K, int path, const Tune& tune, hipStream_t stream,
                mle::WeightLayout layout = mle::WeightLayout::kRaw) {
@@ -177,6 +179,11 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
   mle::LinearSegs one;
   one.seg[0] = mle::LinearSeg{w, bias, y, N};
   one.layout = layout;
+  if (tiled && path == 3 && M <= 4 && mle::gemv_tiled_wins(M, N, K)) {
+    const mle::TiledGemvConfig c = mle::gemv_tiled_pick(M, N, K, false);
+    return check_launch(mle::launch_gemv_tiled_segs(c, x, one, M, K, stream),
+                        "hip sgemm_nt Q8_0 launch failed");
+  }
   if (path == 2) {
     mle::GemmConfig c = mle::gemm_mfma_pick(M, N, K);
     if (tune.gemm.bm) c.bm = tune.gemm.bm;
@@ -254,6 +261,12 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
                         "hip Q8_0 fused Linear launch failed");
   }
   const bool tiled = s.layout == mle::WeightLayout::kTiled;
+  const int rows = swi ? s.seg[0].N : total_n;
+  if (tiled && M <= 4 && mle::gemv_tiled_wins(M, rows, K)) {
+    const mle::TiledGemvConfig c = mle::gemv_tiled_pick(M, rows, K, swi);
+    return check_launch(mle::launch_gemv_tiled_segs(c, x, s, M, K, stream),
+                        "hip Q8_0 fused Linear launch failed");
+  }
   if (!tiled && (swi ? M == 1 : pick_path(M, total_n, K) == 1)) {
     const mle::GemvConfig c = mle::gemv_pick_config(M, total_n, K);
     return check_launch(mle::launch_gemv_segs(c, x, s, M, K, stream),

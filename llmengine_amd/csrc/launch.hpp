@@ -80,6 +80,21 @@ struct LinearSegs {
   Epilogue mode = Epilogue::kPlain;
   WeightLayout layout = WeightLayout::kRaw;
 };
+// FP32 GEMV on kTiled weights (M <= 4 tokens per launch): a workgroup per
+// 16-row group, its waves splitting K in chunks of `ppw` block pairs.
+struct TiledGemvConfig {
+  int mt;   // token tile: 1, 2 or 4 (>= M)
+  int ppw;  // block pairs per wave chunk: 4, 8 or 16
+  int wpg;  // waves per weight in a workgroup (SwiGLU: 2 wpg waves), <= 16 in all
+};
+TiledGemvConfig gemv_tiled_pick(int M, int rows, int K, bool swiglu);
+// Whether an M-token launch of `rows` output rows on tiled weights takes this
+// GEMV rather than the MFMA decode.
+bool gemv_tiled_wins(int M, int rows, int K);
+bool gemv_tiled_config_valid(const TiledGemvConfig& c, bool swiglu);
+hipError_t launch_gemv_tiled_segs(const TiledGemvConfig& c, const float* x,
+                                  const LinearSegs& s, int M, int K, hipStream_t stream);
+
 // Raw Q8_0 [N, K] -> kTiled (one pass; `tiled` holds tiled_bytes(N, K)).
 hipError_t launch_tile_q8_0(const uint8_t* raw, uint8_t* tiled, int N, int K,
                             hipStream_t stream);
