@@ -54,9 +54,12 @@ SEED_W = {"qkv": 21, "o_proj": 22, "gate": 23, "up": 24, "down": 25}
 
 # HBM bytes per dispatch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on
 # `bench.py --profile-kernel M,N,K` (FETCH_SIZE scaled by a device copy's read/write
-# ratio), keyed by (M, N, K); see profiles/gemv_q8_0_mfma_m8_4096x11008_traffic.txt and
-# profiles/gemv_q8_0_mfma_m8_12288x4096_traffic.txt.
-MEASURED_TRAFFIC = {("raw", 8, 4096, 11008): 57.236e6, ("raw", 8, 12288, 4096): 61.745e6}
+# ratio), keyed by (layout, M, N, K); see profiles/gemv_q8_0_mfma_tiled_m8_4096x11008_traffic.txt,
+# profiles/gemv_q8_0_mfma_tiled_m8_12288x4096_traffic.txt, profiles/gemv_tiled_m1_4096x11008_traffic.txt
+# and the raw-layout profiles/gemv_q8_0_mfma_m8_*_traffic.txt.
+MEASURED_TRAFFIC = {("raw", 8, 4096, 11008): 57.236e6, ("raw", 8, 12288, 4096): 61.745e6,
+                    ("tiled", 8, 4096, 11008): 56.736e6, ("tiled", 8, 12288, 4096): 61.374e6,
+                    ("tiled", 1, 4096, 11008): 48.306e6}
 
 
 def gemv_bytes(M, N, K):
