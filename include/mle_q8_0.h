@@ -20,7 +20,8 @@
  *     2 OutOfRange, 3 ShapeMismatch, 4 Unsupported, 6 RuntimeError.  The
  *     message of the last failure on the calling thread is mle_last_error().
  *   - Alignment: fp32 activation/output buffers must be 16-byte aligned (any
- *     hipMalloc'd buffer is), Q8_0 buffers 2-byte aligned, ids 4-byte aligned.
+ *     hipMalloc'd buffer is), Q8_0 buffers 2-byte aligned (16-byte for weights in
+ *     16-row tiles, mle_q8_0_tile), ids 4-byte aligned.
  */
 #ifndef MLE_Q8_0_H
 #define MLE_Q8_0_H
@@ -196,11 +197,14 @@ int mle_top_tokens_f32(const float* logits, int rows, int n, int top_n, float te
  *   Errors: NULL pointers, N or K <= 0, misalignment, overlap ->
  *   InvalidArgument; K % 32 != 0 -> Unsupported.
  * mle_q8_0_linear_tiled / _swiglu_tiled / _multi_tiled: mle_q8_0_linear /
- *   _swiglu / _multi on tiled weights (16-byte aligned), same errors.  M >= 64
- *   runs the bf16-MFMA GEMM and M < 64 the MFMA decode with FP32-exact
- *   activations, each bit-identical to the raw entry point on the same path
- *   (the raw entry point's FP32 GEMV cases, M == 1 and short rows at M <= 4,
- *   agree with it to about 1e-7 relative L2).
+ *   _swiglu / _multi on tiled weights (16-byte aligned), same errors.  Paths:
+ *   an FP32 GEMV for M == 1, M == 2 below 65536 output rows and M <= 4 with
+ *   K <= 1024 and at most 32768 output rows (the K split stays inside a
+ *   workgroup: no workspace); otherwise the MFMA decode (M < 64) and the bf16
+ *   MFMA GEMM (M >= 64), each bit-identical to the raw entry point on the same
+ *   path.  Where one side runs an FP32 GEMV the two agree to about 1e-7
+ *   relative L2; a fused multi-output launch on the GEMV agrees with the single
+ *   tiled Linear to fp32 rounding (its K split follows the launch shape).
  */
 size_t mle_q8_0_tiled_bytes(int N, int K);
 int mle_q8_0_tile(const uint8_t* w_q8_0, uint8_t* w_tiled, int N, int K, hipStream_t stream);
