@@ -123,6 +123,22 @@ class HipExecutor final : public Executor {
   size_t fused_groups() const;
   size_t fused_launches() const { return fused_launches_; }
 
+  // Weights in Q8_0 16-row tiles (no counterpart in the reference executor; a
+  // loader step): makes a tiled copy (mle_q8_0_tile, on this executor's stream)
+  // of every Q8_0 Linear weight of the compiled graph bound in `ctx` on a HIP
+  // device, once per weight buffer.  Later runs give those Linears (and their
+  // fused groups) the tiled copy while the same buffer stays bound; a node
+  // whose bound weight buffer has no copy runs on the raw bytes.  The copies
+  // live until release_tiled_weights() or the executor's destruction; call
+  // again after overwriting a bound weight in place.  Memory: one more copy of
+  // each Linear weight (the raw buffer stays with the caller).
+  Status tile_weights(RuntimeContext& ctx);
+  void release_tiled_weights();
+  size_t tiled_weights() const { return tiled_.size(); }
+  // Linear launches of the last run that read a tiled copy.
+  size_t tiled_launches() const { return tiled_launches_; }
+  ~HipExecutor() override;
+
  private:
   struct Step {
     enum Kind { kNode, kSwiGLU, kMulti } kind;
@@ -137,7 +153,10 @@ class HipExecutor final : public Executor {
   std::vector<Step> plan_;
   bool fusion_{true};
   size_t fused_launches_{0};
+  size_t tiled_launches_{0};
   hipStream_t stream_;
+  std::unordered_map<const void*, const uint8_t*> tiled_;  // raw buffer -> tiled copy
+  std::vector<void*> tiled_bufs_;
 };
 
 // Registers the HIP Q8_0 kernels (Embedding, Linear, MatMul) under
@@ -166,6 +185,19 @@ Status linear_swiglu(const float* x, const uint8_t* w_gate_q8_0, const uint8_t* 
 Status linear_multi(const float* x, int count, const uint8_t* const* w_q8_0,
                     const float* const* bias, float* const* y, const int* N, int M, int K,
                     hipStream_t stream = nullptr);
+// Weights in Q8_0 16-row tiles (mle_q8_0_tile / mle_q8_0_*_tiled; no
+// counterpart in the reference).
+size_t q8_0_tiled_bytes(int N, int K);
+Status tile_q8_0(const uint8_t* w_q8_0, uint8_t* w_tiled, int N, int K,
+                 hipStream_t stream = nullptr);
+Status sgemm_nt_tiled(const float* A, const uint8_t* B_tiled, float* C, int M, int N, int K,
+                      const float* bias = nullptr, hipStream_t stream = nullptr);
+Status linear_swiglu_tiled(const float* x, const uint8_t* w_gate_tiled,
+                           const uint8_t* w_up_tiled, float* y, int M, int N, int K,
+                           hipStream_t stream = nullptr);
+Status linear_multi_tiled(const float* x, int count, const uint8_t* const* w_tiled,
+                          const float* const* bias, float* const* y, const int* N, int M,
+                          int K, hipStream_t stream = nullptr);
 Status argmax(const float* logits, int rows, int n, int32_t* idx, float* val = nullptr,
               hipStream_t stream = nullptr);
 // Sampler::get_top_tokens (sampler.cpp:141-197) on the device: ids / probs

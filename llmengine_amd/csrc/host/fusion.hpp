@@ -2,21 +2,38 @@
 // (internal to the host runtime).
 #pragma once
 
+#include <unordered_map>
 #include <vector>
 
 #include "minillm_hip/runtime.h"
 
 namespace minillm::detail {
 
-// Linear(gate) + Linear(up) + SwiGLU as one mle_q8_0_linear_swiglu launch.
-// Returns false (nothing launched) when the bound tensors do not fit the fused
-// kernel (then the nodes run one by one and report their own errors).
-expected<bool, Status> run_fused_swiglu(const Node& gate, const Node& up, const Node& sw,
-                                        RuntimeContext& ctx);
+// Raw Q8_0 weight buffer (device pointer) -> its copy in 16-row tiles.
+using TiledWeights = std::unordered_map<const void*, const uint8_t*>;
 
-// 2 or 3 Linear nodes on one input as one mle_q8_0_linear_multi launch; same
-// return convention.
+// One Linear node on the tiled copy of its weight (mle_q8_0_linear_tiled).
+// Returns false (nothing launched) when the node's operands do not validate or
+// its weight has no tiled copy; the node then runs through its registered
+// kernel, which reports the reference's errors.
+expected<bool, Status> run_tiled_linear(const Node& node, RuntimeContext& ctx,
+                                        const TiledWeights& tiled);
+
+// Linear(gate) + Linear(up) + SwiGLU as one mle_q8_0_linear_swiglu launch
+// (the _tiled one when `tiled` holds copies of both weights; *used_tiled says
+// which ran).  Returns false
+// (nothing launched) when the bound tensors do not fit the fused kernel (then
+// the nodes run one by one and report their own errors).
+expected<bool, Status> run_fused_swiglu(const Node& gate, const Node& up, const Node& sw,
+                                        RuntimeContext& ctx,
+                                        const TiledWeights* tiled = nullptr,
+                                        bool* used_tiled = nullptr);
+
+// 2 or 3 Linear nodes on one input as one mle_q8_0_linear_multi launch (the
+// _tiled one when `tiled` holds copies of every weight); same return convention.
 expected<bool, Status> run_fused_multi(const std::vector<const Node*>& nodes,
-                                       RuntimeContext& ctx);
+                                       RuntimeContext& ctx,
+                                       const TiledWeights* tiled = nullptr,
+                                       bool* used_tiled = nullptr);
 
 }  // namespace minillm::detail

@@ -358,12 +358,57 @@ Status top_tokens(const float* logits, int rows, int n, int top_n, float tempera
   return from_capi(mle_top_tokens_f32(logits, rows, n, top_n, temperature, ids, probs, stream));
 }
 
+size_t q8_0_tiled_bytes(int N, int K) { return mle_q8_0_tiled_bytes(N, K); }
+
+Status tile_q8_0(const uint8_t* w_q8_0, uint8_t* w_tiled, int N, int K, hipStream_t stream) {
+  return from_capi(mle_q8_0_tile(w_q8_0, w_tiled, N, K, stream));
+}
+
+Status sgemm_nt_tiled(const float* A, const uint8_t* B_tiled, float* C, int M, int N, int K,
+                      const float* bias, hipStream_t stream) {
+  return from_capi(mle_q8_0_linear_tiled(A, B_tiled, bias, C, M, N, K, stream));
+}
+
+Status linear_swiglu_tiled(const float* x, const uint8_t* w_gate_tiled,
+                           const uint8_t* w_up_tiled, float* y, int M, int N, int K,
+                           hipStream_t stream) {
+  return from_capi(
+      mle_q8_0_linear_swiglu_tiled(x, w_gate_tiled, w_up_tiled, y, M, N, K, stream));
+}
+
+Status linear_multi_tiled(const float* x, int count, const uint8_t* const* w_tiled,
+                          const float* const* bias, float* const* y, const int* N, int M,
+                          int K, hipStream_t stream) {
+  return from_capi(mle_q8_0_linear_multi_tiled(x, count, w_tiled, bias, y, N, M, K, stream));
+}
+
 }  // namespace hip
 
 namespace detail {
 
+namespace {
+const uint8_t* tiled_copy(const TiledWeights* tiled, const void* raw) {
+  if (tiled == nullptr) return nullptr;
+  auto it = tiled->find(raw);
+  return it == tiled->end() ? nullptr : it->second;
+}
+}  // namespace
+
+expected<bool, Status> run_tiled_linear(const Node& node, RuntimeContext& ctx,
+                                        const TiledWeights& tiled) {
+  auto o = linear_operands(node, ctx);
+  if (!o) return false;
+  const uint8_t* t = tiled_copy(&tiled, o->w);
+  if (t == nullptr) return false;
+  const Status st = hip::sgemm_nt_tiled(o->x, t, o->y, o->M, o->N, o->K, o->bias,
+                                        ctx.hip_stream());
+  if (!st.ok()) return unexpected(st);
+  return true;
+}
+
 expected<bool, Status> run_fused_swiglu(const Node& gate, const Node& up, const Node& sw,
-                                        RuntimeContext& ctx) {
+                                        RuntimeContext& ctx, const TiledWeights* tiled,
+                                        bool* used_tiled) {
   auto g = linear_operands(gate, ctx);
   auto u = linear_operands(up, ctx);
   if (!g || !u || g->bias || u->bias || g->x != u->x || g->M != u->M || g->N != u->N ||
@@ -373,14 +418,21 @@ expected<bool, Status> run_fused_swiglu(const Node& gate, const Node& up, const 
   if (!ot || !check_hip_float(ot, "output").ok() ||
       !check_storage_bytes(ot, static_cast<size_t>(g->M) * g->N * 4, "output").ok())
     return false;
-  const Status st = hip::linear_swiglu(g->x, g->w, u->w, static_cast<float*>(ot->data()), g->M,
-                                       g->N, g->K, ctx.hip_stream());
+  const uint8_t* tg = tiled_copy(tiled, g->w);
+  const uint8_t* tu = tiled_copy(tiled, u->w);
+  if (used_tiled) *used_tiled = tg && tu;
+  const Status st =
+      tg && tu ? hip::linear_swiglu_tiled(g->x, tg, tu, static_cast<float*>(ot->data()), g->M,
+                                          g->N, g->K, ctx.hip_stream())
+               : hip::linear_swiglu(g->x, g->w, u->w, static_cast<float*>(ot->data()), g->M,
+                                    g->N, g->K, ctx.hip_stream());
   if (!st.ok()) return unexpected(st);
   return true;
 }
 
 expected<bool, Status> run_fused_multi(const std::vector<const Node*>& nodes,
-                                       RuntimeContext& ctx) {
+                                       RuntimeContext& ctx, const TiledWeights* tiled,
+                                       bool* used_tiled) {
   if (nodes.size() < 2 || nodes.size() > 3) return false;
   const uint8_t* w[3];
   const float* b[3];
@@ -397,8 +449,18 @@ expected<bool, Status> run_fused_multi(const std::vector<const Node*>& nodes,
     y[i] = o->y;
     N[i] = o->N;
   }
-  const Status st = hip::linear_multi(first.x, static_cast<int>(nodes.size()), w, b, y, N,
-                                      first.M, first.K, ctx.hip_stream());
+  const uint8_t* tw[3] = {nullptr, nullptr, nullptr};
+  bool all_tiled = true;
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    tw[i] = tiled_copy(tiled, w[i]);
+    all_tiled = all_tiled && tw[i] != nullptr;
+  }
+  if (used_tiled) *used_tiled = all_tiled;
+  const Status st =
+      all_tiled ? hip::linear_multi_tiled(first.x, static_cast<int>(nodes.size()), tw, b, y, N,
+                                          first.M, first.K, ctx.hip_stream())
+                : hip::linear_multi(first.x, static_cast<int>(nodes.size()), w, b, y, N,
+                                    first.M, first.K, ctx.hip_stream());
   if (!st.ok()) return unexpected(st);
   return true;
 }

@@ -2,6 +2,7 @@
 // (see include/minillm_hip/runtime.h).
 #include "minillm_hip/runtime.h"
 
+#include <climits>
 #include <map>
 #include <unordered_map>
 #include <unordered_set>
@@ -113,6 +114,51 @@ Status RuntimeContext::advance_kv_cache_step() { return Status::make_ok(); }
 HipExecutor::HipExecutor(std::shared_ptr<Backend> backend, KernelRegistry& registry,
                          hipStream_t stream)
     : backend_(std::move(backend)), registry_(registry), stream_(stream) {}
+
+HipExecutor::~HipExecutor() { release_tiled_weights(); }
+
+void HipExecutor::release_tiled_weights() {
+  if (!tiled_bufs_.empty()) (void)hipStreamSynchronize(stream_);  // launches may still read them
+  for (void* p : tiled_bufs_) (void)hipFree(p);
+  tiled_bufs_.clear();
+  tiled_.clear();
+}
+
+Status HipExecutor::tile_weights(RuntimeContext& ctx) {
+  if (!graph_) return Status::runtime_error("executor not compiled");
+  // Overwritten weights get fresh copies: drop the old ones first.
+  release_tiled_weights();
+  for (const Node& n : graph_->nodes()) {
+    if (n.op_type() != OpType::Linear || n.inputs().size() < 2) continue;
+    Tensor* w = ctx.get(n.inputs()[1]);
+    if (!w || w->dtype() != DType::Q8_0 || w->device().type != DeviceType::HIP ||
+        w->data() == nullptr || w->shape().rank() != 2)
+      continue;  // not on this path: the node keeps its registered kernel and its checks
+    const int64_t N = w->shape().dim(0), K = w->shape().dim(1);
+    if (N <= 0 || K <= 0 || K % 32 != 0 || N > INT32_MAX || K > INT32_MAX) continue;
+    if (w->allocated_bytes() < q8_0_bytes(N * K)) continue;
+    if (tiled_.count(w->data())) continue;  // shared by several nodes
+    const size_t bytes = hip::q8_0_tiled_bytes(static_cast<int>(N), static_cast<int>(K));
+    void* buf = nullptr;
+    const hipError_t err = hipMalloc(&buf, bytes);
+    if (err != hipSuccess) {
+      release_tiled_weights();
+      return Status::runtime_error(std::string("tiled weight allocation failed: ") +
+                                   hipGetErrorString(err));
+    }
+    tiled_bufs_.push_back(buf);
+    const Status st = hip::tile_q8_0(static_cast<const uint8_t*>(w->data()),
+                                     static_cast<uint8_t*>(buf), static_cast<int>(N),
+                                     static_cast<int>(K), stream_);
+    if (!st.ok()) {
+      release_tiled_weights();
+      return Status::runtime_error("tiling Linear weight of node #" + std::to_string(n.id().value) +
+                                   " failed: " + st.to_string());
+    }
+    tiled_[w->data()] = static_cast<const uint8_t*>(buf);
+  }
+  return Status::make_ok();
+}
 
 Status HipExecutor::compile(const Graph& graph) {
   TRY(graph.validate());
@@ -232,6 +278,8 @@ Status HipExecutor::run(RuntimeContext& ctx) {
   if (!graph_) return Status::runtime_error("executor not compiled");
   ctx.set_hip_stream(stream_);
   fused_launches_ = 0;
+  tiled_launches_ = 0;
+  const detail::TiledWeights* tiled = tiled_.empty() ? nullptr : &tiled_;
   for (const Step& step : plan_) {
     if (step.kind != Step::kNode) {
       std::vector<const Node*> nodes;
@@ -240,9 +288,11 @@ Status HipExecutor::run(RuntimeContext& ctx) {
         if (!nd) return nd.error();
         nodes.push_back(*nd);
       }
+      bool used_tiled = false;
       auto done = step.kind == Step::kSwiGLU
-                      ? detail::run_fused_swiglu(*nodes[0], *nodes[1], *nodes[2], ctx)
-                      : detail::run_fused_multi(nodes, ctx);
+                      ? detail::run_fused_swiglu(*nodes[0], *nodes[1], *nodes[2], ctx, tiled,
+                                                 &used_tiled)
+                      : detail::run_fused_multi(nodes, ctx, tiled, &used_tiled);
       if (!done) {
         std::string ids;
         for (const Node* n : nodes)
@@ -256,7 +306,23 @@ Status HipExecutor::run(RuntimeContext& ctx) {
       }
       if (*done) {
         ++fused_launches_;
+        tiled_launches_ += used_tiled;
         continue;
+      }
+    }
+    if (tiled && step.kind == Step::kNode) {
+      auto nd = graph_->node(step.nodes[0]);
+      if (nd && (*nd)->op_type() == OpType::Linear) {
+        auto done = detail::run_tiled_linear(**nd, ctx, *tiled);
+        if (!done)
+          return Status::runtime_error("HIP kernel Linear failed for node #" +
+                                       std::to_string(step.nodes[0].value) + " (" +
+                                       std::string((*nd)->name()) + "): " +
+                                       done.error().to_string());
+        if (*done) {
+          ++tiled_launches_;
+          continue;
+        }
       }
     }
     TRY(run_nodes(step.nodes, ctx));

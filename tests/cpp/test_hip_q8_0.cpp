@@ -769,6 +769,101 @@ static void test_executor_fusion_end_to_end() {
   std::printf("  PASS test_executor_fusion_end_to_end\n");
 }
 
+static void test_executor_tiled_weights() {
+  // The same graph as the fusion test, run on the raw bytes and then on tiled
+  // copies (HipExecutor::tile_weights): bitwise equal where both run the MFMA
+  // decode (M = 5) or the GEMM (M = 70); within 1e-6 relative L2 where the
+  // tiled FP32 GEMV replaces the raw one (M = 1).  Fused and unfused plans.
+  const int K = 128, I = 96, Q = 64, KV = 32;
+  std::vector<std::vector<uint8_t>> w;
+  const int rows[6] = {I, I, K, Q, KV, KV};
+  const int cols[6] = {K, K, I, K, K, K};
+  for (int i = 0; i < 6; ++i) w.push_back(synth_q8(rows[i], cols[i], 60 + i));
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  for (int fuse = 0; fuse < 2; ++fuse) {
+    for (int M : {1, 5, 70}) {
+      std::vector<float> hx(size_t(M) * K);
+      for (size_t i = 0; i < hx.size(); ++i) hx[i] = float(int(i * 41 % 103) - 51) * 0.02f;
+      Graph g;
+      GraphBuilder gb(g);
+      const Device dev = Device::hip(0);
+      auto x = gb.input("x", Shape({M, K}), DType::Float32, dev);
+      CHECK(x);
+      std::vector<ValueId> cw;
+      const char* names[6] = {"wg", "wu", "wd", "wq", "wk", "wv"};
+      for (int i = 0; i < 6; ++i) {
+        auto c = gb.constant(names[i], Shape({rows[i], cols[i]}), DType::Float32, dev);
+        CHECK(c);
+        cw.push_back(*c);
+      }
+      auto gate = gb.linear(*x, cw[0], std::nullopt, "gate");
+      auto up = gb.linear(*x, cw[1], std::nullopt, "up");
+      CHECK(gate && up);
+      auto act = gb.swiglu(*gate, *up, "swiglu");
+      CHECK(act);
+      auto down = gb.linear(*act, cw[2], std::nullopt, "down");
+      auto q = gb.linear(*x, cw[3], std::nullopt, "q");
+      auto k = gb.linear(*x, cw[4], std::nullopt, "k");
+      auto v = gb.linear(*x, cw[5], std::nullopt, "v");
+      CHECK(down && q && k && v);
+      CHECK(gb.output(*down, "o_down") && gb.output(*q, "o_q") && gb.output(*k, "o_k") &&
+            gb.output(*v, "o_v"));
+      std::vector<std::unique_ptr<Tensor>> tw;
+      RuntimeContext ctx;
+      for (int i = 0; i < 6; ++i) {
+        tw.push_back(std::make_unique<Tensor>(names[i], Shape({rows[i], cols[i]}), DType::Q8_0,
+                                              dev));
+        check_status(tw.back()->allocate_hip_bytes(w[i].size()));
+        upload(*tw.back(), w[i].data(), w[i].size());
+        check_status(ctx.bind(cw[i], tw.back().get()));
+      }
+      Tensor tx("x", Shape({M, K}), DType::Float32, dev);
+      check_status(tx.allocate_hip());
+      upload(tx, hx.data(), hx.size() * 4);
+      check_status(ctx.bind(*x, &tx));
+      check_status(ctx.allocate_intermediates(g));
+      HipExecutor ex(std::make_shared<HipBackend>(), registry);
+      ex.set_fusion(fuse == 1);
+      check_status(ex.compile(g));
+      std::vector<std::vector<float>> outs[2];
+      for (int tiled = 0; tiled < 2; ++tiled) {
+        if (tiled) {
+          check_status(ex.tile_weights(ctx));
+          CHECK(ex.tiled_weights() == 6u);
+        }
+        check_status(ex.run(ctx));
+        check_hip(hipDeviceSynchronize());
+        // fused: gate/up + SwiGLU, q/k/v, down; unfused: six Linears
+        CHECK(ex.tiled_launches() == (tiled ? (fuse ? 3u : 6u) : 0u));
+        outs[tiled] = {download(ctx.get(*down), size_t(M) * K),
+                       download(ctx.get(*q), size_t(M) * Q),
+                       download(ctx.get(*k), size_t(M) * KV),
+                       download(ctx.get(*v), size_t(M) * KV)};
+      }
+      for (int o = 0; o < 4; ++o) {
+        const auto& a = outs[0][o];
+        const auto& b = outs[1][o];
+        double num = 0, den = 0;
+        for (size_t i = 0; i < a.size(); ++i) {
+          num += double(a[i] - b[i]) * (a[i] - b[i]);
+          den += double(a[i]) * a[i];
+        }
+        if (M == 1) CHECK(std::sqrt(num / den) <= 1e-6);
+        else CHECK(std::memcmp(a.data(), b.data(), a.size() * 4) == 0);
+      }
+      ex.release_tiled_weights();
+      CHECK(ex.tiled_weights() == 0u);
+      check_status(ex.run(ctx));
+      check_hip(hipDeviceSynchronize());
+      CHECK(ex.tiled_launches() == 0u);
+      const auto again = download(ctx.get(*q), size_t(M) * Q);
+      CHECK(std::memcmp(again.data(), outs[0][1].data(), again.size() * 4) == 0);
+    }
+  }
+  std::printf("  PASS test_executor_tiled_weights\n");
+}
+
 int main() {
   int count = 0;
   check_hip(hipGetDeviceCount(&count));
@@ -784,6 +879,7 @@ int main() {
   test_gguf_model_end_to_end();
   test_fused_launchers();
   test_executor_fusion_end_to_end();
+  test_executor_tiled_weights();
   std::printf("test_hip_q8_0: all passed\n");
   return 0;
 }
