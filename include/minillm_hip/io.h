@@ -10,9 +10,11 @@
 //     bytes the reference's CPU and CUDA paths keep;
 //   * BF16 tensors stay BF16 (raw copy); every other type becomes Float32 on the
 //     host (F16/BF16 decoded, F32 copied) and is copied to the device.
-// Differences: tensor data is read with buffered file I/O (no mmap view), and
-// the model-config extraction (WeightLoader::extract_config) is not part of this
-// path.
+// Tensor data comes from a read-only mmap view of the file, as in the reference
+// (gguf_parser.h:91-97), with buffered reads when the file cannot be mapped; the
+// HIP branch copies a tensor's bytes to the device straight from the view.
+// Difference: the model-config extraction (WeightLoader::extract_config) is not
+// part of this path.
 #pragma once
 
 #include <cstddef>

@@ -1,7 +1,11 @@
 // io.cpp -- GGUF reader and weight loader (see include/minillm_hip/io.h).
 #include "minillm_hip/io.h"
 
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include <cmath>
 #include <cstdio>
@@ -313,12 +317,55 @@ expected<GGUFFile, Status> GGUFParser::parse(const std::string& filename) {
   return file;
 }
 
+namespace {
+
+// Read-only mapping of a whole GGUF file (the reference's mmap view,
+// gguf_parser.h:91-97).  open() returns null when the file cannot be mapped;
+// callers then stream the bytes with buffered reads.
+class MappedFile {
+ public:
+  static std::unique_ptr<MappedFile> open(const std::string& path) {
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return nullptr;
+    struct stat st {};
+    if (::fstat(fd, &st) != 0 || st.st_size <= 0) {
+      ::close(fd);
+      return nullptr;
+    }
+    void* p = ::mmap(nullptr, static_cast<size_t>(st.st_size), PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);  // the mapping keeps the file
+    if (p == MAP_FAILED) return nullptr;
+    return std::unique_ptr<MappedFile>(new MappedFile(p, static_cast<size_t>(st.st_size)));
+  }
+  ~MappedFile() { ::munmap(base_, size_); }
+  MappedFile(const MappedFile&) = delete;
+  MappedFile& operator=(const MappedFile&) = delete;
+  // Bytes [at, at + n) of the file, or null when the range is outside it.
+  const std::byte* view(uint64_t at, uint64_t n) const {
+    if (at > size_ || n > size_ - at) return nullptr;
+    return static_cast<const std::byte*>(base_) + at;
+  }
+
+ private:
+  MappedFile(void* base, size_t size) : base_(base), size_(size) {}
+  void* base_;
+  size_t size_;
+};
+
+}  // namespace
+
 Status GGUFParser::read_tensor_data(const std::string& filename, uint64_t data_offset,
                                     uint64_t tensor_offset, void* dst, size_t byte_count) {
-  FilePtr f(std::fopen(filename.c_str(), "rb"));
-  if (!f) return Status::io_error("cannot open file: " + filename);
   if (data_offset > std::numeric_limits<uint64_t>::max() - tensor_offset)
     return Status::out_of_range("tensor offset overflow for: " + filename);
+  if (auto map = MappedFile::open(filename)) {  // mmap fast path
+    const std::byte* src = map->view(data_offset + tensor_offset, byte_count);
+    if (!src) return Status::out_of_range("tensor byte range exceeds GGUF file bounds: " + filename);
+    std::memcpy(dst, src, byte_count);
+    return Status::make_ok();
+  }
+  FilePtr f(std::fopen(filename.c_str(), "rb"));
+  if (!f) return Status::io_error("cannot open file: " + filename);
   const uint64_t at = data_offset + tensor_offset, size = file_size(f.get());
   if (at > size || byte_count > size - at)
     return Status::out_of_range("tensor byte range exceeds GGUF file bounds: " + filename);
@@ -368,7 +415,7 @@ Status hip_copy(void* dst, const void* src, size_t bytes, const char* what) {
   return Status::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// Reads a tensor's raw bytes from the file (the reference uses an mmap view).
+// Reads a tensor's raw bytes from the file (streaming fallback of the mmap view).
 expected<std::vector<std::byte>, Status> read_raw(const std::string& path, const GGUFFile& file,
                                                    const GGUFTensorInfo& ti) {
   auto nbytes = ti.bytes();
@@ -383,10 +430,44 @@ expected<std::vector<std::byte>, Status> read_raw(const std::string& path, const
 // Raw-byte payloads (Q8_0 -> Q8_0, BF16 -> BFloat16) are copied as stored; any
 // other pair is decoded to fp32.  Mirrors the reference's load_tensor_from_gguf
 // (src/io/gguf_weight_loader.cpp:85-191) with HIP in place of CUDA.
-Status load_tensor(const std::string& path, const GGUFFile& file, const GGUFTensorInfo& ti,
-                   Tensor& tensor) {
-  if (!tensor.is_allocated()) return Status::runtime_error("tensor not allocated: " + tensor.name());
+// The tensor's bytes: a view into the mapped file when there is one (no host
+// copy; the HIP branch copies straight from it, as the reference's CUDA branch
+// copies from its raw view), else a buffer read from the file.
+struct RawBytes {
+  std::vector<std::byte> owned;
+  const std::byte* ptr = nullptr;
+  size_t n = 0;
+  const std::byte* data() const { return ptr; }
+  size_t size() const { return n; }
+};
+
+expected<RawBytes, Status> tensor_bytes(const std::string& path, const GGUFFile& file,
+                                        const GGUFTensorInfo& ti, const MappedFile* map) {
+  RawBytes r;
+  if (map) {
+    auto nbytes = ti.bytes();
+    if (!nbytes) return unexpected(nbytes.error());
+    if (file.data_offset > std::numeric_limits<uint64_t>::max() - ti.offset)
+      return unexpected(Status::out_of_range("tensor offset overflow for: " + path));
+    r.ptr = map->view(file.data_offset + ti.offset, *nbytes);
+    if (!r.ptr)
+      return unexpected(
+          Status::out_of_range("tensor byte range exceeds GGUF file bounds: " + path));
+    r.n = *nbytes;
+    return r;
+  }
   auto raw = read_raw(path, file, ti);
+  if (!raw) return unexpected(raw.error());
+  r.owned = std::move(*raw);
+  r.ptr = r.owned.data();
+  r.n = r.owned.size();
+  return r;
+}
+
+Status load_tensor(const std::string& path, const GGUFFile& file, const GGUFTensorInfo& ti,
+                   Tensor& tensor, const MappedFile* map) {
+  if (!tensor.is_allocated()) return Status::runtime_error("tensor not allocated: " + tensor.name());
+  auto raw = tensor_bytes(path, file, ti, map);
   if (!raw) return raw.error();
   auto numel = ti.num_elements();
   if (!numel) return numel.error();
@@ -546,6 +627,7 @@ Status WeightLoader::dequantize_to_f32(GgmlDataType src_dtype, const void* src, 
 Status WeightLoader::load_weights(const GGUFFile& file, const Graph& graph,
                                   RuntimeContext& ctx) const {
   const auto names = value_to_gguf(file);
+  const auto map = MappedFile::open(gguf_path_);  // null: streamed reads
   for (const auto& v : graph.values()) {
     if (v.kind != ValueKind::Constant) continue;
     auto it = names.find(v.name);
@@ -553,7 +635,7 @@ Status WeightLoader::load_weights(const GGUFFile& file, const Graph& graph,
     const GGUFTensorInfo* ti = file.find_tensor(it->second);
     Tensor* t = ctx.get(v.id);
     if (!t) return Status::runtime_error("tensor not found in RuntimeContext for value: " + v.name);
-    TRY(load_tensor(gguf_path_, file, *ti, *t));
+    TRY(load_tensor(gguf_path_, file, *ti, *t, map.get()));
   }
   return Status::make_ok();
 }
@@ -561,6 +643,7 @@ Status WeightLoader::load_weights(const GGUFFile& file, const Graph& graph,
 expected<SharedWeightStore, Status> WeightLoader::load_shared_weights(const GGUFFile& file,
                                                                       const Graph& graph) const {
   const auto names = value_to_gguf(file);
+  const auto map = MappedFile::open(gguf_path_);  // null: streamed reads
   SharedWeightStore store;
   for (const auto& v : graph.values()) {
     if (v.kind != ValueKind::Constant) continue;
@@ -593,7 +676,7 @@ expected<SharedWeightStore, Status> WeightLoader::load_shared_weights(const GGUF
         loaded = *nb;
       }
       if (!st.ok()) return unexpected(st);
-      st = load_tensor(gguf_path_, file, *ti, *tensor);
+      st = load_tensor(gguf_path_, file, *ti, *tensor, map.get());
       if (!st.ok()) return unexpected(st);
       shared = tensor.get();
       store.total_bytes_ += loaded;
