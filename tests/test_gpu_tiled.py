@@ -155,6 +155,14 @@ def test_linear_tiled_special_values(dev):
     capi.linear(dx, dw, None, y_raw, M, N, K)
     capi.linear_tiled(dx, dt, None, y_t, M, N, K)
     assert_bitexact(to_host(y_t), to_host(y_raw), "special values")
+    # the GEMM (M >= 64) on rows carrying the same values: bit for bit
+    M2 = 70
+    x2 = np.concatenate([x, S.activations(43, (M2 - M, K))])
+    dx2 = to_dev(x2, dev)
+    y2r, y2t = empty_f32((M2, N), dev), empty_f32((M2, N), dev)
+    capi.linear(dx2, dw, None, y2r, M2, N, K)
+    capi.linear_tiled(dx2, dt, None, y2t, M2, N, K)
+    assert_bitexact(to_host(y2t), to_host(y2r), "special values gemm")
     # the tiled GEMV (one token) on the same rows: non-finite entries as the raw
     # GEMV gives them
     for row in (1, 3, 4):
