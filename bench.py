@@ -66,10 +66,17 @@ def gemv_bytes(M, N, K):
     return N * (K // 32) * 34 + 4 * M * K + 4 * M * N
 
 
-def decode_kernel_name(M, layout="raw"):
+def tiled_gemv_wins(M, N, K):
+    """mle_q8_0_linear_tiled's choice of its FP32 GEMV (mle::gemv_tiled_wins)."""
+    return M == 1 or (M == 2 and N < 65536) or (M <= 4 and K <= 1024 and N <= 32768)
+
+
+def decode_kernel_name(M, layout="raw", N=4096, K=4096):
     """Kernel the C ABI runs for an M-token Linear (mle_q8_0_linear[_tiled] path choice)."""
     if M == 1 and layout == "raw":
         return "gemv_q8_0_kernel (FP32 GEMV)"
+    if layout == "tiled" and tiled_gemv_wins(M, N, K):
+        return "gemv_tiled_kernel (FP32 GEMV, tiled weights)"
     if M < 64:
         return ("gemv_q8_0_mfma_kernel (MFMA decode, exact bf16 activation split"
                 + (", tiled weights)" if layout == "tiled" else ")"))
@@ -270,7 +277,8 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": int(traffic) if traffic else None,
                 "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE)",
-                "kernel": f"{decode_kernel_name(dom['M'], 'tiled')} M={dom['M']} {dom['op']} "
+                "kernel": f"{decode_kernel_name(dom['M'], 'tiled', dom['N'], dom['K'])} "
+                          f"M={dom['M']} {dom['op']} "
                           f"[{dom['N']}x{dom['K']}]",
                 "bytes_per_launch": dom_bytes, "us_per_launch": dom["us"]}
 
