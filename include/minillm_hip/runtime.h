@@ -91,6 +91,19 @@ class RuntimeContext {
   hipStream_t hip_stream_{nullptr};
 };
 
+namespace detail {
+// Raw Q8_0 weight buffer (device pointer) -> its copy in 16-row tiles, with the
+// shape it was made for.  A node whose bound weight has another shape (a buffer
+// freed and its address reused, or one buffer viewed with two shapes) does not
+// match and runs on the raw bytes.
+struct TiledCopy {
+  const uint8_t* data = nullptr;
+  int64_t N = 0, K = 0;
+  size_t bytes = 0;
+};
+using TiledWeights = std::unordered_map<const void*, TiledCopy>;
+}  // namespace detail
+
 class Executor {
  public:
   virtual ~Executor() = default;
@@ -107,6 +120,19 @@ class HipExecutor final : public Executor {
   Status compile(const Graph& graph) override;
   Status run(RuntimeContext& ctx) override;
   hipStream_t stream() const { return stream_; }
+
+  // Split-K workspace of the Q8_0 Linear kernels (no counterpart in the
+  // reference, whose CUDA kernels use none): reserves the executor stream's
+  // workspace for the largest Linear launch of the compiled plan (fused groups
+  // included, raw or tiled weights), with shapes from the tensors bound in
+  // `ctx` where given, else from the graph's static value shapes.  compile()
+  // (on a machine with a HIP device) and tile_weights() call it, so run()
+  // allocates and synchronises nothing; a bound tensor larger than the graph's
+  // shapes makes its launch grow the workspace once.
+  Status reserve_workspace(const RuntimeContext* ctx = nullptr);
+  // Bytes / counters of the last reservation (0 / 0 before any).
+  size_t workspace_bytes() const { return ws_bytes_; }
+  size_t workspace_counters() const { return ws_counters_; }
 
   // Linear epilogue fusion (on by default; takes effect at the next compile):
   //  * Linear(gate) + Linear(up) + SwiGLU, where both Linears read one input,
@@ -155,8 +181,10 @@ class HipExecutor final : public Executor {
   size_t fused_launches_{0};
   size_t tiled_launches_{0};
   hipStream_t stream_;
-  std::unordered_map<const void*, const uint8_t*> tiled_;  // raw buffer -> tiled copy
+  detail::TiledWeights tiled_;  // raw buffer -> tiled copy
   std::vector<void*> tiled_bufs_;
+  size_t ws_bytes_{0}, ws_counters_{0};
+  bool ws_pending_{false};  // a reservation compile() could not make (no HIP device)
 };
 
 // Registers the HIP Q8_0 kernels (Embedding, Linear, MatMul) under

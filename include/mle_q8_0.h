@@ -10,11 +10,14 @@
  *     scale d followed by 32 int8 quants q; value = d * q.
  *   - Work is enqueued on `stream` (NULL = the default stream) and is
  *     asynchronous; the caller synchronises.  The Linear entry points keep one
- *     split-K workspace (partial sums + tile counters) per (device, stream),
- *     allocated with hipMalloc on first need and grown (after a synchronise of
- *     that stream) when a larger shape arrives; it lives until process exit.
- *     Nothing else is allocated.  Entry points are re-entrant; calls writing
- *     the same output buffer on different streams race, as with any kernel.
+ *     split-K workspace (partial sums + tile counters) per (device, stream).
+ *     A caller that must not allocate on its hot path reserves it beforehand
+ *     (mle_q8_0_workspace_size + mle_workspace_reserve); otherwise it is
+ *     allocated with hipMalloc on first need.  It only grows, each buffer to
+ *     max(capacity, need), after a synchronise of that stream, and lives until
+ *     process exit.  Nothing else is allocated.  Entry points are re-entrant;
+ *     calls writing the same output buffer on different streams race, as with
+ *     any kernel.
  *   - Return value: 0 on success, else a value of the reference's ErrorCode
  *     enum (include/minillm/core/status.h:20-32): 1 InvalidArgument,
  *     2 OutOfRange, 3 ShapeMismatch, 4 Unsupported, 6 RuntimeError.  The
@@ -215,6 +218,40 @@ int mle_q8_0_linear_swiglu_tiled(const float* x, const uint8_t* w_gate, const ui
 int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const* w,
                                 const float* const* bias, float* const* y, const int* N, int M,
                                 int K, hipStream_t stream);
+
+/*
+ * Workspace reservation (no counterpart in the reference: its CUDA kernels need
+ * no workspace, cuda_kernels.cu:918-936; this keeps allocation off the hot path
+ * as the reference's RuntimeContext keeps it off for outputs,
+ * runtime_context.cpp:78-220).
+ *
+ * mle_q8_0_workspace_size: *bytes / *counters = the workspace a call would use
+ *   on the per-stream workspace: op MLE_OP_LINEAR (count 1, mle_q8_0_linear),
+ *   MLE_OP_LINEAR_SWIGLU (count 2, N[0] == N[1], mle_q8_0_linear_swiglu) or
+ *   MLE_OP_LINEAR_MULTI (count 1..3, mle_q8_0_linear_multi), with M tokens,
+ *   output sizes N[0..count), input size K, on raw (tiled == 0) or 16-row
+ *   tiled weights.  Launches nothing.  Errors: NULL outputs / N, M or K or an
+ *   N <= 0, a bad count or op -> InvalidArgument; K % 32 != 0 -> Unsupported.
+ * mle_workspace_reserve: grows the workspace of (current device, stream) to
+ *   hold at least `bytes` and `counters` (a no-op when it already does); later
+ *   calls within those sizes allocate and synchronise nothing.
+ * mle_workspace_info: capacity of (current device, stream)'s workspace and the
+ *   number of (re)allocations it has had (0 / 0 / 0 when it has none yet).
+ * mle_workspace_plan_growth (test hook): the growth rule, applied to
+ *   capacities and a need without allocating: returns 1 and the new capacities
+ *   (each max(capacity, need, minimum)) when the need does not fit, else 0 and
+ *   the capacities unchanged; -1 for NULL outputs.
+ */
+#define MLE_OP_LINEAR 0
+#define MLE_OP_LINEAR_SWIGLU 1
+#define MLE_OP_LINEAR_MULTI 2
+int mle_q8_0_workspace_size(int op, int M, int count, const int* N, int K, int tiled,
+                            size_t* bytes, size_t* counters);
+int mle_workspace_reserve(size_t bytes, size_t counters, hipStream_t stream);
+int mle_workspace_info(hipStream_t stream, size_t* bytes, size_t* counters,
+                       uint64_t* generation);
+int mle_workspace_plan_growth(size_t cap_bytes, size_t cap_counters, size_t need_bytes,
+                              size_t need_counters, size_t* new_bytes, size_t* new_counters);
 
 /*
  * Message of the last failed call on this thread ("" if none).  Stands in for

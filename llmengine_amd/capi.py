@@ -25,7 +25,10 @@ EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_q8_0_embedding", "mle_argmax_f32", "mle_top_tokens_f32", "mle_swiglu_f32",
             "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode", "mle_q8_0_tiled_bytes",
             "mle_q8_0_tile", "mle_q8_0_linear_tiled", "mle_q8_0_linear_swiglu_tiled",
-            "mle_q8_0_linear_multi_tiled")
+            "mle_q8_0_linear_multi_tiled", "mle_q8_0_workspace_size", "mle_workspace_reserve",
+            "mle_workspace_info", "mle_workspace_plan_growth")
+
+OP_LINEAR, OP_LINEAR_SWIGLU, OP_LINEAR_MULTI = 0, 1, 2
 
 
 class Q8_0Error(RuntimeError):
@@ -87,6 +90,15 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_linear_swiglu_tiled.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_q8_0_linear_multi_tiled.restype = _i
     lib.mle_q8_0_linear_multi_tiled.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp]
+    _sz = ctypes.c_size_t
+    lib.mle_q8_0_workspace_size.restype = _i
+    lib.mle_q8_0_workspace_size.argtypes = [_i, _i, _i, _vp, _i, _i, _vp, _vp]
+    lib.mle_workspace_reserve.restype = _i
+    lib.mle_workspace_reserve.argtypes = [_sz, _sz, _vp]
+    lib.mle_workspace_info.restype = _i
+    lib.mle_workspace_info.argtypes = [_vp, _vp, _vp, _vp]
+    lib.mle_workspace_plan_growth.restype = _i
+    lib.mle_workspace_plan_growth.argtypes = [_sz, _sz, _sz, _sz, _vp, _vp]
     _lib = lib
     return lib
 
@@ -285,3 +297,42 @@ def linear_swiglu_tiled(x, w_gate, w_up, y, M, N, K, stream=None) -> None:
 def linear_multi_tiled(x, ws, biases, ys, Ns, M, K, stream=None) -> None:
     """linear_multi() on tiled weights."""
     _raise(linear_multi_status(x, ws, biases, ys, Ns, M, K, stream, tiled=True)[0])
+
+
+# Workspace reservation (include/mle_q8_0.h): sizes a call would use, reserving
+# them ahead of the hot path, and the per-stream workspace's capacity.
+
+def workspace_size_status(op, M, Ns, K, tiled=False):
+    """(code, message, bytes, counters) of the workspace an op would use."""
+    n_arr = (_i * max(len(Ns), 1))(*Ns)
+    b, c = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    rc = load().mle_q8_0_workspace_size(op, M, len(Ns), ctypes.cast(n_arr, _vp), K,
+                                        1 if tiled else 0, ctypes.byref(b), ctypes.byref(c))
+    code, msg = _status(rc)
+    return code, msg, b.value, c.value
+
+
+def workspace_size(op, M, Ns, K, tiled=False):
+    code, msg, b, c = workspace_size_status(op, M, Ns, K, tiled)
+    _raise(code)
+    return b, c
+
+
+def workspace_reserve(nbytes, counters, stream=None) -> None:
+    _raise(load().mle_workspace_reserve(nbytes, counters, _stream(stream)))
+
+
+def workspace_info(stream=None):
+    """(bytes, counters, generation) of the (current device, stream) workspace."""
+    b, c, g = ctypes.c_size_t(0), ctypes.c_size_t(0), ctypes.c_uint64(0)
+    _raise(load().mle_workspace_info(_stream(stream), ctypes.byref(b), ctypes.byref(c),
+                                     ctypes.byref(g)))
+    return b.value, c.value, g.value
+
+
+def workspace_plan_growth(cap_bytes, cap_counters, need_bytes, need_counters):
+    """(grow, new_bytes, new_counters) under the library's growth rule."""
+    nb, nc = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    rc = load().mle_workspace_plan_growth(cap_bytes, cap_counters, need_bytes, need_counters,
+                                          ctypes.byref(nb), ctypes.byref(nc))
+    return bool(rc), nb.value, nc.value

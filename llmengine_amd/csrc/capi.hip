@@ -91,54 +91,113 @@ int validate_linear(const float* x, const uint8_t* w, const float* bias, float* 
 // Workspace of the MFMA paths, one per (device, stream): split-K partial sums
 // and tile counters, and the prefill GEMM's bf16 copy of X.  Calls on one
 // stream run in order, so the workspace is never used by two launches at once.
-// Allocated on the first call that needs it (and grown when a larger shape
-// comes), kept until the process ends.
+// It is reserved ahead of the hot path (mle_workspace_reserve, which
+// minillm::HipExecutor calls from compile() and tile_weights() for its graph's
+// largest shapes), or allocated on the first call that needs it; it only ever
+// grows, to max(capacity, need) for each of its two buffers, and lives until
+// the process ends.
 struct StreamWorkspace {
   uint8_t* buf = nullptr;  // partial sums, then scratch
   size_t buf_cap = 0;      // bytes
   uint32_t* counters = nullptr;
-  size_t counter_cap = 0;
+  size_t counter_cap = 0;  // uint32 entries
+  uint64_t generation = 0;  // (re)allocations so far
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, StreamWorkspace> g_ws;
 
-int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWorkspace* out) {
-  *out = mle::SplitKWorkspace{};
-  if (need.partial_floats == 0 && need.scratch_bytes == 0) return MLE_OK;
-  const size_t partial_bytes = (need.partial_floats * sizeof(float) + 255) / 256 * 256;
-  const size_t bytes = partial_bytes + need.scratch_bytes;
+constexpr size_t kMinWorkspaceBytes = size_t(4) << 20;
+constexpr size_t kMinWorkspaceCounters = 4096;
+
+// Growth rule: capacities never shrink, and a buffer that must grow takes
+// max(capacity, need, minimum).  Returns whether an allocation is needed.
+bool plan_growth(size_t cap_bytes, size_t cap_counters, size_t need_bytes, size_t need_counters,
+                 size_t* new_bytes, size_t* new_counters) {
+  *new_bytes = cap_bytes;
+  *new_counters = cap_counters;
+  if (need_bytes <= cap_bytes && need_counters <= cap_counters) return false;
+  *new_bytes = std::max({cap_bytes, need_bytes, kMinWorkspaceBytes});
+  *new_counters = std::max({cap_counters, need_counters, kMinWorkspaceCounters});
+  return true;
+}
+
+// Bytes of the workspace buffer a launch needs: partial sums (256-byte
+// multiple), then scratch.
+size_t need_bytes(const mle::SplitKNeed& need) {
+  if (need.partial_floats == 0 && need.scratch_bytes == 0) return 0;
+  return (need.partial_floats * sizeof(float) + 255) / 256 * 256 + need.scratch_bytes;
+}
+
+int ensure_workspace(size_t bytes, size_t counters, hipStream_t stream, StreamWorkspace** out) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
-  if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 workspace");
-  std::lock_guard<std::mutex> lock(g_ws_mu);
+  if (err != hipSuccess) return check_launch(err, "hip Q8_0 workspace");
   StreamWorkspace& e = g_ws[{dev, stream}];
-  if (e.buf_cap < bytes || e.counter_cap < need.counters) {
+  size_t nb = 0, nc = 0;
+  if (plan_growth(e.buf_cap, e.counter_cap, bytes, counters, &nb, &nc)) {
     if (e.buf != nullptr || e.counters != nullptr) {
       // Earlier launches on this stream may still read the old buffers.
       err = hipStreamSynchronize(stream);
-      if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 workspace");
+      if (err != hipSuccess) return check_launch(err, "hip Q8_0 workspace");
       (void)hipFree(e.buf);
       (void)hipFree(e.counters);
-      e = StreamWorkspace{};
+      e.buf = nullptr;
+      e.counters = nullptr;
+      e.buf_cap = e.counter_cap = 0;
     }
-    const size_t bc = std::max<size_t>(bytes, size_t(4) << 20);
-    const size_t cc = std::max<size_t>(need.counters, 4096);
-    err = hipMalloc(&e.buf, bc);
-    if (err == hipSuccess) err = hipMalloc(&e.counters, cc * sizeof(uint32_t));
-    if (err == hipSuccess) err = hipMemsetAsync(e.counters, 0, cc * sizeof(uint32_t), stream);
+    err = hipMalloc(&e.buf, nb);
+    if (err == hipSuccess) err = hipMalloc(&e.counters, nc * sizeof(uint32_t));
+    // Counters start at zero (the kernels leave them at zero); cleared by a
+    // kernel rather than a memset node, so a captured first call replays too.
+    if (err == hipSuccess) err = mle::launch_fill_u32(e.counters, nc, 0u, stream);
     if (err != hipSuccess) {
       (void)hipFree(e.buf);
       (void)hipFree(e.counters);
-      e = StreamWorkspace{};
-      return check_launch(err, "hip sgemm_nt Q8_0 workspace allocation failed");
+      e.buf = nullptr;
+      e.counters = nullptr;
+      e.buf_cap = e.counter_cap = 0;
+      return check_launch(err, "hip Q8_0 workspace allocation failed");
     }
-    e.buf_cap = bc;
-    e.counter_cap = cc;
+    e.buf_cap = nb;
+    e.counter_cap = nc;
+    ++e.generation;
   }
-  out->partials = reinterpret_cast<float*>(e.buf);
-  out->counters = e.counters;
-  out->scratch = need.scratch_bytes ? e.buf + partial_bytes : nullptr;
+  *out = &e;
   return MLE_OK;
+}
+
+int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWorkspace* out) {
+  *out = mle::SplitKWorkspace{};
+  const size_t bytes = need_bytes(need);
+  if (bytes == 0) return MLE_OK;
+  const size_t partial_bytes = (need.partial_floats * sizeof(float) + 255) / 256 * 256;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  StreamWorkspace* e = nullptr;
+  MLE_TRY(ensure_workspace(bytes, need.counters, stream, &e));
+  out->partials = reinterpret_cast<float*>(e->buf);
+  out->counters = e->counters;
+  out->scratch = need.scratch_bytes ? e->buf + partial_bytes : nullptr;
+  return MLE_OK;
+}
+
+// Where a Linear-family call takes its workspace: the per-stream one, or (plan
+// mode) nowhere: the call only records the largest need of its launches and
+// launches nothing.
+struct Exec {
+  hipStream_t stream = nullptr;
+  size_t* plan_bytes = nullptr;     // non-null: plan mode
+  size_t* plan_counters = nullptr;
+  bool planning() const { return plan_bytes != nullptr; }
+};
+
+int workspace_for(const mle::SplitKNeed& need, const Exec& ex, mle::SplitKWorkspace* out) {
+  if (ex.planning()) {
+    *out = mle::SplitKWorkspace{};
+    *ex.plan_bytes = std::max(*ex.plan_bytes, need_bytes(need));
+    *ex.plan_counters = std::max(*ex.plan_counters, need.counters);
+    return MLE_OK;
+  }
+  return get_workspace(need, ex.stream, out);
 }
 
 // Linear path numbers (mle_q8_0_linear_ex): 1 FP32 GEMV, 2 bf16-MFMA prefill GEMM,
@@ -164,7 +223,7 @@ struct Tune {
 // four on short rows), else the MFMA decode below 64 tokens and the MFMA GEMM
 // from 64.
 int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
-               int N, int K, int path, const Tune& tune, hipStream_t stream,
+               int N, int K, int path, const Tune& tune, const Exec& ex,
                mle::WeightLayout layout = mle::WeightLayout::kRaw) {
   const bool tiled = layout == mle::WeightLayout::kTiled;
   if (path == 0) {
@@ -181,7 +240,7 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
   one.layout = layout;
   if (tiled && path == 3 && M <= 4 && mle::gemv_tiled_wins(M, N, K)) {
     const mle::TiledGemvConfig c = mle::gemv_tiled_pick(M, N, K, false);
-    return check_launch(mle::launch_gemv_tiled_segs(c, x, one, M, K, stream),
+    return check_launch((ex.planning() ? hipSuccess : mle::launch_gemv_tiled_segs(c, x, one, M, K, ex.stream)),
                         "hip sgemm_nt Q8_0 launch failed");
   }
   if (path == 2) {
@@ -199,8 +258,8 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
     if (!mle::gemm_mfma_fits(c, M, N, K))
       return fail(MLE_UNSUPPORTED, "hip sgemm_nt Q8_0: K too large for the MFMA GEMM");
     mle::SplitKWorkspace ws;
-    MLE_TRY(get_workspace(mle::gemm_mfma_workspace(c, M, N, K), stream, &ws));
-    return check_launch(mle::launch_gemm_mfma_segs(c, x, one, M, K, ws, stream),
+    MLE_TRY(workspace_for(mle::gemm_mfma_workspace(c, M, N, K), ex, &ws));
+    return check_launch((ex.planning() ? hipSuccess : mle::launch_gemm_mfma_segs(c, x, one, M, K, ws, ex.stream)),
                         "hip sgemm_nt Q8_0 launch failed");
   }
   if (path == 3) {
@@ -217,9 +276,9 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
       mle::LinearSegs chunk = one;
       chunk.seg[0].y = y + (int64_t)m0 * N;
       mle::SplitKWorkspace ws;
-      MLE_TRY(get_workspace(mle::decode_mfma_workspace_segs(c, chunk, K), stream, &ws));
+      MLE_TRY(workspace_for(mle::decode_mfma_workspace_segs(c, chunk, K), ex, &ws));
       const hipError_t err =
-          mle::launch_gemv_mfma_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ws, stream);
+          (ex.planning() ? hipSuccess : mle::launch_gemv_mfma_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ws, ex.stream));
       if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 launch failed");
     }
     return ok();
@@ -234,8 +293,8 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
       return fail(MLE_INVALID_ARGUMENT, "hip sgemm_nt_q8_0_weight: GEMV token tile " +
                                             std::to_string(c.mt) + " is smaller than M");
     }
-    const hipError_t err = mle::launch_gemv(c, x + (int64_t)m0 * K, w, bias,
-                                            y + (int64_t)m0 * N, mc, N, K, stream);
+    const hipError_t err = (ex.planning() ? hipSuccess : mle::launch_gemv(c, x + (int64_t)m0 * K, w, bias,
+                                            y + (int64_t)m0 * N, mc, N, K, ex.stream));
     if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 launch failed");
   }
   return ok();
@@ -247,7 +306,7 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
 // decode kernel in chunks of up to 16 tokens with FP32-exact activations);
 // SwiGLU takes the GEMV for M == 1 only.
 int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, int K,
-             hipStream_t stream) {
+             const Exec& ex) {
   const bool swi = s.mode == mle::Epilogue::kSwiGLU;
   int total_n = 0;
   for (int i = 0; i < s.count; ++i) total_n += s.seg[i].N;
@@ -256,20 +315,20 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
     if (!mle::gemm_mfma_fits(c, M, 0, K))
       return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": K too large for the MFMA GEMM");
     mle::SplitKWorkspace ws;
-    MLE_TRY(get_workspace(mle::gemm_mfma_workspace_segs(c, M, s, K), stream, &ws));
-    return check_launch(mle::launch_gemm_mfma_segs(c, x, s, M, K, ws, stream),
+    MLE_TRY(workspace_for(mle::gemm_mfma_workspace_segs(c, M, s, K), ex, &ws));
+    return check_launch((ex.planning() ? hipSuccess : mle::launch_gemm_mfma_segs(c, x, s, M, K, ws, ex.stream)),
                         "hip Q8_0 fused Linear launch failed");
   }
   const bool tiled = s.layout == mle::WeightLayout::kTiled;
   const int rows = swi ? s.seg[0].N : total_n;
   if (tiled && M <= 4 && mle::gemv_tiled_wins(M, rows, K)) {
     const mle::TiledGemvConfig c = mle::gemv_tiled_pick(M, rows, K, swi);
-    return check_launch(mle::launch_gemv_tiled_segs(c, x, s, M, K, stream),
+    return check_launch((ex.planning() ? hipSuccess : mle::launch_gemv_tiled_segs(c, x, s, M, K, ex.stream)),
                         "hip Q8_0 fused Linear launch failed");
   }
   if (!tiled && (swi ? M == 1 : pick_path(M, total_n, K) == 1)) {
     const mle::GemvConfig c = mle::gemv_pick_config(M, total_n, K);
-    return check_launch(mle::launch_gemv_segs(c, x, s, M, K, stream),
+    return check_launch((ex.planning() ? hipSuccess : mle::launch_gemv_segs(c, x, s, M, K, ex.stream)),
                         "hip Q8_0 fused Linear launch failed");
   }
   for (int m0 = 0; m0 < M; m0 += 16) {
@@ -283,9 +342,9 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
       chunk.seg[i].y = s.seg[i].y + (int64_t)m0 * s.seg[i].N;
     }
     mle::SplitKWorkspace ws;
-    MLE_TRY(get_workspace(mle::decode_mfma_workspace_segs(c, chunk, K), stream, &ws));
+    MLE_TRY(workspace_for(mle::decode_mfma_workspace_segs(c, chunk, K), ex, &ws));
     const hipError_t err =
-        mle::launch_gemv_mfma_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ws, stream);
+        (ex.planning() ? hipSuccess : mle::launch_gemv_mfma_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ws, ex.stream));
     if (err != hipSuccess) return check_launch(err, "hip Q8_0 fused Linear launch failed");
   }
   return ok();
@@ -310,7 +369,7 @@ int linear_swiglu(const float* x, const uint8_t* w_gate, const uint8_t* w_up, fl
   s.count = 2;
   s.seg[0] = mle::LinearSeg{w_gate, nullptr, y, N};
   s.seg[1] = mle::LinearSeg{w_up, nullptr, y, N};
-  return run_segs(ctx, x, s, M, K, stream);
+  return run_segs(ctx, x, s, M, K, Exec{stream});
 }
 
 int linear_multi(const float* x, int count, const uint8_t* const* w, const float* const* bias,
@@ -332,14 +391,14 @@ int linear_multi(const float* x, int count, const uint8_t* const* w, const float
     if (tiled) MLE_TRY(check_align(ctx, w[i], 16, "B"));
     s.seg[i] = mle::LinearSeg{w[i], b, y[i], N[i]};
   }
-  return run_segs(ctx, x, s, M, K, stream);
+  return run_segs(ctx, x, s, M, K, Exec{stream});
 }
 
 }  // namespace
 
 extern "C" {
 
-int mle_q8_0_abi_version(void) { return 5; }
+int mle_q8_0_abi_version(void) { return 6; }
 
 const char* mle_last_error(void) { return g_last_error.c_str(); }
 
@@ -353,7 +412,7 @@ size_t mle_q8_0_bytes(int64_t numel) {
 int mle_q8_0_linear(const float* x, const uint8_t* w_q8_0, const float* bias, float* y,
                     int M, int N, int K, hipStream_t stream) {
   MLE_TRY(validate_linear(x, w_q8_0, bias, y, M, N, K));
-  return run_linear(x, w_q8_0, bias, y, M, N, K, 0, Tune{}, stream);
+  return run_linear(x, w_q8_0, bias, y, M, N, K, 0, Tune{}, Exec{stream});
 }
 
 int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
@@ -393,7 +452,7 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
                   "hip sgemm_nt_q8_0_weight: a launch shape needs path 1, 2 or 3");
     }
   }
-  return run_linear(x, w_q8_0, bias, y, M, N, K, path, tune, stream);
+  return run_linear(x, w_q8_0, bias, y, M, N, K, path, tune, Exec{stream});
 }
 
 
@@ -435,7 +494,7 @@ int mle_q8_0_linear_tiled(const float* x, const uint8_t* w_tiled, const float* b
                           int M, int N, int K, hipStream_t stream) {
   MLE_TRY(validate_linear(x, w_tiled, bias, y, M, N, K));
   MLE_TRY(check_align("sgemm_nt_q8_0_tiled", w_tiled, 16, "B"));
-  return run_linear(x, w_tiled, bias, y, M, N, K, 0, Tune{}, stream,
+  return run_linear(x, w_tiled, bias, y, M, N, K, 0, Tune{}, Exec{stream},
                     mle::WeightLayout::kTiled);
 }
 
@@ -448,6 +507,84 @@ int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const*
                                 const float* const* bias, float* const* y, const int* N, int M,
                                 int K, hipStream_t stream) {
   return linear_multi(x, count, w, bias, y, N, M, K, stream, mle::WeightLayout::kTiled);
+}
+
+int mle_q8_0_workspace_size(int op, int M, int count, const int* N, int K, int tiled,
+                            size_t* bytes, size_t* counters) {
+  const char* ctx = "q8_0_workspace_size";
+  if (bytes == nullptr || counters == nullptr || N == nullptr)
+    return fail(MLE_INVALID_ARGUMENT,
+                std::string("hip ") + ctx + ": N, bytes and counters must not be null");
+  *bytes = 0;
+  *counters = 0;
+  MLE_TRY(check_positive(ctx, M, "M"));
+  MLE_TRY(check_positive(ctx, K, "K"));
+  if (K % 32 != 0)
+    return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + " requires K to be a multiple of 32");
+  const mle::WeightLayout layout = tiled ? mle::WeightLayout::kTiled : mle::WeightLayout::kRaw;
+  Exec ex;
+  ex.plan_bytes = bytes;
+  ex.plan_counters = counters;
+  mle::LinearSegs s;
+  s.layout = layout;
+  if (op == MLE_OP_LINEAR) {
+    if (count != 1) return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": a Linear has count 1");
+    MLE_TRY(check_positive(ctx, N[0], "N"));
+    return run_linear(nullptr, nullptr, nullptr, nullptr, M, N[0], K, 0, Tune{}, ex, layout);
+  }
+  if (op == MLE_OP_LINEAR_SWIGLU) {
+    if (count != 2 || N[0] != N[1])
+      return fail(MLE_INVALID_ARGUMENT,
+                  std::string("hip ") + ctx + ": a gate/up pair has count 2 and equal N");
+    MLE_TRY(check_positive(ctx, N[0], "N"));
+    s.mode = mle::Epilogue::kSwiGLU;
+    s.count = 2;
+    s.seg[0].N = s.seg[1].N = N[0];
+    return run_segs(ctx, nullptr, s, M, K, ex);
+  }
+  if (op == MLE_OP_LINEAR_MULTI) {
+    if (count < 1 || count > 3)
+      return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": count must be 1, 2 or 3");
+    s.count = count;
+    for (int i = 0; i < count; ++i) {
+      MLE_TRY(check_positive(ctx, N[i], "N"));
+      s.seg[i].N = N[i];
+    }
+    return run_segs(ctx, nullptr, s, M, K, ex);
+  }
+  return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": unknown op " + std::to_string(op));
+}
+
+int mle_workspace_reserve(size_t bytes, size_t counters, hipStream_t stream) {
+  if (bytes == 0 && counters == 0) return ok();
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  StreamWorkspace* e = nullptr;
+  MLE_TRY(ensure_workspace(bytes, counters, stream, &e));
+  return ok();
+}
+
+int mle_workspace_info(hipStream_t stream, size_t* bytes, size_t* counters,
+                       uint64_t* generation) {
+  if (bytes == nullptr || counters == nullptr || generation == nullptr)
+    return fail(MLE_INVALID_ARGUMENT, "hip workspace_info: output pointers must not be null");
+  int dev = 0;
+  const hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return check_launch(err, "hip workspace_info");
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  auto it = g_ws.find({dev, stream});
+  *bytes = it == g_ws.end() ? 0 : it->second.buf_cap;
+  *counters = it == g_ws.end() ? 0 : it->second.counter_cap;
+  *generation = it == g_ws.end() ? 0 : it->second.generation;
+  return ok();
+}
+
+int mle_workspace_plan_growth(size_t cap_bytes, size_t cap_counters, size_t need_bytes_,
+                              size_t need_counters, size_t* new_bytes, size_t* new_counters) {
+  if (new_bytes == nullptr || new_counters == nullptr) return -1;
+  return plan_growth(cap_bytes, cap_counters, need_bytes_, need_counters, new_bytes,
+                     new_counters)
+             ? 1
+             : 0;
 }
 
 int mle_swiglu_f32(const float* gate, const float* up, float* y, int64_t n,

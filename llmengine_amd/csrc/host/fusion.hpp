@@ -9,8 +9,8 @@
 
 namespace minillm::detail {
 
-// Raw Q8_0 weight buffer (device pointer) -> its copy in 16-row tiles.
-using TiledWeights = std::unordered_map<const void*, const uint8_t*>;
+// The tiled copy of `raw` made for an [N, K] weight, or nullptr.
+const uint8_t* tiled_copy_of(const TiledWeights* tiled, const void* raw, int64_t N, int64_t K);
 
 // One Linear node on the tiled copy of its weight (mle_q8_0_linear_tiled).
 // Returns false (nothing launched) when the node's operands do not validate or

@@ -386,19 +386,18 @@ Status linear_multi_tiled(const float* x, int count, const uint8_t* const* w_til
 
 namespace detail {
 
-namespace {
-const uint8_t* tiled_copy(const TiledWeights* tiled, const void* raw) {
+const uint8_t* tiled_copy_of(const TiledWeights* tiled, const void* raw, int64_t N, int64_t K) {
   if (tiled == nullptr) return nullptr;
   auto it = tiled->find(raw);
-  return it == tiled->end() ? nullptr : it->second;
+  if (it == tiled->end() || it->second.N != N || it->second.K != K) return nullptr;
+  return it->second.data;
 }
-}  // namespace
 
 expected<bool, Status> run_tiled_linear(const Node& node, RuntimeContext& ctx,
                                         const TiledWeights& tiled) {
   auto o = linear_operands(node, ctx);
   if (!o) return false;
-  const uint8_t* t = tiled_copy(&tiled, o->w);
+  const uint8_t* t = tiled_copy_of(&tiled, o->w, o->N, o->K);
   if (t == nullptr) return false;
   const Status st = hip::sgemm_nt_tiled(o->x, t, o->y, o->M, o->N, o->K, o->bias,
                                         ctx.hip_stream());
@@ -418,8 +417,8 @@ expected<bool, Status> run_fused_swiglu(const Node& gate, const Node& up, const 
   if (!ot || !check_hip_float(ot, "output").ok() ||
       !check_storage_bytes(ot, static_cast<size_t>(g->M) * g->N * 4, "output").ok())
     return false;
-  const uint8_t* tg = tiled_copy(tiled, g->w);
-  const uint8_t* tu = tiled_copy(tiled, u->w);
+  const uint8_t* tg = tiled_copy_of(tiled, g->w, g->N, g->K);
+  const uint8_t* tu = tiled_copy_of(tiled, u->w, u->N, u->K);
   if (used_tiled) *used_tiled = tg && tu;
   const Status st =
       tg && tu ? hip::linear_swiglu_tiled(g->x, tg, tu, static_cast<float*>(ot->data()), g->M,
@@ -452,7 +451,7 @@ expected<bool, Status> run_fused_multi(const std::vector<const Node*>& nodes,
   const uint8_t* tw[3] = {nullptr, nullptr, nullptr};
   bool all_tiled = true;
   for (size_t i = 0; i < nodes.size(); ++i) {
-    tw[i] = tiled_copy(tiled, w[i]);
+    tw[i] = tiled_copy_of(tiled, w[i], N[i], first.K);
     all_tiled = all_tiled && tw[i] != nullptr;
   }
   if (used_tiled) *used_tiled = all_tiled;

@@ -2,12 +2,14 @@
 // (see include/minillm_hip/runtime.h).
 #include "minillm_hip/runtime.h"
 
+#include <algorithm>
 #include <climits>
 #include <map>
 #include <unordered_map>
 #include <unordered_set>
 
 #include "fusion.hpp"
+#include "mle_q8_0.h"
 
 namespace minillm {
 
@@ -155,8 +157,91 @@ Status HipExecutor::tile_weights(RuntimeContext& ctx) {
       return Status::runtime_error("tiling Linear weight of node #" + std::to_string(n.id().value) +
                                    " failed: " + st.to_string());
     }
-    tiled_[w->data()] = static_cast<const uint8_t*>(buf);
+    tiled_[w->data()] = detail::TiledCopy{static_cast<const uint8_t*>(buf), N, K, bytes};
   }
+  return reserve_workspace(&ctx);
+}
+
+namespace {
+// M, N, K of a Linear node from the tensors bound in ctx, else the graph's
+// static value shapes (false when unknown or dynamic).
+bool linear_dims(const Graph& g, const Node& n, const RuntimeContext* ctx, int64_t* M,
+                 int64_t* N, int64_t* K) {
+  if (n.op_type() != OpType::Linear || n.inputs().size() < 2) return false;
+  auto shape_of = [&](ValueId id, Shape* out) {
+    if (ctx) {
+      if (const Tensor* t = ctx->get(id)) {
+        *out = t->shape();
+        return !out->has_dynamic_dim();
+      }
+    }
+    auto v = g.value(id);
+    if (!v) return false;
+    *out = (*v)->shape;
+    return !out->has_dynamic_dim();
+  };
+  Shape xs, ws;
+  if (!shape_of(n.inputs()[0], &xs) || !shape_of(n.inputs()[1], &ws)) return false;
+  if (xs.rank() == 0 || ws.rank() != 2) return false;
+  int64_t m = 1;
+  for (size_t i = 0; i + 1 < xs.rank(); ++i) m *= xs.dim(i);
+  *M = m;
+  *K = xs.dim(xs.rank() - 1);
+  *N = ws.dim(0);
+  return *M > 0 && *N > 0 && *K > 0 && *M <= INT32_MAX && *N <= INT32_MAX && *K <= INT32_MAX &&
+         *K % 32 == 0;
+}
+}  // namespace
+
+Status HipExecutor::reserve_workspace(const RuntimeContext* ctx) {
+  if (!graph_) return Status::runtime_error("executor not compiled");
+  size_t bytes = 0, counters = 0;
+  auto need = [&](int op, int M, int count, const int* N, int K) {
+    for (int tiled = 0; tiled < 2; ++tiled) {
+      size_t b = 0, c = 0;
+      if (mle_q8_0_workspace_size(op, M, count, N, K, tiled, &b, &c) == MLE_OK) {
+        bytes = std::max(bytes, b);
+        counters = std::max(counters, c);
+      }
+    }
+  };
+  for (const Step& step : plan_) {
+    std::vector<const Node*> nodes;
+    for (const NodeId& nid : step.nodes) {
+      auto nd = graph_->node(nid);
+      if (nd) nodes.push_back(*nd);
+    }
+    // Every Linear also on its own (a fused group that does not fit its kernel
+    // runs node by node), then the fused launch of its group.
+    std::vector<int> Ns;
+    int64_t M0 = 0, K0 = 0;
+    bool same = true;
+    for (const Node* n : nodes) {
+      int64_t M, N, K;
+      if (!linear_dims(*graph_, *n, ctx, &M, &N, &K)) continue;
+      const int n32 = static_cast<int>(N);
+      need(MLE_OP_LINEAR, static_cast<int>(M), 1, &n32, static_cast<int>(K));
+      if (Ns.empty()) M0 = M, K0 = K;
+      same = same && M == M0 && K == K0;
+      Ns.push_back(n32);
+    }
+    if (!same || Ns.size() < 2) continue;
+    if (step.kind == Step::kSwiGLU && Ns.size() == 2 && Ns[0] == Ns[1])
+      need(MLE_OP_LINEAR_SWIGLU, static_cast<int>(M0), 2, Ns.data(), static_cast<int>(K0));
+    else if (step.kind == Step::kMulti && Ns.size() <= 3)
+      need(MLE_OP_LINEAR_MULTI, static_cast<int>(M0), static_cast<int>(Ns.size()), Ns.data(),
+           static_cast<int>(K0));
+  }
+  ws_bytes_ = std::max(ws_bytes_, bytes);
+  ws_counters_ = std::max(ws_counters_, counters);
+  if (ws_bytes_ == 0 && ws_counters_ == 0) {
+    ws_pending_ = false;
+    return Status::make_ok();
+  }
+  const int rc = mle_workspace_reserve(ws_bytes_, ws_counters_, stream_);
+  if (rc != MLE_OK)
+    return Status::runtime_error(std::string("workspace reservation failed: ") + mle_last_error());
+  ws_pending_ = false;
   return Status::make_ok();
 }
 
@@ -248,7 +333,15 @@ Status HipExecutor::compile(const Graph& graph) {
       plan_.push_back(Step{Step::kNode, {nid}});
     }
   }
-  return Status::make_ok();
+  // Workspace for the plan's largest launch, now when a HIP device is present;
+  // on a host without one (graph-only use), at the first run.
+  ws_bytes_ = ws_counters_ = 0;
+  int devices = 0;
+  if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
+    ws_pending_ = true;
+    return Status::make_ok();
+  }
+  return reserve_workspace(nullptr);
 }
 
 size_t HipExecutor::fused_groups() const {
@@ -277,6 +370,7 @@ Status HipExecutor::run_nodes(const std::vector<NodeId>& ids, RuntimeContext& ct
 Status HipExecutor::run(RuntimeContext& ctx) {
   if (!graph_) return Status::runtime_error("executor not compiled");
   ctx.set_hip_stream(stream_);
+  if (ws_pending_) TRY(reserve_workspace(&ctx));
   fused_launches_ = 0;
   tiled_launches_ = 0;
   const detail::TiledWeights* tiled = tiled_.empty() ? nullptr : &tiled_;

@@ -1,4 +1,5 @@
-// elementwise.hip -- the unfused SwiGLU op of the HIP backend.
+// elementwise.hip -- the unfused SwiGLU op of the HIP backend, and a uint32
+// fill used to clear workspace counters.
 //
 // y[i] = silu(gate[i]) * up[i] = (g / (1 + exp(-g))) * u, the reference's
 // operation order (src/runtime/kernels/cpu_kernels.cpp:848-858; device twin
@@ -30,7 +31,22 @@ __global__ __launch_bounds__(256) void swiglu_f32_kernel(const float* __restrict
   for (int64_t j = i; j < n && j < i + 4; ++j) y[j] = (g[j] / (1.0f + expf(-g[j]))) * u[j];
 }
 
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n,
+                                                      uint32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 }  // namespace
+
+hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = (n + 255) / 256;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, (int64_t)n,
+                     v);
+  return hipGetLastError();
+}
 
 hipError_t launch_swiglu(const float* g, const float* u, float* y, int64_t n,
                          hipStream_t stream) {

@@ -39,8 +39,9 @@
 // Split K.  When there are too few row tiles to fill the GPU, the K chunks are
 // split over gridDim.y workgroups.  Each stores its 16 W x MT partial sums to its
 // own aligned workspace region and bumps a per-tile counter; the last workgroup
-// of a tile adds the partials in split order (deterministic) plus bias, writes y
-// and resets the counter to zero for the next launch on the stream.  The
+// of a tile resets the counter to zero for the next launch on the stream and
+// adds the partials in a fixed order (deterministic) plus bias, all its threads
+// loading 16-byte pieces of every split at once, then writes y.  The
 // partials travel by device-scope (sc1, write-through) stores and loads, and the
 // wait for every store's completion (s_waitcnt 0) precedes the counter increment,
 // so the workgroup that sees the final count reads complete data.  A
@@ -531,32 +532,95 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
           __builtin_bit_cast(uint32_t, outv[o]), prs,
           (uint32_t)((blockIdx.y * REGION + wave * S::OUTS + idx) * 4), 0, SC1);
   }
+  // Each tile's counter sits alone in a 128-byte line (kCounterStride), so the
+  // tiles' arrivals do not queue on one line.
+  uint32_t* const counter = counters + (size_t)blockIdx.x * kCounterStride;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);  // every partial has reached the coherence point
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   if (tid == 0)
-    arrived = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+    arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   if (arrived != gridDim.y - 1) return;
+  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  if (gridDim.y <= 8) {
+    // Up to 8 splits: each lane sums its outputs' partials in split order, the
+    // loads of all splits issued together.
+    float total[S::OPL];
+#pragma unroll
+    for (int o = 0; o < S::OPL; ++o) {
+      const int idx = lane + 64 * o;
+      float v[8];
+#pragma unroll
+      for (int sp = 0; sp < 8; ++sp)
+        v[sp] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(
+                       prs,
+                       idx < S::OUTS && (idx >> 4) < M && sp < (int)gridDim.y
+                           ? (uint32_t)((sp * REGION + wave * S::OUTS + idx) * 4)
+                           : 0x80000000u,
+                       0, SC1));
+      float s = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp < 8; ++sp)
+        if (sp < (int)gridDim.y) s += v[sp];
+      total[o] = s;
+    }
+    write_out(total);
+    return;
+  }
+
+  // More splits: the last workgroup reduces with every thread at once. The tile's partials
+  // are CHUNKS 16-byte pieces per split; TPC threads share a piece, thread
+  // (h, c) summing piece c of splits [h SPT, (h+1) SPT) in split order with all
+  // loads of a batch of 8 issued together (one round trip per batch instead of
+  // one per split), then the TPC sums of a piece are added in h order in LDS.
+  // The B-fragment LDS area is free by now (every wave has passed the barrier
+  // after its MFMAs) and holds the sums, then the tile's totals.
+  constexpr int CHUNKS = REGION / 4;
+  constexpr int TPC = S::NT / CHUNKS;  // 16 / MT threads per piece, rounded down
+  static_assert(TPC >= 1, "one thread per piece at least");
+  static_assert((4 * S::NT + REGION) * 4 <= S::BBUF, "reduction scratch fits the B area");
+  float* const sums = reinterpret_cast<float*>(bfr);  // [TPC][CHUNKS] x 4
+  float* const tot = sums + 4 * S::NT;                // [REGION]
+  {
+    const int c = tid % CHUNKS, h = tid / CHUNKS;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    const int off = 4 * c;  // float offset inside a split's region: wave, token, 4 rows
+    if (h < TPC && ((off % S::OUTS) >> 4) < M) {
+      const unsigned nspl = gridDim.y, spt = (nspl + TPC - 1) / TPC;
+      const unsigned s0 = h * spt, s1 = min(nspl, s0 + spt);
+      for (unsigned sp = s0; sp < s1; sp += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          v[j] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         prs, sp + j < s1 ? (uint32_t)(((sp + j) * REGION + off) * 4) : 0x80000000u,
+                         0, SC1));
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (sp + j < s1) s += v[j];
+      }
+    }
+    if (h < TPC) *reinterpret_cast<f32x4*>(sums + 4 * tid) = s;
+  }
+  __syncthreads();
+  for (int c = tid; c < CHUNKS; c += S::NT) {
+    f32x4 t = *reinterpret_cast<const f32x4*>(sums + 4 * c);
+    for (int h = 1; h < TPC; ++h) t += *reinterpret_cast<const f32x4*>(sums + 4 * (h * CHUNKS + c));
+    *reinterpret_cast<f32x4*>(tot + 4 * c) = t;
+  }
+  __syncthreads();
   float total[S::OPL];
 #pragma unroll
   for (int o = 0; o < S::OPL; ++o) {
     const int idx = lane + 64 * o;
-    float s = 0.0f;
-    if (idx < S::OUTS && (idx >> 4) < M) {
-#pragma unroll 8
-      for (unsigned sp = 0; sp < gridDim.y; ++sp)
-        s += __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(
-                       prs, (uint32_t)((sp * REGION + wave * S::OUTS + idx) * 4), 0, SC1));
-    }
-    total[o] = s;
+    total[o] = idx < S::OUTS ? tot[wave * S::OUTS + idx] : 0.0f;
   }
-  if (tid == 0)
-    __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   write_out(total);
 }
 
@@ -683,7 +747,7 @@ SplitKNeed decode_mfma_workspace_segs(const DecodeMfmaConfig& c, const LinearSeg
   need.splits = (int)gr.splits;
   const size_t region = (size_t)16 * c.waves * c.mt;
   need.partial_floats = gr.splits > 1 ? (size_t)gr.tiles * gr.splits * region : 0;
-  need.counters = gr.splits > 1 ? (size_t)gr.tiles : 0;
+  need.counters = gr.splits > 1 ? (size_t)gr.tiles * kCounterStride : 0;
   return need;
 }
 

@@ -36,6 +36,9 @@ struct SplitKNeed {
   size_t counters = 0;        // per-tile arrival counters (0 when splits == 1)
   size_t scratch_bytes = 0;   // other device scratch (256-byte multiple)
 };
+// Split-K tile counters of the MFMA decode are kCounterStride uint32 apart (one
+// 128-byte line each).
+constexpr int kCounterStride = 32;
 struct SplitKWorkspace {
   float* partials = nullptr;     // split-K partial sums
   uint32_t* counters = nullptr;  // zero between launches (the kernel resets them)
@@ -162,6 +165,10 @@ int topk_max_n(int k);
 size_t top_tokens_workspace_floats(int rows, int64_t n, int top_n);
 hipError_t launch_top_tokens(const float* x, int rows, int64_t n, int top_n, float temperature,
                              int32_t* ids, float* probs, float* workspace, hipStream_t stream);
+
+// p[i] = v for i < n (clears workspace counters: a kernel, so that a captured
+// call records no memset node).
+hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t stream);
 
 // y = silu(g) * u over n fp32 elements.
 hipError_t launch_swiglu(const float* g, const float* u, float* y, int64_t n,

@@ -864,6 +864,188 @@ static void test_executor_tiled_weights() {
   std::printf("  PASS test_executor_tiled_weights\n");
 }
 
+static std::vector<uint8_t> random_q8(int64_t N, int64_t K, uint32_t seed) {
+  std::vector<uint8_t> w(size_t(N) * (K / 32) * 34);
+  uint32_t st = seed;
+  for (size_t b = 0; b < w.size() / 34; ++b) {
+    w[b * 34] = 0x00;
+    w[b * 34 + 1] = 0x1c;  // scale 2^-8
+    for (int i = 0; i < 32; ++i) {
+      st = st * 1664525u + 1013904223u;
+      w[b * 34 + 2 + i] = static_cast<uint8_t>(int8_t((st >> 24) % 255) - 127);
+    }
+  }
+  return w;
+}
+
+static void test_workspace_no_regrowth() {
+  // A counter-heavy launch (many row tiles, few K splits) and a partial-heavy
+  // one (few tiles, many splits) alternating on one stream: the workspace grows
+  // at most once for each, then never again (each buffer keeps
+  // max(capacity, need)); results stay the same run to run.
+  hipStream_t stream;
+  check_hip(hipStreamCreate(&stream));
+  struct Shape3 { int M, N, K; };
+  const Shape3 a{4, 32768, 2048}, b{16, 1024, 65536};
+  size_t ab = 0, ac = 0, bb = 0, bc = 0;
+  CHECK(mle_q8_0_workspace_size(MLE_OP_LINEAR, a.M, 1, &a.N, a.K, 0, &ab, &ac) == 0);
+  CHECK(mle_q8_0_workspace_size(MLE_OP_LINEAR, b.M, 1, &b.N, b.K, 0, &bb, &bc) == 0);
+  CHECK(ac > 4096 && bc < ac);  // a needs more counters than the minimum, b fewer
+  CHECK(bb > ab && bb > (size_t(4) << 20));
+  std::vector<DevBuf<uint8_t>*> w;
+  std::vector<DevBuf<float>*> x, y;
+  for (const Shape3& s : {a, b}) {
+    const auto hw = random_q8(s.N, s.K, 7u + s.N);
+    w.push_back(new DevBuf<uint8_t>(hw.size()));
+    w.back()->put(hw);
+    std::vector<float> hx(size_t(s.M) * s.K);
+    for (size_t i = 0; i < hx.size(); ++i) hx[i] = float(int(i * 37 % 201) - 100) * 0.01f;
+    x.push_back(new DevBuf<float>(hx.size()));
+    x.back()->put(hx);
+    y.push_back(new DevBuf<float>(size_t(s.M) * s.N));
+  }
+  size_t cap_b = 0, cap_c = 0;
+  uint64_t gen0 = 0, gen = 0;
+  CHECK(mle_workspace_info(stream, &cap_b, &cap_c, &gen0) == 0);
+  CHECK(gen0 == 0 && cap_b == 0 && cap_c == 0);  // a fresh stream has none yet
+  std::vector<float> first;
+  for (int it = 0; it < 6; ++it) {
+    const Shape3& s = it % 2 ? b : a;
+    const int i = it % 2;
+    CHECK(mle_q8_0_linear(x[i]->p, w[i]->p, nullptr, y[i]->p, s.M, s.N, s.K, stream) == 0);
+    check_hip(hipStreamSynchronize(stream));
+    CHECK(mle_workspace_info(stream, &cap_b, &cap_c, &gen) == 0);
+    if (it == 0) first = y[0]->get();
+    CHECK(gen == uint64_t(it < 2 ? it + 1 : 2));  // grows on the first a and the first b only
+    CHECK(cap_b >= (it == 0 ? ab : bb) && cap_c >= ac);
+  }
+  CHECK(cap_b == bb && cap_c == ac);
+  CHECK(y[0]->get() == first);  // deterministic
+  for (auto* p : w) delete p;
+  for (auto* p : x) delete p;
+  for (auto* p : y) delete p;
+  // A reservation that covers both up front: no growth at all afterwards.
+  hipStream_t s2;
+  check_hip(hipStreamCreate(&s2));
+  CHECK(mle_workspace_reserve(std::max(ab, bb), std::max(ac, bc), s2) == 0);
+  CHECK(mle_workspace_info(s2, &cap_b, &cap_c, &gen) == 0);
+  CHECK(gen == 1 && cap_b >= bb && cap_c >= ac);
+  CHECK(mle_workspace_reserve(ab, ac, s2) == 0);  // within capacity: nothing happens
+  CHECK(mle_workspace_info(s2, &cap_b, &cap_c, &gen) == 0 && gen == 1);
+  check_hip(hipStreamDestroy(s2));
+  check_hip(hipStreamDestroy(stream));
+  std::printf("  workspace_no_regrowth ok\n");
+}
+
+static void test_executor_reserves_workspace() {
+  // compile() reserves the executor stream's workspace for the plan's largest
+  // Linear (here a split-K MFMA decode at M = 8), so run() allocates nothing:
+  // the workspace generation does not move across runs.
+  const int M = 8, N = 4096, K = 11008;
+  hipStream_t stream;
+  check_hip(hipStreamCreate(&stream));
+  Graph g;
+  GraphBuilder gb(g);
+  const Device dev = Device::hip(0);
+  auto x = gb.input("x", Shape({M, K}), DType::Float32, dev);
+  auto w = gb.constant("w", Shape({N, K}), DType::Float32, dev);
+  CHECK(x && w);
+  auto y = gb.linear(*x, *w, std::nullopt, "down");
+  CHECK(y && gb.output(*y, "out"));
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  HipExecutor ex(std::make_shared<HipBackend>(), registry, stream);
+  check_status(ex.compile(g));
+  size_t need_b = 0, need_c = 0, cap_b = 0, cap_c = 0;
+  CHECK(mle_q8_0_workspace_size(MLE_OP_LINEAR, M, 1, &N, K, 0, &need_b, &need_c) == 0);
+  CHECK(need_b > 0 && need_c > 0);
+  CHECK(ex.workspace_bytes() >= need_b && ex.workspace_counters() >= need_c);
+  uint64_t gen = 0, gen2 = 0;
+  CHECK(mle_workspace_info(stream, &cap_b, &cap_c, &gen) == 0);
+  CHECK(gen >= 1 && cap_b >= need_b && cap_c >= need_c);
+  const auto hw = random_q8(N, K, 99);
+  Tensor tw("w", Shape({N, K}), DType::Q8_0, dev);
+  check_status(tw.allocate_hip_bytes(hw.size()));
+  upload(tw, hw.data(), hw.size());
+  std::vector<float> hx(size_t(M) * K);
+  for (size_t i = 0; i < hx.size(); ++i) hx[i] = float(int(i * 13 % 97) - 48) * 0.03f;
+  Tensor tx("x", Shape({M, K}), DType::Float32, dev);
+  check_status(tx.allocate_hip());
+  upload(tx, hx.data(), hx.size() * 4);
+  RuntimeContext ctx;
+  check_status(ctx.bind(*x, &tx));
+  check_status(ctx.bind(*w, &tw));
+  check_status(ctx.allocate_intermediates(g));
+  for (int r = 0; r < 3; ++r) check_status(ex.run(ctx));
+  check_hip(hipStreamSynchronize(stream));
+  CHECK(mle_workspace_info(stream, &cap_b, &cap_c, &gen2) == 0);
+  CHECK(gen2 == gen);
+  // and after tiling the weight (the tiled launch fits the same reservation)
+  check_status(ex.tile_weights(ctx));
+  check_status(ex.run(ctx));
+  check_hip(hipStreamSynchronize(stream));
+  CHECK(ex.tiled_launches() == 1u);
+  CHECK(mle_workspace_info(stream, &cap_b, &cap_c, &gen2) == 0 && gen2 == gen);
+  check_hip(hipStreamDestroy(stream));
+  std::printf("  executor_reserves_workspace ok\n");
+}
+
+static void test_tiled_copy_shape_guard() {
+  // A tiled copy is used only for the weight shape it was made for: after the
+  // executor is recompiled for a graph that views the same weight buffer as
+  // [N/2, 2K], its Linear runs on the raw bytes and matches the raw launcher.
+  const int M = 2, N = 64, K = 128;
+  const auto hw = random_q8(N, K, 5);
+  DevBuf<uint8_t> buf(hw.size());
+  buf.put(hw);
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  HipExecutor exe(std::make_shared<HipBackend>(), registry);
+  Graph graphs[2];
+  const Device dev = Device::hip(0);
+  for (int pass = 0; pass < 2; ++pass) {
+    const int n = pass ? N / 2 : N, k = pass ? 2 * K : K;
+    Graph& g = graphs[pass];
+    GraphBuilder gb(g);
+    auto x = gb.input("x", Shape({M, k}), DType::Float32, dev);
+    auto w = gb.constant("w", Shape({n, k}), DType::Float32, dev);
+    CHECK(x && w);
+    auto y = gb.linear(*x, *w, std::nullopt, "lin");
+    CHECK(y && gb.output(*y, "out"));
+    std::vector<float> hx(size_t(M) * k);
+    for (size_t i = 0; i < hx.size(); ++i) hx[i] = float(int(i * 7 % 31) - 15) * 0.1f;
+    Tensor tx("x", Shape({M, k}), DType::Float32, dev);
+    check_status(tx.allocate_hip());
+    upload(tx, hx.data(), hx.size() * 4);
+    Tensor tw("w", Shape({n, k}), DType::Q8_0, dev);
+    check_status(tw.bind_hip_data(buf.p, hw.size()));
+    RuntimeContext ctx;
+    check_status(ctx.bind(*x, &tx));
+    check_status(ctx.bind(*w, &tw));
+    check_status(ctx.allocate_intermediates(g));
+    check_status(exe.compile(g));
+    if (pass == 0) check_status(exe.tile_weights(ctx));
+    CHECK(exe.tiled_weights() == 1u);  // the copy of pass 0 is still held in pass 1
+    check_status(exe.run(ctx));
+    check_hip(hipDeviceSynchronize());
+    CHECK(exe.tiled_launches() == (pass == 0 ? 1u : 0u));
+    DevBuf<float> ref(size_t(M) * n);
+    DevBuf<float> dx(hx.size());
+    dx.put(hx);
+    CHECK(mle_q8_0_linear(dx.p, buf.p, nullptr, ref.p, M, n, k, nullptr) == 0);
+    check_hip(hipDeviceSynchronize());
+    const auto got = download(ctx.get(*y), size_t(M) * n);
+    const auto want = ref.get();
+    double num = 0, den = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+      num += double(got[i] - want[i]) * (got[i] - want[i]);
+      den += double(want[i]) * want[i];
+    }
+    CHECK(std::sqrt(num / den) <= 1e-6);
+  }
+  std::printf("  tiled_copy_shape_guard ok\n");
+}
+
 int main() {
   int count = 0;
   check_hip(hipGetDeviceCount(&count));
@@ -880,6 +1062,9 @@ int main() {
   test_fused_launchers();
   test_executor_fusion_end_to_end();
   test_executor_tiled_weights();
+  test_workspace_no_regrowth();
+  test_executor_reserves_workspace();
+  test_tiled_copy_shape_guard();
   std::printf("test_hip_q8_0: all passed\n");
   return 0;
 }

@@ -26,7 +26,7 @@ def declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     lib = capi.load()
-    assert lib.mle_q8_0_abi_version() == 5
+    assert lib.mle_q8_0_abi_version() == 6
     out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH],
                          stdout=subprocess.PIPE, text=True, check=True).stdout
     exported = set(re.findall(r" T (mle_\w+)", out))
@@ -275,3 +275,50 @@ def test_tile_validation_errors():
     code, msg = capi.linear_multi_status(FAKE, [FAKE, FAKE + 4], None, [FAKE, FAKE], [16, 16],
                                          1, 32, stream=0, tiled=True)
     assert code == 1 and "16-byte aligned" in msg
+
+
+def test_workspace_growth_rule():
+    """Capacities never shrink; a buffer that grows takes max(capacity, need, minimum),
+    so alternating a counter-heavy and a partial-heavy need settles after one pair."""
+    MIN_B, MIN_C = 4 << 20, 4096
+    assert capi.workspace_plan_growth(0, 0, 100, 10) == (True, MIN_B, MIN_C)
+    assert capi.workspace_plan_growth(MIN_B, MIN_C, MIN_B, MIN_C) == (False, MIN_B, MIN_C)
+    # more counters only: the partial buffer keeps its (larger) capacity
+    assert capi.workspace_plan_growth(64 << 20, MIN_C, 1 << 20, 20000) == (True, 64 << 20, 20000)
+    # more bytes only: the counter buffer keeps its capacity
+    assert capi.workspace_plan_growth(MIN_B, 20000, 8 << 20, 10) == (True, 8 << 20, 20000)
+    caps, grows = (0, 0), 0
+    for need in [(8 << 20, 100), (1 << 20, 50000)] * 3:
+        grow, b, c = capi.workspace_plan_growth(*caps, *need)
+        grows += grow
+        caps = (b, c)
+    assert grows == 2 and caps == (8 << 20, 50000)
+
+
+def test_workspace_size_matches_launch_plan():
+    """mle_q8_0_workspace_size runs the path choice of the Linear calls without launching
+    (no GPU needed): decode launches with K split need partials and 128-byte counters;
+    the FP32 GEMV and the tiled GEMV need nothing; prefill needs the bf16 copy of X."""
+    ws = capi.workspace_size
+    assert ws(capi.OP_LINEAR, 1, [4096], 4096) == (0, 0)              # FP32 GEMV
+    assert ws(capi.OP_LINEAR, 1, [4096], 4096, tiled=True) == (0, 0)  # tiled GEMV
+    b, c = ws(capi.OP_LINEAR, 8, [4096], 11008)                       # MFMA decode, 22 splits
+    # every row x 22 K slices x 8 tokens of partial floats; 32 counters per row tile
+    # (4-wave tiles of 64 rows on raw weights, 8-wave tiles of 128 rows when tiled)
+    assert b == 4096 * 22 * 8 * 4 and c == (4096 // 64) * 32
+    assert ws(capi.OP_LINEAR, 8, [4096], 11008, tiled=True) == (b, (4096 // 128) * 32)
+    bg, cg = ws(capi.OP_LINEAR, 512, [11008], 4096)                   # prefill GEMM
+    assert bg >= 512 * 4096 * 2                                       # bf16 copy of X
+    b3, c3 = ws(capi.OP_LINEAR_MULTI, 8, [4096, 4096, 4096], 4096)
+    b1, c1 = ws(capi.OP_LINEAR, 8, [12288], 4096)
+    assert b3 > 0 and c3 > 0 and b1 > 0
+    bs, cs = ws(capi.OP_LINEAR_SWIGLU, 4, [11008, 11008], 4096)
+    assert bs > 0 and cs > 0
+    # chunks of 16 tokens share one workspace: the need is the largest chunk's
+    assert ws(capi.OP_LINEAR, 40, [4096], 11008) == ws(capi.OP_LINEAR, 16, [4096], 11008)
+    code, msg, _, _ = capi.workspace_size_status(capi.OP_LINEAR, 1, [64], 48)
+    assert code == 4 and "multiple of 32" in msg
+    code, msg, _, _ = capi.workspace_size_status(capi.OP_LINEAR_SWIGLU, 1, [64, 32], 64)
+    assert code == 1 and "equal N" in msg
+    code, msg, _, _ = capi.workspace_size_status(7, 1, [64], 64)
+    assert code == 1 and "unknown op" in msg

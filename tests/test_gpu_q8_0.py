@@ -351,6 +351,39 @@ def test_linear_decode_mfma_two_streams_concurrently(dev, orc):
             assert rel_l2(to_host(y), want) <= GEMV_TOL
 
 
+def test_linear_decode_mfma_split_k_after_poisoned_workspace(dev, orc):
+    """The split-K hand-off reads only partials written by its own launch: before each
+    split-K launch, a launch of another shape on the same stream fills the same
+    workspace lines with NaN partials (NaN activations, 22 splits).  Every result of
+    the split-K shapes (8, 16 and 22 splits; raw and tiled weights) stays finite and
+    within 1e-5 relative L2 of the oracle."""
+    import torch
+    Mp, Np, Kp = 8, 4096, 11008
+    xp = np.full((Mp, Kp), np.nan, dtype=np.float32)
+    dwp, dxp = to_dev(weight(130, Np, Kp), dev), to_dev(xp, dev)
+    yp = empty_f32((Mp, Np), dev)
+    cases = [(8, 4096, 4096, False), (4, 4096, 11008, False), (8, 4096, 8192, True)]
+    for M, N, K, tiled in cases:
+        note(f"split-K after poisoned workspace M={M} N={N} K={K} tiled={tiled}")
+        w, x = weight(131 + K, N, K), acts(132 + M, M, K)
+        want = orc.sgemm_nt(x, w, M, N, K)
+        dw, dx = to_dev(w, dev), to_dev(x, dev)
+        if tiled:
+            dwt = torch.empty(capi.tiled_bytes(N, K), dtype=torch.uint8, device=dev)
+            capi.tile(dw, dwt, N, K)
+            dw = dwt
+        lin = capi.linear_tiled if tiled else capi.linear
+        for _ in range(3):
+            capi.linear(dxp, dwp, None, yp, Mp, Np, Kp)     # NaN partials everywhere
+            y = empty_f32((M, N), dev)
+            lin(dx, dw, None, y, M, N, K)
+            torch.cuda.synchronize()
+            got = to_host(y)
+            assert np.isfinite(got).all()
+            assert rel_l2(got, want) <= GEMV_TOL
+        assert np.isnan(to_host(yp)).all()
+
+
 # ----------------------------------------------------------------------------- linear MFMA
 
 @pytest.mark.parametrize("M,N,K", [(64, 64, 64), (65, 130, 96), (128, 128, 128),
