@@ -254,6 +254,23 @@ int mle_workspace_plan_growth(size_t cap_bytes, size_t cap_counters, size_t need
                               size_t need_counters, size_t* new_bytes, size_t* new_counters);
 
 /*
+ * mle_q8_0_linear without any allocation, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same operands, paths,
+ * kernels, results (bit-identical to mle_q8_0_linear) and errors, but the
+ * split-K partials, tile counters and prefill scratch live in one static device
+ * array per GPU (32 MiB + 65536 counters, held from library load until process
+ * exit) instead of the per-stream workspace; nothing is allocated or freed.
+ * A shape needing more scratch than that is rejected with Unsupported before
+ * any launch (every BASELINE shape fits: prefill [512 x 4096 x 11008] takes
+ * 28 MB).  All calls on one GPU share the array: calls that overlap in time on
+ * one GPU (different streams, or threads without ordering) race and give wrong
+ * results; calls ordered on one stream do not.
+ */
+int mle_q8_0_linear_noalloc(const float* x, const uint8_t* w_q8_0, const float* bias,
+                            float* y, int M, int N, int K, hipStream_t stream);
+
+/*
  * Message of the last failed call on this thread ("" if none).  Stands in for
  * the message of the reference's Status return (status.h:34-59).  The pointer
  * stays valid until the next call on the same thread.

@@ -26,7 +26,7 @@ EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode", "mle_q8_0_tiled_bytes",
             "mle_q8_0_tile", "mle_q8_0_linear_tiled", "mle_q8_0_linear_swiglu_tiled",
             "mle_q8_0_linear_multi_tiled", "mle_q8_0_workspace_size", "mle_workspace_reserve",
-            "mle_workspace_info", "mle_workspace_plan_growth")
+            "mle_workspace_info", "mle_workspace_plan_growth", "mle_q8_0_linear_noalloc")
 
 OP_LINEAR, OP_LINEAR_SWIGLU, OP_LINEAR_MULTI = 0, 1, 2
 
@@ -90,6 +90,8 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_linear_swiglu_tiled.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_q8_0_linear_multi_tiled.restype = _i
     lib.mle_q8_0_linear_multi_tiled.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp]
+    lib.mle_q8_0_linear_noalloc.restype = _i
+    lib.mle_q8_0_linear_noalloc.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
     _sz = ctypes.c_size_t
     lib.mle_q8_0_workspace_size.restype = _i
     lib.mle_q8_0_workspace_size.argtypes = [_i, _i, _i, _vp, _i, _i, _vp, _vp]
@@ -142,6 +144,18 @@ def linear_status(x, w, bias, y, M, N, K, stream=None):
 def linear(x, w, bias, y, M, N, K, stream=None) -> None:
     """y[M,N] = x[M,K] . W^T (+ bias); W raw Q8_0 [N,K]."""
     _raise(linear_status(x, w, bias, y, M, N, K, stream)[0])
+
+
+def linear_noalloc_status(x, w, bias, y, M, N, K, stream=None):
+    rc = load().mle_q8_0_linear_noalloc(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K,
+                                        _stream(stream))
+    return _status(rc)
+
+
+def linear_noalloc(x, w, bias, y, M, N, K, stream=None) -> None:
+    """linear() with its workspace in the library's static device scratch (no
+    allocation; calls overlapping on one GPU race)."""
+    _raise(linear_noalloc_status(x, w, bias, y, M, N, K, stream)[0])
 
 
 def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice=0,

@@ -187,6 +187,13 @@ struct Exec {
   hipStream_t stream = nullptr;
   size_t* plan_bytes = nullptr;     // non-null: plan mode
   size_t* plan_counters = nullptr;
+  // A caller-fixed workspace (the no-allocation entry point): the launches use
+  // these buffers and nothing is allocated.
+  bool fixed = false;
+  uint8_t* fixed_buf = nullptr;
+  size_t fixed_bytes = 0;
+  uint32_t* fixed_counters = nullptr;
+  size_t fixed_counter_count = 0;
   bool planning() const { return plan_bytes != nullptr; }
 };
 
@@ -195,6 +202,22 @@ int workspace_for(const mle::SplitKNeed& need, const Exec& ex, mle::SplitKWorksp
     *out = mle::SplitKWorkspace{};
     *ex.plan_bytes = std::max(*ex.plan_bytes, need_bytes(need));
     *ex.plan_counters = std::max(*ex.plan_counters, need.counters);
+    return MLE_OK;
+  }
+  if (ex.fixed) {
+    *out = mle::SplitKWorkspace{};
+    const size_t bytes = need_bytes(need);
+    if (bytes > ex.fixed_bytes || need.counters > ex.fixed_counter_count)
+      return fail(MLE_UNSUPPORTED, "hip Q8_0 fixed workspace too small: need " +
+                                       std::to_string(bytes) + " bytes and " +
+                                       std::to_string(need.counters) + " counters");
+    if (bytes == 0) return MLE_OK;
+    if (ex.fixed_buf == nullptr)
+      return fail(MLE_RUNTIME_ERROR, "hip Q8_0 fixed workspace missing");
+    const size_t partial_bytes = (need.partial_floats * sizeof(float) + 255) / 256 * 256;
+    out->partials = reinterpret_cast<float*>(ex.fixed_buf);
+    out->counters = ex.fixed_counters;
+    out->scratch = need.scratch_bytes ? ex.fixed_buf + partial_bytes : nullptr;
     return MLE_OK;
   }
   return get_workspace(need, ex.stream, out);
@@ -394,6 +417,46 @@ int linear_multi(const float* x, int count, const uint8_t* const* w, const float
   return run_segs(ctx, x, s, M, K, Exec{stream});
 }
 
+// Workspace of mle_q8_0_linear_noalloc: a file-scope device array (each GPU
+// holds its own copy from module load until the process ends), bytes
+// [0, kNoAllocBytes) for partial sums and scratch, then kNoAllocCounters tile
+// counters.  Host code reaches it only through the address that
+// hipGetSymbolAddress returns for the current device (the array's name in host
+// code is a stand-in, not a device address).
+constexpr size_t kNoAllocBytes = size_t(32) << 20;
+constexpr size_t kNoAllocCounters = 65536;
+__device__ __align__(256) uint8_t scratch[kNoAllocBytes + kNoAllocCounters * sizeof(uint32_t)];
+
+struct NoAllocScratch {
+  uint8_t* base = nullptr;  // device address of `scratch` on that device
+};
+std::mutex g_noalloc_mu;
+std::map<int, NoAllocScratch> g_noalloc;  // device -> its scratch
+
+// Device address of `scratch` on the current device; on the first call there,
+// its counters are cleared on `stream` (a fill kernel, enqueued before the
+// caller's launch).  Later launches leave the counters at zero.
+int noalloc_scratch(hipStream_t stream, uint8_t** base) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return check_launch(err, "hip linear_noalloc");
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  auto it = g_noalloc.find(dev);
+  if (it == g_noalloc.end()) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return check_launch(err == hipSuccess ? hipErrorInvalidSymbol : err,
+                          "hip linear_noalloc: scratch address");
+    err = mle::launch_fill_u32(reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p) + kNoAllocBytes),
+                               kNoAllocCounters, 0u, stream);
+    if (err != hipSuccess) return check_launch(err, "hip linear_noalloc: clearing counters");
+    it = g_noalloc.emplace(dev, NoAllocScratch{static_cast<uint8_t*>(p)}).first;
+  }
+  *base = it->second.base;
+  return MLE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -507,6 +570,37 @@ int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const*
                                 const float* const* bias, float* const* y, const int* N, int M,
                                 int K, hipStream_t stream) {
   return linear_multi(x, count, w, bias, y, N, M, K, stream, mle::WeightLayout::kTiled);
+}
+
+int mle_q8_0_linear_noalloc(const float* x, const uint8_t* w_q8_0, const float* bias,
+                            float* y, int M, int N, int K, hipStream_t stream) {
+  MLE_TRY(validate_linear(x, w_q8_0, bias, y, M, N, K));
+  size_t bytes = 0, counters = 0;
+  {
+    Exec plan;
+    plan.plan_bytes = &bytes;
+    plan.plan_counters = &counters;
+    MLE_TRY(run_linear(x, w_q8_0, bias, y, M, N, K, 0, Tune{}, plan));
+  }
+  if (bytes > kNoAllocBytes || counters > kNoAllocCounters)
+    return fail(MLE_UNSUPPORTED,
+                "hip linear_noalloc: this shape needs " + std::to_string(bytes) +
+                    " bytes and " + std::to_string(counters) +
+                    " counters of scratch; the no-allocation entry point holds " +
+                    std::to_string(kNoAllocBytes) + " bytes and " +
+                    std::to_string(kNoAllocCounters) + " counters (use mle_q8_0_linear)");
+  Exec ex;
+  ex.stream = stream;
+  ex.fixed = true;  // launches needing no workspace get none
+  if (bytes != 0 || counters != 0) {
+    uint8_t* base = nullptr;
+    MLE_TRY(noalloc_scratch(stream, &base));
+    ex.fixed_buf = base;
+    ex.fixed_bytes = kNoAllocBytes;
+    ex.fixed_counters = reinterpret_cast<uint32_t*>(base + kNoAllocBytes);
+    ex.fixed_counter_count = kNoAllocCounters;
+  }
+  return run_linear(x, w_q8_0, bias, y, M, N, K, 0, Tune{}, ex);
 }
 
 int mle_q8_0_workspace_size(int op, int M, int count, const int* N, int K, int tiled,
