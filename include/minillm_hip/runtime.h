@@ -198,10 +198,21 @@ void register_hip_kernels(KernelRegistry& registry);
 namespace hip {
 Status sgemm_nt(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
                 const float* bias = nullptr, hipStream_t stream = nullptr);
+// Linear with a BFloat16 bias (mle_q8_0_linear_bias_bf16): the reference's
+// sgemm_nt + add_bias(float*, const uint16_t*, ...) for a BF16 bias
+// (cuda_kernel_adapter.cpp:204-218), fused.
+Status sgemm_nt_bias_bf16(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
+                          const uint16_t* bias_bf16, hipStream_t stream = nullptr);
+Status sgemm_nt_tiled_bias_bf16(const float* A, const uint8_t* B_tiled, float* C, int M, int N,
+                                int K, const uint16_t* bias_bf16, hipStream_t stream = nullptr);
 Status sgemm(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
              hipStream_t stream = nullptr);
 Status embedding(const uint8_t* weight_q8_0, const int* ids, float* out, int seq_len,
                  int vocab_size, int hidden, hipStream_t stream = nullptr);
+// WeightLoader::dequantize_to_f32's Q8_0 case on the device (mle_q8_0_dequantize;
+// reference src/io/gguf_weight_loader.cpp:446-463): out[e] = q * d, e < n.
+Status dequantize_q8_0(const uint8_t* src_q8_0, float* out, int64_t n,
+                       hipStream_t stream = nullptr);
 
 // Fused launchers with no counterpart among the reference's kernels (see
 // mle_q8_0.h): y = silu(x.Wg^T) * (x.Wu^T) in place of Linear + Linear +

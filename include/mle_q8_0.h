@@ -72,6 +72,22 @@ int mle_q8_0_linear(const float* x, const uint8_t* w_q8_0, const float* bias,
                     float* y, int M, int N, int K, hipStream_t stream);
 
 /*
+ * mle_q8_0_linear with a BFloat16 bias: y[M,N] = x . W^T + (float)bias_bf16[N],
+ * the bias widened exactly and added in fp32 once, after the dot product, as
+ * the reference's CUDA adapter does for a BFloat16 bias on a Q8_0 Linear
+ * (cuda_kernel_adapter.cpp:204-218: sgemm_nt, then add_bias(float*, const
+ * uint16_t*, rows, cols), cuda_kernels.cu:229-233, 963-969), fused into the
+ * Linear's epilogue.  bias_bf16 may be NULL (no bias), else 2-byte aligned.
+ * The _tiled form takes weights in 16-row tiles (mle_q8_0_tile).  Paths,
+ * precision and errors as mle_q8_0_linear / mle_q8_0_linear_tiled.
+ */
+int mle_q8_0_linear_bias_bf16(const float* x, const uint8_t* w_q8_0, const uint16_t* bias_bf16,
+                              float* y, int M, int N, int K, hipStream_t stream);
+int mle_q8_0_linear_tiled_bias_bf16(const float* x, const uint8_t* w_tiled,
+                                    const uint16_t* bias_bf16, float* y, int M, int N, int K,
+                                    hipStream_t stream);
+
+/*
  * Fused gate/up Linear + SwiGLU: y[M,N] = silu(x . Wg^T) * (x . Wu^T), with
  * silu(g) = g / (1 + exp(-g)) evaluated as the reference does
  * (src/runtime/kernels/cpu_kernels.cpp:848-858).  Wg and Wu are [N,K] Q8_0.
@@ -133,6 +149,18 @@ int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M,
  */
 int mle_q8_0_embedding(const uint8_t* table_q8_0, const int32_t* ids, float* out,
                        int seq_len, int vocab, int hidden, hipStream_t stream);
+
+/*
+ * Q8_0 -> fp32 dequantisation of a whole tensor on the device: dst[e] = q * d
+ * for the n elements of the raw block stream (ceil(n/32) blocks; a partial last
+ * block reads only its first n % 32 quants).  Replaces the Q8_0 case of
+ * WeightLoader::dequantize_to_f32 (reference src/io/gguf_weight_loader.cpp:446-463),
+ * which the loader runs on the host for Float32 tensors; bit-identical to it
+ * (one fp32 multiply of an exactly decoded binary16 scale).
+ * Errors: NULL pointers or n < 0 -> InvalidArgument; src must be 2-byte and dst
+ * 16-byte aligned.  n == 0 is a no-op.
+ */
+int mle_q8_0_dequantize(const uint8_t* src_q8_0, float* dst, int64_t n, hipStream_t stream);
 
 /*
  * Unfused SwiGLU: y[i] = silu(gate[i]) * up[i] for i < n (n == 0: no-op),

@@ -26,7 +26,9 @@ EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode", "mle_q8_0_tiled_bytes",
             "mle_q8_0_tile", "mle_q8_0_linear_tiled", "mle_q8_0_linear_swiglu_tiled",
             "mle_q8_0_linear_multi_tiled", "mle_q8_0_workspace_size", "mle_workspace_reserve",
-            "mle_workspace_info", "mle_workspace_plan_growth", "mle_q8_0_linear_noalloc")
+            "mle_workspace_info", "mle_workspace_plan_growth", "mle_q8_0_linear_noalloc",
+            "mle_q8_0_dequantize", "mle_q8_0_linear_bias_bf16",
+            "mle_q8_0_linear_tiled_bias_bf16")
 
 OP_LINEAR, OP_LINEAR_SWIGLU, OP_LINEAR_MULTI = 0, 1, 2
 
@@ -90,6 +92,11 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_linear_swiglu_tiled.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_q8_0_linear_multi_tiled.restype = _i
     lib.mle_q8_0_linear_multi_tiled.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp]
+    for fn in (lib.mle_q8_0_linear_bias_bf16, lib.mle_q8_0_linear_tiled_bias_bf16):
+        fn.restype = _i
+        fn.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_q8_0_dequantize.restype = _i
+    lib.mle_q8_0_dequantize.argtypes = [_vp, _vp, ctypes.c_int64, _vp]
     lib.mle_q8_0_linear_noalloc.restype = _i
     lib.mle_q8_0_linear_noalloc.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
     _sz = ctypes.c_size_t
@@ -173,6 +180,17 @@ def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice
     rc = load().mle_q8_0_linear_ex(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K,
                                    path, *t, _stream(stream))
     _raise(rc)
+
+
+def linear_bias_bf16_status(x, w, bias_bf16, y, M, N, K, stream=None, tiled=False):
+    fn = (load().mle_q8_0_linear_tiled_bias_bf16 if tiled else load().mle_q8_0_linear_bias_bf16)
+    rc = fn(_addr(x), _addr(w), _addr(bias_bf16), _addr(y), M, N, K, _stream(stream))
+    return _status(rc)
+
+
+def linear_bias_bf16(x, w, bias_bf16, y, M, N, K, stream=None, tiled=False) -> None:
+    """y[M,N] = x . W^T + (float)bias_bf16 (bias as raw bf16 bits, uint16 [N])."""
+    _raise(linear_bias_bf16_status(x, w, bias_bf16, y, M, N, K, stream, tiled)[0])
 
 
 def linear_swiglu_status(x, w_gate, w_up, y, M, N, K, stream=None):
@@ -259,6 +277,16 @@ def top_tokens(logits, rows, n, top_n, ids, probs, temperature=1.0, stream=None)
     """ids/probs [rows, min(top_n, n)]: the top tokens of each logits row by softmax
     probability (after 1/temperature), largest first (Sampler::get_top_tokens)."""
     _raise(top_tokens_status(logits, rows, n, top_n, ids, probs, temperature, stream)[0])
+
+
+def dequantize_status(src, dst, n, stream=None):
+    rc = load().mle_q8_0_dequantize(_addr(src), _addr(dst), n, _stream(stream))
+    return _status(rc)
+
+
+def dequantize(src, dst, n, stream=None) -> None:
+    """dst[e] = q * d for the n elements of a raw Q8_0 block stream."""
+    _raise(dequantize_status(src, dst, n, stream)[0])
 
 
 def f16_decode(bits, out, n, stream=None) -> None:

@@ -72,8 +72,8 @@ int check_align(const char* ctx, const void* p, uintptr_t a, const char* name) {
     if (_rc != MLE_OK) return _rc; \
   } while (0)
 
-int validate_linear(const float* x, const uint8_t* w, const float* bias, float* y,
-                    int M, int N, int K) {
+int validate_linear(const float* x, const uint8_t* w, const void* bias, float* y,
+                    int M, int N, int K, uintptr_t bias_align = 4) {
   const char* ctx = "sgemm_nt_q8_0_weight";
   MLE_TRY(check_ptrs(ctx, x, "A", w, "B", y, "C"));
   MLE_TRY(check_positive(ctx, M, "M"));
@@ -84,7 +84,7 @@ int validate_linear(const float* x, const uint8_t* w, const float* bias, float* 
   MLE_TRY(check_align(ctx, x, 16, "A"));
   MLE_TRY(check_align(ctx, w, 2, "B"));
   MLE_TRY(check_align(ctx, y, 16, "C"));
-  MLE_TRY(check_align(ctx, bias, 4, "bias"));
+  MLE_TRY(check_align(ctx, bias, bias_align, "bias"));
   return MLE_OK;
 }
 
@@ -245,9 +245,9 @@ struct Tune {
 // mle::gemv_tiled_wins (one token; two below vocabulary-sized outputs; up to
 // four on short rows), else the MFMA decode below 64 tokens and the MFMA GEMM
 // from 64.
-int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, int M,
+int run_linear(const float* x, const uint8_t* w, const void* bias, float* y, int M,
                int N, int K, int path, const Tune& tune, const Exec& ex,
-               mle::WeightLayout layout = mle::WeightLayout::kRaw) {
+               mle::WeightLayout layout = mle::WeightLayout::kRaw, bool bias_bf16 = false) {
   const bool tiled = layout == mle::WeightLayout::kTiled;
   if (path == 0) {
     path = tiled ? (M >= 64 ? 2 : 3) : pick_path(M, N, K);
@@ -260,6 +260,7 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
   }
   mle::LinearSegs one;
   one.seg[0] = mle::LinearSeg{w, bias, y, N};
+  one.seg[0].bias_bf16 = bias_bf16 ? 1 : 0;
   one.layout = layout;
   if (tiled && path == 3 && M <= 4 && mle::gemv_tiled_wins(M, N, K)) {
     const mle::TiledGemvConfig c = mle::gemv_tiled_pick(M, N, K, false);
@@ -316,8 +317,11 @@ int run_linear(const float* x, const uint8_t* w, const float* bias, float* y, in
       return fail(MLE_INVALID_ARGUMENT, "hip sgemm_nt_q8_0_weight: GEMV token tile " +
                                             std::to_string(c.mt) + " is smaller than M");
     }
-    const hipError_t err = (ex.planning() ? hipSuccess : mle::launch_gemv(c, x + (int64_t)m0 * K, w, bias,
-                                            y + (int64_t)m0 * N, mc, N, K, ex.stream));
+    mle::LinearSegs chunk = one;
+    chunk.seg[0].y = y + (int64_t)m0 * N;
+    const hipError_t err =
+        ex.planning() ? hipSuccess
+                      : mle::launch_gemv_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ex.stream);
     if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 launch failed");
   }
   return ok();
@@ -553,6 +557,22 @@ int mle_q8_0_tile(const uint8_t* w_q8_0, uint8_t* w_tiled, int N, int K, hipStre
                       "hip tile_q8_0 launch failed");
 }
 
+int mle_q8_0_linear_bias_bf16(const float* x, const uint8_t* w_q8_0, const uint16_t* bias_bf16,
+                              float* y, int M, int N, int K, hipStream_t stream) {
+  MLE_TRY(validate_linear(x, w_q8_0, bias_bf16, y, M, N, K, 2));
+  return run_linear(x, w_q8_0, bias_bf16, y, M, N, K, 0, Tune{}, Exec{stream},
+                    mle::WeightLayout::kRaw, true);
+}
+
+int mle_q8_0_linear_tiled_bias_bf16(const float* x, const uint8_t* w_tiled,
+                                    const uint16_t* bias_bf16, float* y, int M, int N, int K,
+                                    hipStream_t stream) {
+  MLE_TRY(validate_linear(x, w_tiled, bias_bf16, y, M, N, K, 2));
+  MLE_TRY(check_align("sgemm_nt_q8_0_tiled", w_tiled, 16, "B"));
+  return run_linear(x, w_tiled, bias_bf16, y, M, N, K, 0, Tune{}, Exec{stream},
+                    mle::WeightLayout::kTiled, true);
+}
+
 int mle_q8_0_linear_tiled(const float* x, const uint8_t* w_tiled, const float* bias, float* y,
                           int M, int N, int K, hipStream_t stream) {
   MLE_TRY(validate_linear(x, w_tiled, bias, y, M, N, K));
@@ -777,6 +797,16 @@ int mle_q8_0_embedding(const uint8_t* table_q8_0, const int32_t* ids, float* out
   return check_launch(
       mle::launch_embedding(table_q8_0, ids, out, seq_len, vocab, hidden, stream),
       "hip embedding Q8_0 launch failed");
+}
+
+int mle_q8_0_dequantize(const uint8_t* src_q8_0, float* dst, int64_t n, hipStream_t stream) {
+  const char* ctx = "dequantize_q8_0";
+  MLE_TRY(check_ptrs(ctx, src_q8_0, "src", dst, "dst", dst, "dst"));
+  if (n < 0) return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": n must not be negative");
+  MLE_TRY(check_align(ctx, src_q8_0, 2, "src"));
+  MLE_TRY(check_align(ctx, dst, 16, "dst"));
+  return check_launch(mle::launch_dequantize_q8_0(src_q8_0, dst, n, stream),
+                      "hip dequantize_q8_0 launch failed");
 }
 
 int mle_q8_0_f16_decode(const uint16_t* bits, float* out, int64_t n, hipStream_t stream) {

@@ -51,6 +51,16 @@ Status check_hip_device(const Tensor* t, std::string_view name) {
   return Status::make_ok();
 }
 
+// Linear bias: Float32 or BFloat16, as the reference's CUDA adapter accepts
+// (cuda_kernel_adapter.cpp:48-59, 204-218).
+Status check_hip_float_or_bf16(const Tensor* t, std::string_view name) {
+  TRY(check_allocated(t, name));
+  TRY(check_hip_device(t, name));
+  if (t->dtype() == DType::Float32 || t->dtype() == DType::BFloat16) return Status::make_ok();
+  return Status::unsupported(std::string(name) + " supports Float32 or BFloat16, got " +
+                             std::string(dtype_name(t->dtype())));
+}
+
 Status check_hip_float(const Tensor* t, std::string_view name) {
   TRY(check_allocated(t, name));
   TRY(check_hip_device(t, name));
@@ -177,23 +187,31 @@ Status kernel_linear(const Node& node, RuntimeContext& ctx) {
   if (*wk != *K)
     return Status::shape_mismatch("Linear x last dimension must match weight input dimension");
 
-  const float* bias = nullptr;
+  const void* bias = nullptr;
+  bool bias_bf16 = false;
   if (node.inputs().size() >= 3) {
     auto bt = get_tensor(node.inputs()[2], ctx, "bias");
     if (!bt) return bt.error();
-    TRY(check_hip_float(*bt, "bias"));
+    TRY(check_hip_float_or_bf16(*bt, "bias"));
     if ((*bt)->shape().rank() != 1 || (*bt)->shape().dim(0) != *N)
       return Status::shape_mismatch("Linear bias shape must match output features");
-    TRY(check_storage_bytes(*bt, static_cast<size_t>(*N) * 4, "bias"));
-    bias = static_cast<const float*>((*bt)->data());
+    bias_bf16 = (*bt)->dtype() == DType::BFloat16;
+    TRY(check_storage_bytes(*bt, static_cast<size_t>(*N) * (bias_bf16 ? 2 : 4), "bias"));
+    bias = (*bt)->data();
   }
   TRY(check_q8_block_aligned(*K, "linear"));
   TRY(check_q8_storage_bytes(*wt, "linear weight"));
   TRY(check_storage_bytes(*xt, static_cast<size_t>(*M) * static_cast<size_t>(*K) * 4, "x"));
   TRY(check_storage_bytes(*ot, static_cast<size_t>(*M) * static_cast<size_t>(*N) * 4, "output"));
+  if (bias_bf16)
+    return hip::sgemm_nt_bias_bf16(static_cast<const float*>((*xt)->data()),
+                                   static_cast<const uint8_t*>((*wt)->data()),
+                                   static_cast<float*>((*ot)->data()), *M, *N, *K,
+                                   static_cast<const uint16_t*>(bias), ctx.hip_stream());
   return hip::sgemm_nt(static_cast<const float*>((*xt)->data()),
                        static_cast<const uint8_t*>((*wt)->data()),
-                       static_cast<float*>((*ot)->data()), *M, *N, *K, bias, ctx.hip_stream());
+                       static_cast<float*>((*ot)->data()), *M, *N, *K,
+                       static_cast<const float*>(bias), ctx.hip_stream());
 }
 
 Status kernel_swiglu(const Node& node, RuntimeContext& ctx) {
@@ -223,7 +241,8 @@ Status kernel_swiglu(const Node& node, RuntimeContext& ctx) {
 struct LinearOperands {
   const float* x = nullptr;
   const uint8_t* w = nullptr;
-  const float* bias = nullptr;
+  const void* bias = nullptr;
+  bool bias_bf16 = false;
   float* y = nullptr;
   int M = 0, N = 0, K = 0;
   ValueId x_id;
@@ -257,13 +276,14 @@ expected<LinearOperands, Status> linear_operands(const Node& node, RuntimeContex
   if (node.inputs().size() >= 3) {
     auto bt = get_tensor(node.inputs()[2], ctx, "bias");
     if (!bt) return unexpected(bt.error());
-    st = check_hip_float(*bt, "bias");
+    st = check_hip_float_or_bf16(*bt, "bias");
     if (!st.ok()) return unexpected(st);
     if ((*bt)->shape().rank() != 1 || (*bt)->shape().dim(0) != *N)
       return unexpected(Status::shape_mismatch("Linear bias shape must match output features"));
-    st = check_storage_bytes(*bt, static_cast<size_t>(*N) * 4, "bias");
+    o.bias_bf16 = (*bt)->dtype() == DType::BFloat16;
+    st = check_storage_bytes(*bt, static_cast<size_t>(*N) * (o.bias_bf16 ? 2 : 4), "bias");
     if (!st.ok()) return unexpected(st);
-    o.bias = static_cast<const float*>((*bt)->data());
+    o.bias = (*bt)->data();
   }
   st = check_q8_block_aligned(*K, "linear");
   if (st.ok()) st = check_q8_storage_bytes(*wt, "linear weight");
@@ -326,6 +346,16 @@ Status sgemm_nt(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, i
   return from_capi(mle_q8_0_linear(A, B_q8_0, bias, C, M, N, K, stream));
 }
 
+Status sgemm_nt_bias_bf16(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
+                          const uint16_t* bias_bf16, hipStream_t stream) {
+  return from_capi(mle_q8_0_linear_bias_bf16(A, B_q8_0, bias_bf16, C, M, N, K, stream));
+}
+
+Status sgemm_nt_tiled_bias_bf16(const float* A, const uint8_t* B_tiled, float* C, int M, int N,
+                                int K, const uint16_t* bias_bf16, hipStream_t stream) {
+  return from_capi(mle_q8_0_linear_tiled_bias_bf16(A, B_tiled, bias_bf16, C, M, N, K, stream));
+}
+
 Status sgemm(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int K,
              hipStream_t stream) {
   return from_capi(mle_q8_0_matmul(A, B_q8_0, C, M, N, K, stream));
@@ -335,6 +365,10 @@ Status embedding(const uint8_t* weight_q8_0, const int* ids, float* out, int seq
                  int vocab_size, int hidden, hipStream_t stream) {
   return from_capi(mle_q8_0_embedding(weight_q8_0, reinterpret_cast<const int32_t*>(ids), out,
                                       seq_len, vocab_size, hidden, stream));
+}
+
+Status dequantize_q8_0(const uint8_t* src_q8_0, float* out, int64_t n, hipStream_t stream) {
+  return from_capi(mle_q8_0_dequantize(src_q8_0, out, n, stream));
 }
 
 Status linear_swiglu(const float* x, const uint8_t* w_gate_q8_0, const uint8_t* w_up_q8_0,
@@ -399,8 +433,12 @@ expected<bool, Status> run_tiled_linear(const Node& node, RuntimeContext& ctx,
   if (!o) return false;
   const uint8_t* t = tiled_copy_of(&tiled, o->w, o->N, o->K);
   if (t == nullptr) return false;
-  const Status st = hip::sgemm_nt_tiled(o->x, t, o->y, o->M, o->N, o->K, o->bias,
-                                        ctx.hip_stream());
+  const Status st =
+      o->bias_bf16
+          ? hip::sgemm_nt_tiled_bias_bf16(o->x, t, o->y, o->M, o->N, o->K,
+                                          static_cast<const uint16_t*>(o->bias), ctx.hip_stream())
+          : hip::sgemm_nt_tiled(o->x, t, o->y, o->M, o->N, o->K,
+                                static_cast<const float*>(o->bias), ctx.hip_stream());
   if (!st.ok()) return unexpected(st);
   return true;
 }
@@ -440,11 +478,11 @@ expected<bool, Status> run_fused_multi(const std::vector<const Node*>& nodes,
   LinearOperands first;
   for (size_t i = 0; i < nodes.size(); ++i) {
     auto o = linear_operands(*nodes[i], ctx);
-    if (!o) return false;
+    if (!o || o->bias_bf16) return false;  // BF16 biases run node by node
     if (i == 0) first = *o;
     else if (o->x != first.x || o->M != first.M || o->K != first.K) return false;
     w[i] = o->w;
-    b[i] = o->bias;
+    b[i] = static_cast<const float*>(o->bias);
     y[i] = o->y;
     N[i] = o->N;
   }

@@ -187,7 +187,9 @@ __global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
                      : 0;
   const unsigned tile0 = si == 0 ? 0u : si == 1 ? args.tile_end[0] : args.tile_end[1];
   const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
-  const float* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const void* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const int bias_bf16 =
+      si == 0 ? args.seg[0].bias_bf16 : si == 1 ? args.seg[1].bias_bf16 : args.seg[2].bias_bf16;
   float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
   const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
   const int64_t n0 = (int64_t)(tile - tile0) * BNO;
@@ -244,12 +246,14 @@ __global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
         if (m >= M) continue;
         if (vec) {
           if (n >= N) continue;
-          if (bias) val += f32x4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
+          if (bias)
+            val += f32x4{bias_at(bias, bias_bf16, n), bias_at(bias, bias_bf16, n + 1),
+                         bias_at(bias, bias_bf16, n + 2), bias_at(bias, bias_bf16, n + 3)};
           *reinterpret_cast<f32x4*>(y + m * N + n) = val;
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (n + e < N) y[m * N + n + e] = val[e] + (bias ? bias[n + e] : 0.0f);
+            if (n + e < N) y[m * N + n + e] = val[e] + (bias ? bias_at(bias, bias_bf16, n + e) : 0.0f);
         }
       }
     }

@@ -120,7 +120,9 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(const float* __restrict_
                      : 0;
   const unsigned wg0 = si == 0 ? 0u : si == 1 ? args.wg_end[0] : args.wg_end[1];
   const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
-  const float* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const void* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const int bias_bf16 =
+      si == 0 ? args.seg[0].bias_bf16 : si == 1 ? args.seg[1].bias_bf16 : args.seg[2].bias_bf16;
   float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
   const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
   const int64_t row0 = ((int64_t)(wg - wg0) * G + grp) * RW;
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(const float* __restrict_
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       if (row0 + r >= N) continue;
-      const float bv = (!kSwi && bias) ? bias[row0 + r] : 0.0f;
+      const float bv = (!kSwi && bias) ? bias_at(bias, bias_bf16, row0 + r) : 0.0f;
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         if (m >= M) continue;

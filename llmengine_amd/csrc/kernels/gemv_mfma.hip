@@ -261,7 +261,9 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
                      : 0;
   const unsigned tile0 = si == 0 ? 0u : si == 1 ? args.tile_end[0] : args.tile_end[1];
   const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
-  const float* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const void* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const int bias_bf16 =
+      si == 0 ? args.seg[0].bias_bf16 : si == 1 ? args.seg[1].bias_bf16 : args.seg[2].bias_bf16;
   float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
   const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
   const int wrow = kSwi ? wave % RW : wave;  // this wave's 16-row group
@@ -506,7 +508,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
       if constexpr (kSwi)
         y[(int64_t)m * N + n] = silu_mul(gate_out[wrow][64 * o + lane], v[o]);
       else
-        y[(int64_t)m * N + n] = v[o] + (bias ? bias[n] : 0.0f);
+        y[(int64_t)m * N + n] = v[o] + (bias ? bias_at(bias, bias_bf16, n) : 0.0f);
     }
   };
 

@@ -83,7 +83,9 @@ __global__ __launch_bounds__(1024) void gemv_tiled_kernel(const float* __restric
                      : 0;
   const unsigned grp0 = si == 0 ? 0u : si == 1 ? args.grp_end[0] : args.grp_end[1];
   const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
-  const float* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const void* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const int bias_bf16 =
+      si == 0 ? args.seg[0].bias_bf16 : si == 1 ? args.seg[1].bias_bf16 : args.seg[2].bias_bf16;
   float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
   const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
   if (half) w = args.seg[1].w;
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(1024) void gemv_tiled_kernel(const float* __restric
     for (int wi = 0; wi < wpg; ++wi) u += red[((wpg + wi) * MT + m) * 16 + rr];
     y[(int64_t)m * N + n] = silu_mul_t(s, u);
   } else {
-    y[(int64_t)m * N + n] = s + (bias ? bias[n] : 0.0f);
+    y[(int64_t)m * N + n] = s + (bias ? bias_at(bias, bias_bf16, n) : 0.0f);
   }
 }
 

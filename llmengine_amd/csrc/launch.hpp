@@ -50,9 +50,10 @@ int decode_mfma_tile(int M);
 // (gate, up) combined into y = silu(x.Wg^T) * (x.Wu^T) in seg[0].y.
 struct LinearSeg {
   const uint8_t* w = nullptr;
-  const float* bias = nullptr;  // optional; not used in kSwiGLU mode
+  const void* bias = nullptr;  // optional [N], fp32 (bf16 when bias_bf16); not in kSwiGLU mode
   float* y = nullptr;
   int N = 0;
+  int bias_bf16 = 0;
 };
 enum class Epilogue { kPlain = 0, kSwiGLU = 1 };
 // Byte layout of the weights of a launch.
@@ -178,6 +179,10 @@ hipError_t launch_swiglu(const float* g, const float* u, float* y, int64_t n,
 hipError_t launch_embedding(const uint8_t* w, const int32_t* ids, float* out,
                             int64_t seq_len, int vocab, int hidden,
                             hipStream_t stream);
+
+// dst[e] = q * d over the flat element stream of a Q8_0 tensor of n elements
+// (the weight loader's Float32 branch); dst 16-byte aligned.
+hipError_t launch_dequantize_q8_0(const uint8_t* w, float* out, int64_t n, hipStream_t stream);
 
 // Scale decode of raw binary16 patterns (test hook).
 hipError_t launch_f16_decode(const uint16_t* bits, float* out, int64_t n,

@@ -89,6 +89,13 @@ __device__ __forceinline__ Block load_block(const uint8_t* __restrict__ blk) {
   return finish_block(load_block_raw(blk));
 }
 
+// Element n of a Linear bias: fp32, or bf16 widened exactly (the reference's
+// add_bias adds weight_to_f32(bias[n]) in fp32, cuda_kernels.cu:229-233).
+__device__ __forceinline__ float bias_at(const void* bias, int bf16, int64_t n) {
+  if (bf16) return __builtin_bit_cast(float, (uint32_t)static_cast<const uint16_t*>(bias)[n] << 16);
+  return static_cast<const float*>(bias)[n];
+}
+
 // Signed int8 byte j of a dword, as float (one v_cvt_f32_i32 with SDWA sext).
 __device__ __forceinline__ float q_at(uint32_t word, int j) {
   return (float)(int8_t)(word >> (8 * j));

@@ -87,6 +87,8 @@ class Oracle(_Lib):
         self.lib.oracle_embedding_q8_0_zero_fill.restype = None
         self.lib.oracle_add_bias.argtypes = [_f32p, _f32p, _int, _int]
         self.lib.oracle_add_bias.restype = None
+        self.lib.oracle_dequantize_q8_0.argtypes = [_u8p, _f32p, ctypes.c_size_t]
+        self.lib.oracle_dequantize_q8_0.restype = None
 
     def f16_to_f32(self, bits: int) -> float:
         return self.lib.oracle_f16_to_f32(bits)
@@ -102,6 +104,15 @@ class Oracle(_Lib):
         out = np.empty((ids.size, hidden), dtype=np.float32)
         self.lib.oracle_embedding_q8_0_zero_fill(
             _ptr(W, _u8p), _ptr(ids, _i32p), _ptr(out, _f32p), ids.size, vocab, hidden)
+        return out
+
+    def dequantize_q8_0(self, W: np.ndarray, n: int) -> np.ndarray:
+        """The n elements of a raw Q8_0 block stream as fp32 (the weight loader's
+        dequantize_to_f32, gguf_weight_loader.cpp:446-463)."""
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        assert W.size >= (n + 31) // 32 * 34
+        out = np.empty(n, dtype=np.float32)
+        self.lib.oracle_dequantize_q8_0(_ptr(W, _u8p), _ptr(out, _f32p), n)
         return out
 
     def linear(self, A, W, bias, M, N, K):

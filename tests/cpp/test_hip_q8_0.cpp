@@ -1046,6 +1046,121 @@ static void test_tiled_copy_shape_guard() {
   std::printf("  tiled_copy_shape_guard ok\n");
 }
 
+static void test_loader_dequantizes_q8_0_on_device() {
+  // WeightLoader::load_weights into a Float32 HIP tensor bound to a Q8_0 GGUF
+  // tensor: the raw blocks go to the device and are dequantised there
+  // (hip::dequantize_q8_0); the bits equal the loader's host loop
+  // WeightLoader::dequantize_to_f32 (reference gguf_weight_loader.cpp:446-463),
+  // special binary16 scales included.
+  const int R = 96, C = 160;
+  auto q = synth_q8(R, C, 21);
+  const uint16_t special[] = {0x0001, 0x03ff, 0x0000, 0x8000, 0x7c00, 0xfc00, 0x7e00, 0x3c00};
+  for (int i = 0; i < 8; ++i) {
+    q[size_t(i) * 7 * 34] = uint8_t(special[i] & 0xff);
+    q[size_t(i) * 7 * 34 + 1] = uint8_t(special[i] >> 8);
+  }
+  GgufWriter w;
+  w.kv_str("general.architecture", "llama");
+  w.kv_u32("llama.embedding_length", C);
+  w.tensor("blk.0.ffn_up.weight", {R, C}, 8, q);
+  const std::string path = w.write("mle_dequant");
+  Graph g;
+  GraphBuilder gb(g);
+  const Device dev = Device::hip(0);
+  auto wv = gb.constant("layer_0.up_proj.weight", Shape({R, C}), DType::Float32, dev);
+  CHECK(wv);
+  WeightLoader loader(path);
+  auto file = loader.open();
+  CHECK(file);
+  Tensor t("layer_0.up_proj.weight", Shape({R, C}), DType::Float32, dev);
+  check_status(t.allocate_hip());
+  RuntimeContext ctx;
+  check_status(ctx.bind(*wv, &t));
+  check_status(loader.load_weights(*file, g, ctx));
+  const auto got = download(&t, size_t(R) * C);
+  std::vector<float> want(size_t(R) * C);
+  check_status(WeightLoader::dequantize_to_f32(GgmlDataType::Q8_0, q.data(), want.data(), want.size()));
+  for (size_t i = 0; i < want.size(); ++i) {
+    if (std::isnan(want[i])) {
+      CHECK(std::isnan(got[i]));
+      continue;
+    }
+    uint32_t a, b;
+    std::memcpy(&a, &got[i], 4);
+    std::memcpy(&b, &want[i], 4);
+    CHECK(a == b);
+  }
+  std::printf("  loader_dequantizes_q8_0_on_device ok\n");
+}
+
+static void test_executor_linear_bf16_bias() {
+  // Linear nodes with a BFloat16 bias (the reference CUDA adapter's accepted
+  // bias dtypes, cuda_kernel_adapter.cpp:204-218): the same bits as the bias
+  // widened to Float32, on raw and tiled weights; two sibling Linears with BF16
+  // biases run node by node (no fused launch) and still agree.
+  const int M = 5, N = 96, K = 256;
+  const Device dev = Device::hip(0);
+  const auto hw = random_q8(N, K, 41);
+  std::vector<uint16_t> b16(N);
+  std::vector<float> b32(N);
+  for (int i = 0; i < N; ++i) {
+    const float v = float(i % 13 - 6) * 0.37f + 0.01f * i;
+    uint32_t bits;
+    std::memcpy(&bits, &v, 4);
+    b16[i] = uint16_t(bits >> 16);
+    const uint32_t wide = uint32_t(b16[i]) << 16;
+    std::memcpy(&b32[i], &wide, 4);
+  }
+  std::vector<float> hx(size_t(M) * K);
+  for (size_t i = 0; i < hx.size(); ++i) hx[i] = float(int(i * 29 % 83) - 41) * 0.05f;
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  std::vector<float> outs[2][2];  // [bias dtype][tiled]
+  for (int bf = 0; bf < 2; ++bf) {
+    Graph g;
+    GraphBuilder gb(g);
+    auto x = gb.input("x", Shape({M, K}), DType::Float32, dev);
+    auto w = gb.constant("w", Shape({N, K}), DType::Float32, dev);
+    auto w2 = gb.constant("w2", Shape({N, K}), DType::Float32, dev);
+    auto b = gb.constant("b", Shape({N}), DType::Float32, dev);
+    CHECK(x && w && w2 && b);
+    auto y = gb.linear(*x, *w, *b, "lin");
+    auto y2 = gb.linear(*x, *w2, *b, "lin2");  // sibling on the same input
+    CHECK(y && y2 && gb.output(*y, "out") && gb.output(*y2, "out2"));
+    Tensor tx("x", Shape({M, K}), DType::Float32, dev), tw("w", Shape({N, K}), DType::Q8_0, dev);
+    Tensor tw2("w2", Shape({N, K}), DType::Q8_0, dev);
+    Tensor tb("b", Shape({N}), bf ? DType::BFloat16 : DType::Float32, dev);
+    check_status(tx.allocate_hip());
+    check_status(tw.allocate_hip_bytes(hw.size()));
+    check_status(tw2.allocate_hip_bytes(hw.size()));
+    check_status(tb.allocate_hip());
+    upload(tx, hx.data(), hx.size() * 4);
+    upload(tw, hw.data(), hw.size());
+    upload(tw2, hw.data(), hw.size());
+    if (bf) upload(tb, b16.data(), N * 2); else upload(tb, b32.data(), N * 4);
+    RuntimeContext ctx;
+    check_status(ctx.bind(*x, &tx));
+    check_status(ctx.bind(*w, &tw));
+    check_status(ctx.bind(*w2, &tw2));
+    check_status(ctx.bind(*b, &tb));
+    check_status(ctx.allocate_intermediates(g));
+    HipExecutor ex(std::make_shared<HipBackend>(), registry);
+    check_status(ex.compile(g));
+    CHECK(ex.fused_groups() == 1u);
+    for (int tiled = 0; tiled < 2; ++tiled) {
+      if (tiled) check_status(ex.tile_weights(ctx));
+      check_status(ex.run(ctx));
+      check_hip(hipDeviceSynchronize());
+      CHECK(ex.fused_launches() == (bf ? 0u : 1u));
+      outs[bf][tiled] = download(ctx.get(*y), size_t(M) * N);
+      CHECK(download(ctx.get(*y2), size_t(M) * N) == outs[bf][tiled]);
+    }
+  }
+  CHECK(outs[1][0] == outs[0][0]);
+  CHECK(outs[1][1] == outs[0][1]);
+  std::printf("  executor_linear_bf16_bias ok\n");
+}
+
 int main() {
   int count = 0;
   check_hip(hipGetDeviceCount(&count));
@@ -1065,6 +1180,8 @@ int main() {
   test_workspace_no_regrowth();
   test_executor_reserves_workspace();
   test_tiled_copy_shape_guard();
+  test_loader_dequantizes_q8_0_on_device();
+  test_executor_linear_bf16_bias();
   std::printf("test_hip_q8_0: all passed\n");
   return 0;
 }

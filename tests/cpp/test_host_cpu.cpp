@@ -153,6 +153,7 @@ struct LinearCase {
   Device w_device = Device::hip(0);
   bool with_bias = false;
   int64_t bias_len = 2;
+  DType bias_dtype = DType::Float32;
 };
 
 static Status run_linear_case(const LinearCase& c) {
@@ -166,11 +167,12 @@ static Status run_linear_case(const LinearCase& c) {
   CHECK(y);
   Tensor tx("x", Shape({c.M, c.K}), DType::Float32, Device::hip(0));
   Tensor tw("w", Shape({c.N, c.K}), c.w_dtype, c.w_device);
-  Tensor tb("b", Shape({c.bias_len}), DType::Float32, Device::hip(0));
+  Tensor tb("b", Shape({c.bias_len}), c.bias_dtype, Device::hip(0));
   Tensor ty("y", Shape({c.M, c.N}), DType::Float32, Device::hip(0));
   CHECK(tx.bind_hip_data(fake_ptr(), size_t(c.M) * c.K * 4).ok());
   CHECK(ty.bind_hip_data(fake_ptr(), size_t(c.M) * c.N * 4).ok());
-  CHECK(tb.bind_hip_data(fake_ptr(), size_t(c.bias_len) * 4).ok());
+  const size_t bias_elem = c.bias_dtype == DType::BFloat16 ? 2 : 4;
+  CHECK(tb.bind_hip_data(fake_ptr(), size_t(c.bias_len) * bias_elem).ok());
   const size_t wbytes = c.w_dtype == DType::Q8_0 ? q8_0_bytes(size_t(c.N) * c.K)
                                                  : size_t(c.N) * c.K * 4;
   if (c.w_device.type == DeviceType::HIP) {
@@ -213,6 +215,15 @@ static void test_linear_validation() {
   c.bias_len = 3;  // tensor bound with a shape that does not match N = 2
   st = run_linear_case(c);
   CHECK(contains(st.message(), "Linear bias shape must match output features"));
+
+  // Bias dtypes: Float32 or BFloat16 (reference cuda_kernel_adapter.cpp:48-59, 204-218).
+  c = LinearCase{};
+  c.K = 64;
+  c.with_bias = true;
+  c.bias_dtype = DType::Int32;
+  st = run_linear_case(c);
+  CHECK(st.code() == ErrorCode::RuntimeError);
+  CHECK(contains(st.message(), "bias supports Float32 or BFloat16, got Int32"));
   std::printf("  PASS test_linear_validation\n");
 }
 

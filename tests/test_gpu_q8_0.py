@@ -133,6 +133,39 @@ def test_embedding_empty_is_noop(dev):
     assert np.all(np.isnan(to_host(out)))
 
 
+@pytest.mark.parametrize("rows,cols,cut", [(151936, 896, 0), (4096, 4096, 0), (77, 96, 5),
+                                           (1, 32, 31), (3, 64, 0)])
+def test_dequantize_bitexact(dev, orc, rows, cols, cut):
+    """Loader Q8_0 -> fp32 on the device against the oracle's whole-stream dequantisation,
+    bit for bit; `cut` elements short of whole blocks exercises the partial last block."""
+    note(f"dequantize {rows}x{cols} - {cut}")
+    w, _, _ = S.q8_0_weight(140 + cols, rows, cols)
+    n = rows * cols - cut
+    out = empty_f32((n,), dev)
+    capi.dequantize(to_dev(w, dev), out, n)
+    assert_bitexact(to_host(out), orc.dequantize_q8_0(w, n), "dequantize")
+
+
+def test_dequantize_special_scales_and_errors(dev, orc):
+    import torch
+    special = np.array([0x0001, 0x03ff, 0x0000, 0x8000, 0x7c00, 0xfc00, 0x7e00, 0x3c00] * 4,
+                       dtype=np.uint16)
+    w, _, _ = S.q8_0_weight(150, 32, 32)
+    w = w.copy()
+    w.reshape(32, 34)[:, :2] = special.view(np.uint8).reshape(32, 2)
+    out = empty_f32((32 * 32,), dev)
+    capi.dequantize(to_dev(w, dev), out, 32 * 32)
+    assert_bitexact(to_host(out), orc.dequantize_q8_0(w, 32 * 32), "special scales")
+    capi.dequantize(to_dev(w, dev), out, 0)  # no-op
+    code, msg = capi.dequantize_status(None, out, 4)
+    assert code == 1 and "src pointer" in msg
+    code, msg = capi.dequantize_status(to_dev(w, dev), out[1:], 4)
+    assert code == 1 and "16-byte aligned" in msg
+    code, msg = capi.dequantize_status(to_dev(w, dev), out, -1)
+    assert code == 1 and "negative" in msg
+    torch.cuda.synchronize()
+
+
 # ----------------------------------------------------------------------------- linear GEMV
 
 def test_linear_known_answers_exact(dev, golden):
@@ -478,3 +511,42 @@ def test_device_error_paths(dev):
     with pytest.raises(capi.Q8_0Error) as e:
         capi.matmul(x, w, y, 1, 2, 64)
     assert e.value.code == 4
+
+
+# ----------------------------------------------------------------------------- BF16 bias
+
+@pytest.mark.parametrize("M,N,K,tiled", [(1, 384, 1024, False), (1, 384, 1024, True),
+                                         (3, 384, 1024, True), (5, 300, 256, False),
+                                         (8, 4096, 11008, True), (70, 257, 512, False),
+                                         (128, 256, 4096, True)])
+def test_linear_bf16_bias(dev, orc, M, N, K, tiled):
+    """A BFloat16 bias on a Q8_0 Linear (reference cuda_kernel_adapter.cpp:204-218:
+    sgemm_nt, then add_bias of the widened bf16 in fp32): bit-identical to the same
+    Linear with the widened fp32 bias on every path (GEMV, tiled GEMV, MFMA decode with
+    split K, MFMA GEMM; raw and tiled weights), and within the path's bar of the oracle."""
+    import torch
+    note(f"bf16 bias M={M} N={N} K={K} tiled={tiled}")
+    w, x = weight(160 + N, N, K), acts(161 + M, M, K)
+    b32 = S.activations(162, (N,), tag=S.TAG_BIAS)
+    b16 = (b32.view(np.uint32) >> 16).astype(np.uint16)        # bf16 bits (truncated)
+    widened = (b16.astype(np.uint32) << 16).view(np.float32)    # exact widening
+    dx, dw = to_dev(x, dev), to_dev(w, dev)
+    if tiled:
+        dwt = torch.empty(capi.tiled_bytes(N, K), dtype=torch.uint8, device=dev)
+        capi.tile(dw, dwt, N, K)
+        dw = dwt
+    y16, y32 = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    capi.linear_bias_bf16(dx, dw, to_dev(b16, dev), y16, M, N, K, tiled=tiled)
+    (capi.linear_tiled if tiled else capi.linear)(dx, dw, to_dev(widened, dev), y32, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(y16, y32)
+    err = rel_l2(to_host(y16), orc.linear(x, w, widened, M, N, K))
+    assert err <= (MFMA_TOL if M >= 64 else GEMV_TOL), err
+
+
+def test_linear_bf16_bias_errors(dev):
+    FAKE = 0x1000
+    code, msg = capi.linear_bias_bf16_status(FAKE, FAKE, FAKE + 1, FAKE, 1, 64, 64)
+    assert code == 1 and "bias must be 2-byte aligned" in msg
+    code, msg = capi.linear_bias_bf16_status(FAKE, FAKE, FAKE, FAKE, 1, 64, 48, tiled=True)
+    assert code == 4 and "multiple of 32" in msg

@@ -197,6 +197,31 @@ def test_embedding_closed_form(orc):
     assert np.array_equal(bits(out), bits(expect))
 
 
+def test_dequantize_closed_form_and_embedding(orc):
+    """Whole-stream dequantisation: the closed form fp32(d) * fp32(q) (numpy float16
+    decode, one rounding) bit for bit, including a partial last block and every class
+    of binary16 scale (subnormal, zero, inf, NaN by position); and the same bits as
+    the embedding gather of every row."""
+    vocab, hidden = 300, 64
+    w, q, d = S.q8_0_weight(38, vocab, hidden)
+    dq = (d.astype(np.float32).reshape(-1, 1) * q.reshape(-1, 32).astype(np.float32)).reshape(-1)
+    for n in (vocab * hidden, vocab * hidden - 5, 33, 1):
+        out = orc.dequantize_q8_0(w, n)
+        assert np.array_equal(bits(out), bits(dq[:n])), n
+    rows = orc.embedding(w, np.arange(vocab, dtype=np.int32), hidden)
+    assert np.array_equal(bits(orc.dequantize_q8_0(w, vocab * hidden)), bits(rows.reshape(-1)))
+    special = np.array([0x0001, 0x03ff, 0x0000, 0x8000, 0x7c00, 0xfc00, 0x7e00, 0x3c00],
+                       dtype=np.uint16)
+    ws = w[: 8 * 34].copy()
+    ws.reshape(8, 34)[:, :2] = special.view(np.uint8).reshape(8, 2)
+    got = orc.dequantize_q8_0(ws, 8 * 32)
+    want = (special.view(np.float16).astype(np.float32).reshape(-1, 1)
+            * ws.reshape(8, 34)[:, 2:].view(np.int8).astype(np.float32)).reshape(-1)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(bits(got[fin]), bits(want[fin]))
+
+
 def test_embedding_zero_fill_semantics(orc):
     vocab, hidden = 40, 64
     w, _, _ = S.q8_0_weight(37, vocab, hidden)
