@@ -9,8 +9,8 @@ M in {1, 4, 8}, the five Q8_0 Linears [4096->12288] QKV, [4096->4096] o_proj,
 [4096->11008] gate, [4096->11008] up and [11008->4096] down, each a separate launch
 (15 launches), FP32 activations ~N(0,1), synthetic Q8_0 weights (int8 uniform in
 [-127,127], fp16 scales |N(0,1)|*0.02/127), no bias.  Inputs are resident in HBM before
-timing.  Weights rotate over R copies of the set (R * 215 MB >= 1 GiB) so that no
-launch finds its weights in the 256 MB Infinity Cache.
+timing.  Every weight rotates over its own R_w = ceil(1 GiB / W) + 1 copies, so no launch
+(in the step or in the per-launch rows) finds its weight in the 256 MB Infinity Cache.
 
 Weights in Q8_0 16-row tiles: each weight is repacked once at load time
 (mle_q8_0_tile, outside the timed region) into the tiled layout of include/mle_q8_0.h --
@@ -21,20 +21,24 @@ bytes (mle_q8_0_linear) is timed too and reported as raw_value / per_launch_raw.
 value = algorithmic bytes of all launches / wall time of the timed steps (GB/s), with
 algorithmic bytes per launch = N*(K/32)*34 + 4*M*K + 4*M*N (either layout).
 
-Also reported: per-launch kernel durations (HIP events on the launch stream, >= 100
-launches each), the roofline of the dominant launch, the prefill GEMM of configs[2]
-(M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding gather of configs[4], the
-Qwen-shaped decode Linears and lm_head of configs[3] (per launch), the fused
-Linear entry points (gate/up + SwiGLU, q/k/v multi-output) against their unfused launches,
-the device argmax of an lm_head logits row against copying the row to the host, the
-device top-n tokens with softmax probabilities (sampling candidates), and the reference's
-own CPU kernels timed on this host (cpu_baseline).
+Also reported: per-launch kernel durations (HIP events on the launch stream, median of 3
+repetitions of >= 100 launches, with the spread), the roofline of the dominant launch,
+the prefill GEMM of configs[2] (M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding
+gather of configs[4], the Qwen-shaped decode Linears and lm_head of configs[3], the fused
+Linear entry points against their unfused launches, the device argmax and top-n tokens,
+a same-run parity gate (every timed shape against the reference CPU kernels on sampled
+output rows; the configs[4] embedding bit for bit in full), and the reference's own CPU
+kernels timed on this host (cpu_baseline, per config).  Python's garbage collector is
+off inside every timed region.
 """
 from __future__ import annotations
 
 import argparse
+import functools
+import gc
 import json
 import os
+import platform
 import sys
 import time
 
@@ -46,24 +50,40 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, 8 TB/s
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, 2.5 PFLOP/s
 ROTATE_BYTES = 1 << 30          # >= 4x the 256 MB Infinity Cache
+REPS = 3                        # repetitions of each per-launch / fused timing (median, spread)
 
 LLAMA_SET = [("qkv", 12288, 4096), ("o_proj", 4096, 4096), ("gate", 11008, 4096),
              ("up", 11008, 4096), ("down", 4096, 11008)]
 MS = (1, 4, 8)
 SEED_W = {"qkv": 21, "o_proj": 22, "gate": 23, "up": 24, "down": 25}
+QWEN_SET = (("qkv", 1152, 896, (1,)), ("gate", 4864, 896, (1,)), ("up", 4864, 896, (1,)),
+            ("down", 896, 4864, (1,)), ("lm_head", 151936, 896, (1, 8)))
+PREFILL = (("gate", 11008, 4096), ("down", 4096, 11008))
+GEMV_BAR, GEMM_BAR = 1e-5, 1e-2  # relative L2 parity bars (north_star)
+PARITY_ROWS = 64                 # output rows (n) sampled per shape for the parity gate
 
 # HBM bytes per dispatch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on
-# `bench.py --profile-kernel M,N,K` (FETCH_SIZE scaled by a device copy's read/write
-# ratio), keyed by (layout, M, N, K); see profiles/gemv_q8_0_mfma_tiled_m8_4096x11008_traffic.txt,
-# profiles/gemv_q8_0_mfma_tiled_m8_12288x4096_traffic.txt, profiles/gemv_tiled_m1_4096x11008_traffic.txt
-# and the raw-layout profiles/gemv_q8_0_mfma_m8_*_traffic.txt.
+# `bench.py --profile-kernel M,N,K[,tiled]` (FETCH_SIZE scaled by a device copy's
+# read/write ratio), keyed by (layout, M, N, K); the summaries are in profiles/.
 MEASURED_TRAFFIC = {("raw", 8, 4096, 11008): 57.236e6, ("raw", 8, 12288, 4096): 61.745e6,
                     ("tiled", 8, 4096, 11008): 56.736e6, ("tiled", 8, 12288, 4096): 61.374e6,
                     ("tiled", 1, 4096, 11008): 48.306e6}
 
 
+@functools.lru_cache(maxsize=None)
+def qweight(seed, rows, cols):
+    """Synthetic Q8_0 weight bytes (host), generated once per process."""
+    from llmengine_amd import synthetic as S
+    return S.q8_0_weight(seed, rows, cols)[0]
+
+
 def gemv_bytes(M, N, K):
     return N * (K // 32) * 34 + 4 * M * K + 4 * M * N
+
+
+def rotation(nbytes):
+    """Copies of one weight that together exceed ROTATE_BYTES (at least 2)."""
+    return max(2, -(-ROTATE_BYTES // nbytes) + 1)
 
 
 def tiled_gemv_wins(M, N, K):
@@ -95,16 +115,33 @@ def linear_fn(capi, layout):
     return capi.linear_tiled if layout == "tiled" else capi.linear
 
 
+def sample_rows(N, seed):
+    rng = np.random.default_rng(seed)
+    return np.sort(rng.choice(N, size=min(PARITY_ROWS, N), replace=False))
+
+
+def rows_of(w_raw, N, K, rows):
+    """Raw Q8_0 bytes of the given output rows of a [N, K] weight (rows are contiguous)."""
+    rb = (K // 32) * 34
+    return np.ascontiguousarray(w_raw.reshape(N, rb)[rows]).reshape(-1)
+
+
+def rel_l2(a, ref):
+    a, ref = np.asarray(a, np.float64), np.asarray(ref, np.float64)
+    den = np.linalg.norm(ref)
+    return float(np.linalg.norm(a - ref) / (den if den > 0 else 1.0))
+
+
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--launch-iters", type=int, default=120,
-                   help="launches per shape for the per-launch kernel timings")
+                   help="launches per shape and repetition for the per-launch timings")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true",
-                   help="skip the prefill and embedding figures")
+                   help="skip the prefill, embedding, configs[3], fused, argmax and top-n rows")
     p.add_argument("--profile-kernel", default=None, metavar="M,N,K[,tiled]",
                    help="counter-collection mode: run only the decode Linear of this shape "
                         "(raw weights, or tiled with a 4th field 'tiled') 200 times (rotating "
@@ -126,7 +163,7 @@ def profile_kernel(spec):
     w = torch.from_numpy(S.q8_0_weight(7, N, K)[0]).to(dev)
     if layout == "tiled":
         w = tiled_copy(capi, w, N, K, stream)
-    R = max(2, -(-ROTATE_BYTES // w.numel()) + 1)
+    R = rotation(w.numel())
     ws = [w] + [w.clone() for _ in range(R - 1)]
     x = torch.from_numpy(S.activations(8, (M, K))).to(dev)
     y = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -144,28 +181,125 @@ def profile_kernel(spec):
                                    "calibration_copy_bytes": src.numel() * 4}}), flush=True)
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(weights_host, xs_host):
-    """Time the reference's CPU kernels (oracle/_ref, else the C restatement) on the
-    M=1 and M=4 launches of one step (10 of the 15 launches, every row)."""
+    """The reference's CPU Q8_0 kernels (oracle/_ref, else the C restatement) on this
+    host, per config, on a bounded sample (about 20-30 s in all).  The reference
+    parallelises Linear/MatMul over M only (OpenMP), so an M-token launch uses
+    min(M, threads) threads and M = 1 one; Embedding is single-threaded."""
     import oracle
+    from llmengine_amd import synthetic as S
     if oracle.reference_available():
         lib, kind = oracle.reference(), "reference"
     else:
         lib, kind = oracle.oracle(), "port"
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+    def timed(fn, min_s, max_reps=1000, min_reps=3, warm=True):
+        if warm:
+            fn()
+        reps, t0 = 0, time.perf_counter()
+        while reps < min_reps or (time.perf_counter() - t0 < min_s and reps < max_reps):
+            fn()
+            reps += 1
+        return (time.perf_counter() - t0) / reps, reps
+
+    per = {}
+    # configs[1]: the decode step (all 15 launches, all rows), once or more
     total_bytes, reps, t0 = 0, 0, time.perf_counter()
-    while reps == 0 or time.perf_counter() - t0 < 10.0:  # a ~10 s bounded sample
-        for M in (1, 4):
+    while reps == 0 or time.perf_counter() - t0 < 6.0:
+        for M in MS:
             for name, N, K in LLAMA_SET:
                 lib.sgemm_nt(xs_host[(M, K)], weights_host[name], M, N, K)
                 total_bytes += gemv_bytes(M, N, K)
         reps += 1
     dt = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(total_bytes / dt / 1e9, 4), "unit": "GB/s",
-            "cores": min(4, threads), "kind": kind,
-            "sample": (f"M=1 and M=4 launches of one step (10 Q8_0 Linears, all rows), "
-                       f"{reps} times in {dt:.1f} s; the reference parallelises over M only, "
-                       f"so M=1 ran on 1 thread and M=4 on 4 (OMP_NUM_THREADS={threads})")}
+    step_gbs = total_bytes / dt / 1e9
+    per["configs[1] decode step"] = {"GBps": round(step_gbs, 4), "steps": reps,
+                                     "seconds": round(dt, 2),
+                                     "threads": {str(M): min(M, threads) for M in MS}}
+    # configs[0] / C1: 1 x 4096 x 4096
+    w1, _, _ = S.q8_0_weight(11, 4096, 4096)
+    x1 = S.activations(12, (1, 4096))
+    s, r = timed(lambda: lib.sgemm_nt(x1, w1, 1, 4096, 4096), 2.0)
+    per["configs[0] 1x4096x4096"] = {"GBps": round(gemv_bytes(1, 4096, 4096) / s / 1e9, 4),
+                                     "ms": round(s * 1e3, 2), "reps": r, "threads": 1}
+    # configs[2]: prefill 512 x [11008x4096] and [4096x11008] on a 32-row sample of M
+    # (OpenMP over rows: 32 rows keep up to 32 threads busy), one timed call each
+    for name, N, K in PREFILL:
+        xp = S.activations(2000 + K, (32, K))
+        s, r = timed(lambda: lib.sgemm_nt(xp, weights_host[name], 32, N, K), 0.0, 1, 1, False)
+        per[f"configs[2] prefill {N}x{K} (32 of 512 rows)"] = {
+            "GFLOPs": round(2.0 * 32 * N * K / s / 1e9, 3), "s": round(s, 3), "reps": r,
+            "threads": min(32, threads)}
+    # configs[3]: Qwen decode Linears at M = 1 and the lm_head at M = 1 and 8
+    for name, N, K, Ms in QWEN_SET:
+        wq = qweight(3000 + N, N, K)
+        for M in Ms:
+            xq = S.activations(3100 + K, (M, K))
+            big = N * K > 16 << 20  # the lm_head: one timed call after a warm-up
+            s, r = timed(lambda: lib.sgemm_nt(xq, wq, M, N, K), 0.0 if big else 0.5, 50,
+                         1 if big else 3)
+            per[f"configs[3] {name} M={M}"] = {"GBps": round(gemv_bytes(M, N, K) / s / 1e9, 4),
+                                               "ms": round(s * 1e3, 2), "reps": r,
+                                               "threads": min(M, threads)}
+    # configs[4]: embedding of 8 x 512 ids from a [151936, 896] table (single-threaded)
+    V, H, T = 151936, 896, 8 * 512
+    tbl = qweight(5, V, H)
+    ids = S.token_ids(5, T, V)
+    s, r = timed(lambda: lib.embedding(tbl, ids, H), 1.0, 100)
+    eb = T * (H // 32) * 34 + 4 * T + 4 * T * H
+    per["configs[4] embedding 4096 ids x 896"] = {"GBps": round(eb / s / 1e9, 4),
+                                                  "ms": round(s * 1e3, 3), "reps": r,
+                                                  "threads": 1}
+    return {"value": round(step_gbs, 4), "unit": "GB/s", "cores": min(max(MS), threads),
+            "kind": kind,
+            "sample": (f"configs[1] decode step (all 15 Q8_0 Linears, every row) {reps} "
+                       f"time(s) in {dt:.1f} s; the reference parallelises over M only, so "
+                       f"M=1/4/8 ran on {min(1, threads)}/{min(4, threads)}/"
+                       f"{min(8, threads)} threads (OMP_NUM_THREADS={threads}); other "
+                       f"configs in per_config (configs[2] on 32 of its 512 rows)"),
+            "nproc": os.cpu_count(), "omp_threads": threads, "cpu_model": cpu_model(),
+            "per_config": per}
+
+
+class Timer:
+    """HIP-event timing of back-to-back launches on one stream, GC off, REPS repetitions."""
+
+    def __init__(self, stream):
+        self.stream = stream
+
+    def __call__(self, fn, iters, warm=3):
+        import torch
+        for j in range(warm):
+            fn(j)
+        torch.cuda.synchronize()
+        us = []
+        gc.disable()
+        try:
+            for _ in range(REPS):
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(self.stream)
+                for j in range(iters):
+                    fn(j)
+                b.record(self.stream)
+                torch.cuda.synchronize()
+                us.append(a.elapsed_time(b) * 1e3 / iters)
+        finally:
+            gc.enable()
+        us.sort()
+        return us[len(us) // 2], us[0], us[-1]
 
 
 def main():
@@ -179,22 +313,32 @@ def main():
         sys.exit(2)
 
     import torch
+    import oracle
     from llmengine_amd import capi
     from llmengine_amd import synthetic as S
 
     dev = torch.device("cuda:0")
     capi.load()
     stream = torch.cuda.current_stream()
+    timer = Timer(stream)
+    orc = oracle.reference() if oracle.reference_available() else oracle.oracle()
+    parity = {"checker": "oracle/_ref (reference cpu_kernels.cpp)"
+              if oracle.reference_available() else "oracle (C restatement)",
+              "rows_sampled_per_shape": PARITY_ROWS, "checks": []}
 
-    # ---- inputs, resident in HBM before timing
-    set_bytes = sum(S.weight_bytes(N, K) for _, N, K in LLAMA_SET)
-    R = max(2, -(-ROTATE_BYTES // set_bytes) + 1)
-    weights_host, wdev, tdev = {}, {}, {}
+    def gate(what, got, want, bar):
+        err = rel_l2(got, want)
+        parity["checks"].append({"what": what, "rel_l2": float(f"{err:.3g}"), "bar": bar,
+                                 "ok": bool(err <= bar)})
+
+    # ---- inputs, resident in HBM before timing; every weight rotates over >= 1 GiB
+    weights_host, wdev, tdev, rot = {}, {}, {}, {}
     for name, N, K in LLAMA_SET:
         w, _, _ = S.q8_0_weight(SEED_W[name], N, K)
         weights_host[name] = w
         base = torch.from_numpy(w).to(dev)
-        wdev[name] = [base] + [base.clone() for _ in range(R - 1)]
+        rot[name] = rotation(base.numel())
+        wdev[name] = [base] + [base.clone() for _ in range(rot[name] - 1)]
         tdev[name] = [tiled_copy(capi, c, N, K, stream) for c in wdev[name]]
     wsets = {"tiled": tdev, "raw": wdev}
     # one-time cost of the repack (a loader step; outside every timed region below)
@@ -220,17 +364,20 @@ def main():
     def step(i, layout):
         lin, ws = linear_fn(capi, layout), wsets[layout]
         for mi, M in enumerate(MS):
-            c = (i * len(MS) + mi) % R
+            c = i * len(MS) + mi
             for name, N, K in LLAMA_SET:
-                lin(xdev[(M, K)], ws[name][c], None, ydev[(M, name)], M, N, K, stream=stream)
+                lin(xdev[(M, K)], ws[name][c % rot[name]], None, ydev[(M, name)], M, N, K,
+                    stream=stream)
 
-    # ---- timed steps (tiled weights: the headline value; raw GGUF bytes beside it)
+    # ---- timed steps (tiled weights: the headline value; raw GGUF bytes beside it),
+    # then the parity gate on the outputs of the last step of each layout
     timing = {}
     for layout in ("tiled", "raw"):
         for i in range(args.warmup):
             step(i, layout)
         torch.cuda.synchronize()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gc.disable()
         t0 = time.perf_counter()
         ev0.record(stream)
         for i in range(args.steps):
@@ -238,9 +385,17 @@ def main():
         ev1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        gc.enable()
         gpu_ms = ev0.elapsed_time(ev1)
         elapsed_l = max(wall, gpu_ms / 1e3)
         timing[layout] = (elapsed_l, step_bytes * args.steps / elapsed_l / 1e9)
+        for M in MS:
+            for name, N, K in LLAMA_SET:
+                rows = sample_rows(N, 100 * M + SEED_W[name])
+                want = orc.sgemm_nt(xs_host[(M, K)], rows_of(weights_host[name], N, K, rows),
+                                    M, len(rows), K)
+                got = ydev[(M, name)].cpu().numpy()[:, rows]
+                gate(f"decode {layout} M={M} {name} [{N}x{K}]", got, want, GEMV_BAR)
     elapsed, value = timing["tiled"]
     raw_elapsed, raw_value = timing["raw"]
 
@@ -250,21 +405,16 @@ def main():
         rows = []
         for M in MS:
             for name, N, K in LLAMA_SET:
-                for j in range(3):  # warm
-                    lin(xdev[(M, K)], ws[name][j % R], None, ydev[(M, name)], M, N, K,
-                        stream=stream)
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record(stream)
-                for j in range(args.launch_iters):
-                    lin(xdev[(M, K)], ws[name][j % R], None, ydev[(M, name)], M, N, K,
-                        stream=stream)
-                b.record(stream)
-                torch.cuda.synchronize()
-                us = a.elapsed_time(b) * 1e3 / args.launch_iters
+                R = rot[name]
+                med, lo, hi = timer(lambda j: lin(xdev[(M, K)], ws[name][j % R], None,
+                                                  ydev[(M, name)], M, N, K, stream=stream),
+                                    args.launch_iters)
                 nbytes = gemv_bytes(M, N, K)
-                rows.append({"M": M, "op": name, "N": N, "K": K, "us": round(us, 3),
-                             "GBps": round(nbytes / us / 1e3, 1),
-                             "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+                rows.append({"M": M, "op": name, "N": N, "K": K, "us": round(med, 3),
+                             "us_min": round(lo, 3), "us_max": round(hi, 3),
+                             "GBps": round(nbytes / med / 1e3, 1),
+                             "frac_hbm": round(nbytes / med / 1e3 / HBM_PEAK_GBS, 4),
+                             "rotated_copies": R})
         return rows
 
     per_launch = launches("tiled")
@@ -280,106 +430,94 @@ def main():
                 "kernel": f"{decode_kernel_name(dom['M'], 'tiled', dom['N'], dom['K'])} "
                           f"M={dom['M']} {dom['op']} "
                           f"[{dom['N']}x{dom['K']}]",
-                "bytes_per_launch": dom_bytes, "us_per_launch": dom["us"]}
+                "bytes_per_launch": dom_bytes, "us_per_launch": dom["us"],
+                "us_spread": [dom["us_min"], dom["us_max"]],
+                "rotated_copies": dom["rotated_copies"]}
 
     extras = {}
     if not args.no_extras:
         # ---- prefill GEMM, configs[2]: M=512 on the bf16 MFMA path
         pre = []
-        for layout in ("tiled", "raw"):
-            lin, ws = linear_fn(capi, layout), wsets[layout]
-            for name, N, K in (("gate", 11008, 4096), ("down", 4096, 11008)):
-                M = 512
-                x = torch.from_numpy(S.activations(2000 + K, (M, K))).to(dev)
+        for name, N, K in PREFILL:
+            M = 512
+            xh = S.activations(2000 + K, (M, K))
+            x = torch.from_numpy(xh).to(dev)
+            rows = sample_rows(N, 7 + N)
+            want = orc.sgemm_nt(xh, rows_of(weights_host[name], N, K, rows), M, len(rows), K)
+            for layout in ("tiled", "raw"):
+                lin, ws, R = linear_fn(capi, layout), wsets[layout], rot[name]
                 y = torch.empty((M, N), dtype=torch.float32, device=dev)
-                for j in range(3):
-                    lin(x, ws[name][j % R], None, y, M, N, K, stream=stream)
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                iters = 40
-                a.record(stream)
-                for j in range(iters):
-                    lin(x, ws[name][j % R], None, y, M, N, K, stream=stream)
-                b.record(stream)
-                torch.cuda.synchronize()
-                us = a.elapsed_time(b) * 1e3 / iters
-                tflops = 2.0 * M * N * K / us / 1e6
-                pre.append({"M": M, "N": N, "K": K, "layout": layout, "us": round(us, 2),
+                med, lo, hi = timer(lambda j: lin(x, ws[name][j % R], None, y, M, N, K,
+                                                  stream=stream), 40)
+                gate(f"prefill {layout} M=512 [{N}x{K}]", y.cpu().numpy()[:, rows], want,
+                     GEMM_BAR)
+                tflops = 2.0 * M * N * K / med / 1e6
+                pre.append({"M": M, "N": N, "K": K, "layout": layout, "us": round(med, 2),
+                            "us_min": round(lo, 2), "us_max": round(hi, 2),
                             "TFLOPs": round(tflops, 1),
                             "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                             "note": "per call: X->bf16 fragment pre-pass + GEMM kernel"})
         extras["prefill"] = pre
-        # ---- embedding gather, configs[4]
+        # ---- embedding gather, configs[4] (parity: the whole output, bit for bit)
         V, H, T = 151936, 896, 8 * 512
-        tbl = torch.from_numpy(S.q8_0_weight(5, V, H)[0]).to(dev)
-        Re = max(2, -(-ROTATE_BYTES // tbl.numel()) + 1)
+        tbl_h = qweight(5, V, H)
+        tbl = torch.from_numpy(tbl_h).to(dev)
+        Re = rotation(tbl.numel())
         tbls = [tbl] + [tbl.clone() for _ in range(Re - 1)]
-        ids = torch.from_numpy(S.token_ids(5, T, V)).to(dev)
+        ids_h = S.token_ids(5, T, V)
+        ids = torch.from_numpy(ids_h).to(dev)
         out = torch.empty((T, H), dtype=torch.float32, device=dev)
-        for j in range(3):
-            capi.embedding(tbls[j % Re], ids, out, T, V, H, stream=stream)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        iters = 100
-        a.record(stream)
-        for j in range(iters):
-            capi.embedding(tbls[j % Re], ids, out, T, V, H, stream=stream)
-        b.record(stream)
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / iters
+        med, lo, hi = timer(lambda j: capi.embedding(tbls[j % Re], ids, out, T, V, H,
+                                                     stream=stream), 100)
+        got, want = out.cpu().numpy(), orc.embedding(tbl_h, ids_h, H)
+        same = bool(np.array_equal(np.isnan(got), np.isnan(want)) and np.array_equal(
+            got[~np.isnan(want)].view(np.uint32), want[~np.isnan(want)].view(np.uint32)))
+        parity["checks"].append({"what": "embedding configs[4] full output", "bitexact": same,
+                                 "ok": same})
         eb = T * (H // 32) * 34 + 4 * T + 4 * T * H
-        extras["embedding"] = {"T": T, "vocab": V, "hidden": H, "us": round(us, 2),
-                               "GBps": round(eb / us / 1e3, 1),
-                               "frac_hbm": round(eb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        extras["embedding"] = {"T": T, "vocab": V, "hidden": H, "us": round(med, 2),
+                               "us_min": round(lo, 2), "us_max": round(hi, 2),
+                               "GBps": round(eb / med / 1e3, 1),
+                               "frac_hbm": round(eb / med / 1e3 / HBM_PEAK_GBS, 4),
+                               "rotated_copies": Re}
         del tbls
         # ---- Qwen2.5-0.5B-shaped decode Linears at M = 1 and the tied
-        # lm_head at M = 1 and 8 (weights rotated over >= 1 GiB; small ones are
-        # latency-bound, so wall-clock per launch is the figure)
+        # lm_head at M = 1 and 8 (small ones are latency-bound: wall-clock per launch)
         qwen = []
-        for name, N, K, Ms in (("qkv", 1152, 896, (1,)), ("gate", 4864, 896, (1,)),
-                               ("up", 4864, 896, (1,)), ("down", 896, 4864, (1,)),
-                               ("lm_head", 151936, 896, (1, 8))):
-            wq = torch.from_numpy(S.q8_0_weight(3000 + N, N, K)[0]).to(dev)
-            Rq = max(2, -(-ROTATE_BYTES // wq.numel()) + 1)
+        for name, N, K, Ms in QWEN_SET:
+            wq_h = qweight(3000 + N, N, K)
+            wq = torch.from_numpy(wq_h).to(dev)
+            Rq = rotation(wq.numel())
             wqs = {"raw": [wq] + [wq.clone() for _ in range(Rq - 1)]}
             wqs["tiled"] = [tiled_copy(capi, c, N, K, stream) for c in wqs["raw"]]
+            rows = sample_rows(N, 11 + N)
             for M in Ms:
-                x = torch.from_numpy(S.activations(3100 + K, (M, K))).to(dev)
+                xh = S.activations(3100 + K, (M, K))
+                x = torch.from_numpy(xh).to(dev)
                 y = torch.empty((M, N), dtype=torch.float32, device=dev)
-                row = {"op": name, "M": M, "N": N, "K": K}
+                want = orc.sgemm_nt(xh, rows_of(wq_h, N, K, rows), M, len(rows), K)
+                row = {"op": name, "M": M, "N": N, "K": K, "rotated_copies": Rq}
                 for layout in ("tiled", "raw"):
                     lin = linear_fn(capi, layout)
                     for j in range(Rq):  # touch every copy once (first-use page mapping)
                         lin(x, wqs[layout][j], None, y, M, N, K, stream=stream)
-                    a, b = (torch.cuda.Event(enable_timing=True),
-                            torch.cuda.Event(enable_timing=True))
-                    iters = 100
-                    a.record(stream)
-                    for j in range(iters):
-                        lin(x, wqs[layout][j % Rq], None, y, M, N, K, stream=stream)
-                    b.record(stream)
-                    torch.cuda.synchronize()
-                    us = a.elapsed_time(b) * 1e3 / iters
-                    gb = gemv_bytes(M, N, K) / us / 1e3
+                    med, lo, hi = timer(lambda j: lin(x, wqs[layout][j % Rq], None, y, M, N,
+                                                      K, stream=stream), 100)
+                    gate(f"configs[3] {layout} M={M} {name} [{N}x{K}]",
+                         y.cpu().numpy()[:, rows], want, GEMV_BAR)
+                    gb = gemv_bytes(M, N, K) / med / 1e3
                     sfx = "" if layout == "tiled" else "_raw"
-                    row.update({"us" + sfx: round(us, 2), "GBps" + sfx: round(gb, 1),
-                                "frac_hbm" + sfx: round(gb / HBM_PEAK_GBS, 4)})
+                    row.update({"us" + sfx: round(med, 2), "GBps" + sfx: round(gb, 1),
+                                "frac_hbm" + sfx: round(gb / HBM_PEAK_GBS, 4),
+                                "us_spread" + sfx: [round(lo, 2), round(hi, 2)]})
                 qwen.append(row)
             del wqs
         extras["qwen_lm_head"] = qwen
 
-        def timed(fn, iters):
-            for j in range(3):
-                fn(j)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for j in range(iters):
-                fn(j)
-            b.record(stream)
-            torch.cuda.synchronize()
-            return a.elapsed_time(b) * 1e3 / iters
-
         # ---- fused FFN front (gate/up + SwiGLU) and q/k/v multi-output, per call
         fused = []
-        gw, uw = wdev["gate"], wdev["up"]
+        gw, uw, tgw, tuw = wdev["gate"], wdev["up"], tdev["gate"], tdev["up"]
+        R = min(rot["gate"], rot["up"])
         N, K = 11008, 4096
         for M in (1, 4, 8, 512):
             x = xdev[(M, K)] if (M, K) in xdev else torch.from_numpy(
@@ -387,40 +525,44 @@ def main():
             y = torch.empty((M, N), dtype=torch.float32, device=dev)
             g2 = torch.empty_like(y)
             iters = 40 if M >= 64 else 100
-            tf = timed(lambda j: capi.linear_swiglu(x, gw[j % R], uw[j % R], y, M, N, K,
+            tf = timer(lambda j: capi.linear_swiglu(x, gw[j % R], uw[j % R], y, M, N, K,
                                                     stream=stream), iters)
-            tgw, tuw = tdev["gate"], tdev["up"]
-            tft = timed(lambda j: capi.linear_swiglu_tiled(x, tgw[j % R], tuw[j % R], y, M, N,
+            tft = timer(lambda j: capi.linear_swiglu_tiled(x, tgw[j % R], tuw[j % R], y, M, N,
                                                            K, stream=stream), iters)
-            ts = timed(lambda j: (capi.linear(x, gw[j % R], None, y, M, N, K, stream=stream),
+            ts = timer(lambda j: (capi.linear(x, gw[j % R], None, y, M, N, K, stream=stream),
                                   capi.linear(x, uw[j % R], None, g2, M, N, K,
                                               stream=stream)), iters)
             nb = 2 * gemv_bytes(M, N, K) - 4 * M * K - 4 * M * N
             fused.append({"op": "gate+up -> SwiGLU [2 x 11008x4096]", "M": M,
-                          "us_fused": round(tf, 2), "us_two_linears": round(ts, 2),
-                          "GBps_fused": round(nb / tf / 1e3, 1),
-                          "us_fused_tiled": round(tft, 2),
-                          "GBps_fused_tiled": round(nb / tft / 1e3, 1)})
+                          "us_fused": round(tf[0], 2), "us_fused_spread": [round(v, 2) for v in tf[1:]],
+                          "us_two_linears": round(ts[0], 2),
+                          "GBps_fused": round(nb / tf[0] / 1e3, 1),
+                          "us_fused_tiled": round(tft[0], 2),
+                          "us_fused_tiled_spread": [round(v, 2) for v in tft[1:]],
+                          "GBps_fused_tiled": round(nb / tft[0] / 1e3, 1)})
         qkv = [torch.from_numpy(S.q8_0_weight(40 + i, 4096, 4096)[0]).to(dev) for i in range(3)]
-        Rq = max(2, -(-ROTATE_BYTES // (3 * qkv[0].numel())) + 1)  # past the Infinity Cache
+        Rq = rotation(3 * qkv[0].numel())
         qkv_r = [qkv] + [[w.clone() for w in qkv] for _ in range(Rq - 1)]
         qkv_t = [[tiled_copy(capi, w, 4096, 4096, stream) for w in ws3] for ws3 in qkv_r]
         for M in (1, 4, 8):
             x = xdev[(M, 4096)]
             ys = [torch.empty((M, 4096), dtype=torch.float32, device=dev) for _ in range(3)]
-            tf = timed(lambda j: capi.linear_multi(x, qkv_r[j % Rq], None, ys, (4096,) * 3, M,
+            tf = timer(lambda j: capi.linear_multi(x, qkv_r[j % Rq], None, ys, (4096,) * 3, M,
                                                    4096, stream=stream), 100)
-            ts = timed(lambda j: [capi.linear(x, qkv_r[j % Rq][i], None, ys[i], M, 4096, 4096,
+            ts = timer(lambda j: [capi.linear(x, qkv_r[j % Rq][i], None, ys[i], M, 4096, 4096,
                                               stream=stream) for i in range(3)], 100)
-            tft = timed(lambda j: capi.linear_multi_tiled(x, qkv_t[j % Rq], None, ys,
+            tft = timer(lambda j: capi.linear_multi_tiled(x, qkv_t[j % Rq], None, ys,
                                                           (4096,) * 3, M, 4096, stream=stream),
                         100)
             nb = 3 * gemv_bytes(M, 4096, 4096) - 2 * 4 * M * 4096
             fused.append({"op": "q,k,v multi-output [3 x 4096x4096]", "M": M,
-                          "us_fused": round(tf, 2), "us_three_linears": round(ts, 2),
-                          "GBps_fused": round(nb / tf / 1e3, 1),
-                          "us_fused_tiled": round(tft, 2),
-                          "GBps_fused_tiled": round(nb / tft / 1e3, 1)})
+                          "us_fused": round(tf[0], 2),
+                          "us_fused_spread": [round(v, 2) for v in tf[1:]],
+                          "us_three_linears": round(ts[0], 2),
+                          "GBps_fused": round(nb / tf[0] / 1e3, 1),
+                          "us_fused_tiled": round(tft[0], 2),
+                          "us_fused_tiled_spread": [round(v, 2) for v in tft[1:]],
+                          "GBps_fused_tiled": round(nb / tft[0] / 1e3, 1)})
         extras["fused"] = fused
         del qkv, qkv_r, qkv_t
 
@@ -428,7 +570,7 @@ def main():
         V = 151936
         logits = torch.from_numpy(S.activations(7, (1, V))).to(dev)
         idx = torch.empty(1, dtype=torch.int32, device=dev)
-        t_arg = timed(lambda j: capi.argmax(logits, 1, V, idx, stream=stream), 200)
+        t_arg = timer(lambda j: capi.argmax(logits, 1, V, idx, stream=stream), 200)[0]
         host = torch.empty((1, V), dtype=torch.float32).pin_memory()
         for _ in range(3):
             host.copy_(logits)
@@ -442,17 +584,19 @@ def main():
                                     "and picks there; the device argmax returns 4 bytes"}
         # ---- sampling candidates: device top-n tokens with softmax probabilities
         tk = []
-        for rows, top_n in ((1, 40), (8, 40), (1, 128)):
-            lg = torch.from_numpy(S.activations(8, (rows, V))).to(dev)
-            tid = torch.empty((rows, top_n), dtype=torch.int32, device=dev)
-            tpr = torch.empty((rows, top_n), dtype=torch.float32, device=dev)
-            t_top = timed(lambda j: capi.top_tokens(lg, rows, V, top_n, tid, tpr, 0.8,
-                                                    stream=stream), 200)
-            tk.append({"rows": rows, "top_n": top_n, "us_device": round(t_top, 2)})
+        for rows_n, top_n in ((1, 40), (8, 40), (1, 128)):
+            lg = torch.from_numpy(S.activations(8, (rows_n, V))).to(dev)
+            tid = torch.empty((rows_n, top_n), dtype=torch.int32, device=dev)
+            tpr = torch.empty((rows_n, top_n), dtype=torch.float32, device=dev)
+            t_top = timer(lambda j: capi.top_tokens(lg, rows_n, V, top_n, tid, tpr, 0.8,
+                                                    stream=stream), 200)[0]
+            tk.append({"rows": rows_n, "top_n": top_n, "us_device": round(t_top, 2)})
         extras["top_tokens"] = {"vocab": V, "temperature": 0.8, "runs": tk,
                                 "note": "Sampler::get_top_tokens on the device (softmax + "
                                         "top-n); the reference sorts the copied row on the host"}
 
+    parity["all_ok"] = all(c["ok"] for c in parity["checks"])
+    parity["checked"] = len(parity["checks"])
     cpu = None if args.no_cpu_baseline else cpu_baseline(weights_host, xs_host)
 
     line = {
@@ -467,10 +611,11 @@ def main():
                    "weights": "Q8_0 16-row tiles (repacked once at load, 34 B per block as "
                               "raw); raw GGUF layout in raw_value / per_launch_raw",
                    "tile_once_us": round(tile_once_us, 1),
-                   "rotated_weight_copies": R, "bytes_per_step": step_bytes,
+                   "rotated_weight_copies": rot, "bytes_per_step": step_bytes,
                    "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "parity": parity,
         "raw_value": round(raw_value, 1),
         "raw_ms_per_step": round(raw_elapsed * 1e3 / args.steps, 4),
         "per_launch": per_launch,
