@@ -23,7 +23,8 @@ algorithmic bytes per launch = N*(K/32)*34 + 4*M*K + 4*M*N (either layout).
 
 Also reported: per-launch kernel durations (HIP events on the launch stream, median of 3
 repetitions of >= 100 launches, with the spread), the roofline of the dominant launch,
-the prefill GEMM of configs[2] (M=512, TFLOP/s vs bf16 dense MFMA peak), the embedding
+the prefill GEMM of configs[2] (M=512, TFLOP/s vs bf16 dense MFMA peak, beside the
+vendor's bf16 GEMM of the same shape on bf16 operands as a yardstick), the embedding
 gather of configs[4], the Qwen-shaped decode Linears and lm_head of configs[3], the fused
 Linear entry points against their unfused launches, the device argmax and top-n tokens,
 a same-run parity gate (every timed shape against the reference CPU kernels on sampled
@@ -65,9 +66,10 @@ PARITY_ROWS = 64                 # output rows (n) sampled per shape for the par
 # HBM bytes per dispatch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on
 # `bench.py --profile-kernel M,N,K[,tiled]` (FETCH_SIZE scaled by a device copy's
 # read/write ratio), keyed by (layout, M, N, K); the summaries are in profiles/.
-MEASURED_TRAFFIC = {("raw", 8, 4096, 11008): 57.236e6, ("raw", 8, 12288, 4096): 61.745e6,
-                    ("tiled", 8, 4096, 11008): 56.736e6, ("tiled", 8, 12288, 4096): 61.374e6,
-                    ("tiled", 1, 4096, 11008): 48.306e6}
+MEASURED_TRAFFIC = {("raw", 8, 4096, 11008): 57.242e6, ("raw", 8, 12288, 4096): 61.358e6,
+                    ("tiled", 8, 4096, 11008): 56.746e6, ("tiled", 8, 12288, 4096): 61.403e6,
+                    ("tiled", 1, 4096, 11008): 48.306e6,
+                    ("raw", 512, 11008, 4096): 152.297e6, ("tiled", 512, 11008, 4096): 152.287e6}
 
 
 @functools.lru_cache(maxsize=None)
@@ -452,11 +454,36 @@ def main():
                 gate(f"prefill {layout} M=512 [{N}x{K}]", y.cpu().numpy()[:, rows], want,
                      GEMM_BAR)
                 tflops = 2.0 * M * N * K / med / 1e6
+                traffic = MEASURED_TRAFFIC.get((layout, M, N, K))
                 pre.append({"M": M, "N": N, "K": K, "layout": layout, "us": round(med, 2),
                             "us_min": round(lo, 2), "us_max": round(hi, 2),
                             "TFLOPs": round(tflops, 1),
                             "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                            "gemm_kernel_hbm_bytes": int(traffic) if traffic else None,
                             "note": "per call: X->bf16 fragment pre-pass + GEMM kernel"})
+            # Yardstick on the same GPU (not the product path): the vendor's bf16
+            # GEMM (hipBLASLt through torch.mm) of the same shape on operands that
+            # are already bf16 -- no Q8_0 decode, no fp32 -> bf16 pass over X --
+            # with an fp32 output, over the same >= 1 GiB rotation of W copies.
+            wb_bytes = N * K * 2
+            Rb = rotation(wb_bytes)
+            wbs = [torch.randn((N, K), dtype=torch.bfloat16, device=dev) for _ in range(Rb)]
+            xb = x.to(torch.bfloat16)
+            try:
+                med, lo, hi = timer(lambda j: torch.mm(xb, wbs[j % Rb].t(),
+                                                       out_dtype=torch.float32), 40)
+                vendor_out = "fp32"
+            except (TypeError, RuntimeError):
+                med, lo, hi = timer(lambda j: torch.mm(xb, wbs[j % Rb].t()), 40)
+                vendor_out = "bf16"
+            tflops = 2.0 * M * N * K / med / 1e6
+            pre.append({"M": M, "N": N, "K": K, "layout": "vendor bf16 GEMM (torch.mm)",
+                        "us": round(med, 2), "us_min": round(lo, 2), "us_max": round(hi, 2),
+                        "TFLOPs": round(tflops, 1),
+                        "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "note": f"hipBLASLt bf16 x bf16 -> {vendor_out}, operands already "
+                                f"bf16 (no Q8_0 decode); {Rb} rotated W copies"})
+            del wbs, xb
         extras["prefill"] = pre
         # ---- embedding gather, configs[4] (parity: the whole output, bit for bit)
         V, H, T = 151936, 896, 8 * 512

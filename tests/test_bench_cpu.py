@@ -30,8 +30,10 @@ def test_algorithmic_bytes_per_launch():
 def test_measured_traffic_table():
     for (layout, M, N, K), nbytes in bench.MEASURED_TRAFFIC.items():
         assert layout in ("raw", "tiled")
-        # measured HBM bytes are at least the algorithmic bytes, and not wildly above
-        assert 1.0 <= nbytes / bench.gemv_bytes(M, N, K) < 1.5, (layout, M, N, K)
+        # measured HBM bytes are at least the algorithmic bytes, and not wildly above;
+        # the prefill GEMM reads W once per 256-row M tile (two tiles at M = 512)
+        hi = 1.5 if M < 64 else 2.5
+        assert 1.0 <= nbytes / bench.gemv_bytes(M, N, K) < hi, (layout, M, N, K)
 
 
 def test_kernel_names_follow_the_path_choice():
