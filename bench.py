@@ -650,6 +650,10 @@ def main():
     }
     line.update(extras)
     print(json.dumps(line), flush=True)
+    if not parity["all_ok"]:
+        bad = [c["what"] for c in parity["checks"] if not c["ok"]]
+        print(f"bench.py: parity gate failed for {bad}", file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":
