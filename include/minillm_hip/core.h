@@ -139,6 +139,12 @@ class Shape {
 // ---------------------------------------------------------------- Tensor
 // Physical data container bound to a graph ValueId.  Owns host storage, HIP
 // device storage, or views external storage.  Move-only.
+// Byte order of a tensor's storage.  Raw: the dtype's own layout (GGUF blocks for
+// Q8_0).  Q8_0Tiled: the Q8_0 16-row tiles of mle_q8_0_tile, which a HipExecutor
+// puts in place of a Linear-only weight's raw bytes when asked to
+// (HipExecutor::tile_weights with release_raw; no counterpart in the reference).
+enum class StorageLayout { Raw = 0, Q8_0Tiled = 1 };
+
 class Tensor {
  public:
   Tensor() = default;
@@ -172,6 +178,16 @@ class Tensor {
   Status bind_hip_data(void* data, size_t bytes);
   Status release();
 
+  StorageLayout storage_layout() const { return layout_; }
+  // Whether the device storage was allocated by this tensor (allocate_hip*), as
+  // opposed to bound (bind_hip_data) or absent.
+  bool owns_hip_storage() const { return hip_ != nullptr; }
+  // Replaces owned device storage by `data` (hipMalloc'd, `bytes` long, now owned
+  // by the tensor and freed by release()) holding the same values in `layout`.
+  // The old storage is freed with hipFree, so no launch may still read it.
+  // InvalidArgument unless the tensor owns HIP storage and `data` is not null.
+  Status adopt_hip_bytes(void* data, size_t bytes, StorageLayout layout);
+
  private:
   std::string name_;
   Shape shape_;
@@ -182,6 +198,7 @@ class Tensor {
   size_t external_bytes_{0};
   void* hip_{nullptr};
   size_t hip_bytes_{0};
+  StorageLayout layout_{StorageLayout::Raw};
 };
 
 }  // namespace minillm

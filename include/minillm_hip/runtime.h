@@ -158,10 +158,22 @@ class HipExecutor final : public Executor {
   // live until release_tiled_weights() or the executor's destruction; call
   // again after overwriting a bound weight in place.  Memory: one more copy of
   // each Linear weight (the raw buffer stays with the caller).
-  Status tile_weights(RuntimeContext& ctx);
+  //
+  // release_raw: a weight whose tensor owns its device storage
+  // (allocate_hip*) and whose buffer the graph reads only as Linear weights
+  // (not as an Embedding table, e.g. a tied lm_head, nor a MatMul operand) is
+  // re-tiled in place instead: the tensor adopts the tiled buffer
+  // (StorageLayout::Q8_0Tiled) and its raw bytes are freed after a synchronise
+  // of this stream, so the weight costs no extra memory.  Such a tensor stays
+  // tiled for good: any executor's Linear kernel runs it on the tiled entry
+  // points, Embedding and MatMul reject it, and it must not be refilled with
+  // raw bytes (reallocate it first).  Other weights get copies as above.
+  Status tile_weights(RuntimeContext& ctx, bool release_raw = false);
   void release_tiled_weights();
   size_t tiled_weights() const { return tiled_.size(); }
-  // Linear launches of the last run that read a tiled copy.
+  // Weights the last tile_weights re-tiled in place.
+  size_t tiled_in_place() const { return in_place_; }
+  // Linear launches of the last run on 16-row tiles (a copy or in place).
   size_t tiled_launches() const { return tiled_launches_; }
   ~HipExecutor() override;
 
@@ -183,6 +195,7 @@ class HipExecutor final : public Executor {
   hipStream_t stream_;
   detail::TiledWeights tiled_;  // raw buffer -> tiled copy
   std::vector<void*> tiled_bufs_;
+  size_t in_place_{0};
   size_t ws_bytes_{0}, ws_counters_{0};
   bool ws_pending_{false};  // a reservation compile() could not make (no HIP device)
 };

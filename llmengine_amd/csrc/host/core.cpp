@@ -161,11 +161,13 @@ Tensor::~Tensor() { (void)release(); }
 Tensor::Tensor(Tensor&& o) noexcept
     : name_(std::move(o.name_)), shape_(std::move(o.shape_)), dtype_(o.dtype_),
       device_(o.device_), host_(std::move(o.host_)), external_(o.external_),
-      external_bytes_(o.external_bytes_), hip_(o.hip_), hip_bytes_(o.hip_bytes_) {
+      external_bytes_(o.external_bytes_), hip_(o.hip_), hip_bytes_(o.hip_bytes_),
+      layout_(o.layout_) {
   o.external_ = nullptr;
   o.external_bytes_ = 0;
   o.hip_ = nullptr;
   o.hip_bytes_ = 0;
+  o.layout_ = StorageLayout::Raw;
 }
 
 Tensor& Tensor::operator=(Tensor&& o) noexcept {
@@ -180,10 +182,12 @@ Tensor& Tensor::operator=(Tensor&& o) noexcept {
   external_bytes_ = o.external_bytes_;
   hip_ = o.hip_;
   hip_bytes_ = o.hip_bytes_;
+  layout_ = o.layout_;
   o.external_ = nullptr;
   o.external_bytes_ = 0;
   o.hip_ = nullptr;
   o.hip_bytes_ = 0;
+  o.layout_ = StorageLayout::Raw;
   return *this;
 }
 
@@ -307,6 +311,18 @@ Status Tensor::bind_hip_data(void* data, size_t bytes) {
   return Status::make_ok();
 }
 
+Status Tensor::adopt_hip_bytes(void* data, size_t bytes, StorageLayout layout) {
+  if (data == nullptr || hip_ == nullptr || device_.type != DeviceType::HIP)
+    return Status::invalid_argument("adopt_hip_bytes needs a tensor that owns HIP storage: " +
+                                    name_);
+  const hipError_t err = hipFree(hip_);
+  if (err != hipSuccess) return hip_status(err, "hipFree failed");
+  hip_ = data;
+  hip_bytes_ = bytes;
+  layout_ = layout;
+  return Status::make_ok();
+}
+
 Status Tensor::release() {
   Status st;
   if (hip_) {
@@ -319,6 +335,7 @@ Status Tensor::release() {
   external_bytes_ = 0;
   host_.clear();
   host_.shrink_to_fit();
+  layout_ = StorageLayout::Raw;
   return st;
 }
 

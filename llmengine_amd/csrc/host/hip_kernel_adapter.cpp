@@ -99,6 +99,26 @@ Status check_q8_storage_bytes(const Tensor* t, std::string_view name) {
   return Status::make_ok();
 }
 
+// Embedding and MatMul read GGUF blocks; a Linear weight re-tiled in place by
+// HipExecutor::tile_weights(ctx, true) holds another byte order.
+Status check_raw_layout(const Tensor* t, std::string_view name) {
+  if (t->storage_layout() == StorageLayout::Raw) return Status::make_ok();
+  return Status::unsupported(std::string(name) +
+                             " holds Q8_0 16-row tiles (re-tiled in place for Linear); this op "
+                             "reads raw Q8_0 blocks");
+}
+
+// Storage of a Q8_0 weight in its layout: raw blocks, or N x K in 16-row tiles.
+Status check_q8_layout_bytes(const Tensor* t, int N, int K, std::string_view name) {
+  if (t->storage_layout() == StorageLayout::Raw) return check_q8_storage_bytes(t, name);
+  const size_t need = hip::q8_0_tiled_bytes(N, K);
+  if (t->allocated_bytes() < need)
+    return Status::out_of_range(std::string(name) + " Q8_0 tiled storage is too small: need " +
+                                std::to_string(need) + " bytes, got " +
+                                std::to_string(t->allocated_bytes()));
+  return Status::make_ok();
+}
+
 Status check_storage_bytes(const Tensor* t, size_t need, std::string_view name) {
   if (t->allocated_bytes() < need)
     return Status::out_of_range(std::string(name) + " storage is too small: need " +
@@ -147,6 +167,7 @@ Status kernel_embedding(const Node& node, RuntimeContext& ctx) {
   auto hidden = checked_dim((*wt)->shape().dim(1), "embedding hidden");
   if (!hidden) return hidden.error();
   TRY(check_q8_block_aligned(*hidden, "embedding"));
+  TRY(check_raw_layout(*wt, "embedding weight"));
   TRY(check_q8_storage_bytes(*wt, "embedding weight"));
   TRY(check_storage_bytes(*ids, static_cast<size_t>(*seq_len) * 4, "input_ids"));
   TRY(check_storage_bytes(*ot, static_cast<size_t>(*seq_len) * static_cast<size_t>(*hidden) * 4,
@@ -200,9 +221,19 @@ Status kernel_linear(const Node& node, RuntimeContext& ctx) {
     bias = (*bt)->data();
   }
   TRY(check_q8_block_aligned(*K, "linear"));
-  TRY(check_q8_storage_bytes(*wt, "linear weight"));
+  TRY(check_q8_layout_bytes(*wt, *N, *K, "linear weight"));
   TRY(check_storage_bytes(*xt, static_cast<size_t>(*M) * static_cast<size_t>(*K) * 4, "x"));
   TRY(check_storage_bytes(*ot, static_cast<size_t>(*M) * static_cast<size_t>(*N) * 4, "output"));
+  if ((*wt)->storage_layout() == StorageLayout::Q8_0Tiled) {
+    const auto* x = static_cast<const float*>((*xt)->data());
+    const auto* w = static_cast<const uint8_t*>((*wt)->data());
+    auto* y = static_cast<float*>((*ot)->data());
+    return bias_bf16 ? hip::sgemm_nt_tiled_bias_bf16(x, w, y, *M, *N, *K,
+                                                     static_cast<const uint16_t*>(bias),
+                                                     ctx.hip_stream())
+                     : hip::sgemm_nt_tiled(x, w, y, *M, *N, *K, static_cast<const float*>(bias),
+                                           ctx.hip_stream());
+  }
   if (bias_bf16)
     return hip::sgemm_nt_bias_bf16(static_cast<const float*>((*xt)->data()),
                                    static_cast<const uint8_t*>((*wt)->data()),
@@ -241,6 +272,7 @@ Status kernel_swiglu(const Node& node, RuntimeContext& ctx) {
 struct LinearOperands {
   const float* x = nullptr;
   const uint8_t* w = nullptr;
+  bool w_tiled = false;  // w holds 16-row tiles (re-tiled in place), not GGUF blocks
   const void* bias = nullptr;
   bool bias_bf16 = false;
   float* y = nullptr;
@@ -286,7 +318,7 @@ expected<LinearOperands, Status> linear_operands(const Node& node, RuntimeContex
     o.bias = (*bt)->data();
   }
   st = check_q8_block_aligned(*K, "linear");
-  if (st.ok()) st = check_q8_storage_bytes(*wt, "linear weight");
+  if (st.ok()) st = check_q8_layout_bytes(*wt, *N, *K, "linear weight");
   if (st.ok())
     st = check_storage_bytes(*xt, static_cast<size_t>(*M) * static_cast<size_t>(*K) * 4, "x");
   if (st.ok())
@@ -295,6 +327,7 @@ expected<LinearOperands, Status> linear_operands(const Node& node, RuntimeContex
   if (!st.ok()) return unexpected(st);
   o.x = static_cast<const float*>((*xt)->data());
   o.w = static_cast<const uint8_t*>((*wt)->data());
+  o.w_tiled = (*wt)->storage_layout() == StorageLayout::Q8_0Tiled;
   o.y = static_cast<float*>((*ot)->data());
   o.M = *M;
   o.N = *N;
@@ -329,6 +362,7 @@ Status kernel_matmul(const Node& node, RuntimeContext& ctx) {
   if (*bk != *K) return Status::shape_mismatch("MatMul inner dimensions differ");
   TRY(check_q8_block_aligned(*K, "matmul reduction dimension"));
   TRY(check_q8_block_aligned(*N, "matmul output dimension"));
+  TRY(check_raw_layout(*bt, "matmul b"));
   TRY(check_q8_storage_bytes(*bt, "matmul b"));
   TRY(check_storage_bytes(*at, static_cast<size_t>(*M) * static_cast<size_t>(*K) * 4, "a"));
   TRY(check_storage_bytes(*ot, static_cast<size_t>(*M) * static_cast<size_t>(*N) * 4, "output"));
@@ -428,10 +462,10 @@ const uint8_t* tiled_copy_of(const TiledWeights* tiled, const void* raw, int64_t
 }
 
 expected<bool, Status> run_tiled_linear(const Node& node, RuntimeContext& ctx,
-                                        const TiledWeights& tiled) {
+                                        const TiledWeights* tiled) {
   auto o = linear_operands(node, ctx);
   if (!o) return false;
-  const uint8_t* t = tiled_copy_of(&tiled, o->w, o->N, o->K);
+  const uint8_t* t = o->w_tiled ? o->w : tiled_copy_of(tiled, o->w, o->N, o->K);
   if (t == nullptr) return false;
   const Status st =
       o->bias_bf16
@@ -455,8 +489,10 @@ expected<bool, Status> run_fused_swiglu(const Node& gate, const Node& up, const 
   if (!ot || !check_hip_float(ot, "output").ok() ||
       !check_storage_bytes(ot, static_cast<size_t>(g->M) * g->N * 4, "output").ok())
     return false;
-  const uint8_t* tg = tiled_copy_of(tiled, g->w, g->N, g->K);
-  const uint8_t* tu = tiled_copy_of(tiled, u->w, u->N, u->K);
+  const uint8_t* tg = g->w_tiled ? g->w : tiled_copy_of(tiled, g->w, g->N, g->K);
+  const uint8_t* tu = u->w_tiled ? u->w : tiled_copy_of(tiled, u->w, u->N, u->K);
+  // One weight re-tiled in place and the other raw with no copy: node by node.
+  if ((g->w_tiled || u->w_tiled) && !(tg && tu)) return false;
   if (used_tiled) *used_tiled = tg && tu;
   const Status st =
       tg && tu ? hip::linear_swiglu_tiled(g->x, tg, tu, static_cast<float*>(ot->data()), g->M,
@@ -472,6 +508,7 @@ expected<bool, Status> run_fused_multi(const std::vector<const Node*>& nodes,
                                        bool* used_tiled) {
   if (nodes.size() < 2 || nodes.size() > 3) return false;
   const uint8_t* w[3];
+  bool in_place[3] = {false, false, false};
   const float* b[3];
   float* y[3];
   int N[3];
@@ -482,16 +519,19 @@ expected<bool, Status> run_fused_multi(const std::vector<const Node*>& nodes,
     if (i == 0) first = *o;
     else if (o->x != first.x || o->M != first.M || o->K != first.K) return false;
     w[i] = o->w;
+    in_place[i] = o->w_tiled;
     b[i] = static_cast<const float*>(o->bias);
     y[i] = o->y;
     N[i] = o->N;
   }
   const uint8_t* tw[3] = {nullptr, nullptr, nullptr};
-  bool all_tiled = true;
+  bool all_tiled = true, any_in_place = false;
   for (size_t i = 0; i < nodes.size(); ++i) {
-    tw[i] = tiled_copy_of(tiled, w[i], N[i], first.K);
+    tw[i] = in_place[i] ? w[i] : tiled_copy_of(tiled, w[i], N[i], first.K);
     all_tiled = all_tiled && tw[i] != nullptr;
+    any_in_place = any_in_place || in_place[i];
   }
+  if (any_in_place && !all_tiled) return false;  // mixed layouts: node by node
   if (used_tiled) *used_tiled = all_tiled;
   const Status st =
       all_tiled ? hip::linear_multi_tiled(first.x, static_cast<int>(nodes.size()), tw, b, y, N,

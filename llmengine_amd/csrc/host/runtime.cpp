@@ -126,16 +126,27 @@ void HipExecutor::release_tiled_weights() {
   tiled_.clear();
 }
 
-Status HipExecutor::tile_weights(RuntimeContext& ctx) {
+Status HipExecutor::tile_weights(RuntimeContext& ctx, bool release_raw) {
   if (!graph_) return Status::runtime_error("executor not compiled");
   // Overwritten weights get fresh copies: drop the old ones first.
   release_tiled_weights();
+  in_place_ = 0;
+  // Buffers read other than as a Linear weight (an Embedding table, a MatMul
+  // operand, ...), through any value bound to them, keep their raw bytes.
+  std::unordered_set<const void*> other_use;
+  if (release_raw)
+    for (const Node& n : graph_->nodes())
+      for (size_t i = 0; i < n.inputs().size(); ++i) {
+        if (n.op_type() == OpType::Linear && i == 1) continue;
+        if (const Tensor* t = ctx.get(n.inputs()[i]); t && t->data()) other_use.insert(t->data());
+      }
   for (const Node& n : graph_->nodes()) {
     if (n.op_type() != OpType::Linear || n.inputs().size() < 2) continue;
     Tensor* w = ctx.get(n.inputs()[1]);
     if (!w || w->dtype() != DType::Q8_0 || w->device().type != DeviceType::HIP ||
         w->data() == nullptr || w->shape().rank() != 2)
       continue;  // not on this path: the node keeps its registered kernel and its checks
+    if (w->storage_layout() != StorageLayout::Raw) continue;  // re-tiled in place already
     const int64_t N = w->shape().dim(0), K = w->shape().dim(1);
     if (N <= 0 || K <= 0 || K % 32 != 0 || N > INT32_MAX || K > INT32_MAX) continue;
     if (w->allocated_bytes() < q8_0_bytes(N * K)) continue;
@@ -148,14 +159,27 @@ Status HipExecutor::tile_weights(RuntimeContext& ctx) {
       return Status::runtime_error(std::string("tiled weight allocation failed: ") +
                                    hipGetErrorString(err));
     }
-    tiled_bufs_.push_back(buf);
-    const Status st = hip::tile_q8_0(static_cast<const uint8_t*>(w->data()),
-                                     static_cast<uint8_t*>(buf), static_cast<int>(N),
-                                     static_cast<int>(K), stream_);
+    const bool in_place = release_raw && w->owns_hip_storage() && !other_use.count(w->data());
+    if (!in_place) tiled_bufs_.push_back(buf);
+    Status st = hip::tile_q8_0(static_cast<const uint8_t*>(w->data()),
+                               static_cast<uint8_t*>(buf), static_cast<int>(N),
+                               static_cast<int>(K), stream_);
+    if (st.ok() && in_place) {
+      // The tile kernel must be done with the raw bytes before they are freed.
+      const hipError_t e = hipStreamSynchronize(stream_);
+      st = e == hipSuccess ? w->adopt_hip_bytes(buf, bytes, StorageLayout::Q8_0Tiled)
+                           : Status::runtime_error(std::string("hipStreamSynchronize failed: ") +
+                                                   hipGetErrorString(e));
+      if (!st.ok()) (void)hipFree(buf);
+    }
     if (!st.ok()) {
       release_tiled_weights();
       return Status::runtime_error("tiling Linear weight of node #" + std::to_string(n.id().value) +
                                    " failed: " + st.to_string());
+    }
+    if (in_place) {
+      ++in_place_;
+      continue;
     }
     tiled_[w->data()] = detail::TiledCopy{static_cast<const uint8_t*>(buf), N, K, bytes};
   }
@@ -404,10 +428,10 @@ Status HipExecutor::run(RuntimeContext& ctx) {
         continue;
       }
     }
-    if (tiled && step.kind == Step::kNode) {
+    if (step.kind == Step::kNode) {
       auto nd = graph_->node(step.nodes[0]);
       if (nd && (*nd)->op_type() == OpType::Linear) {
-        auto done = detail::run_tiled_linear(**nd, ctx, *tiled);
+        auto done = detail::run_tiled_linear(**nd, ctx, tiled);
         if (!done)
           return Status::runtime_error("HIP kernel Linear failed for node #" +
                                        std::to_string(step.nodes[0].value) + " (" +

@@ -1161,6 +1161,152 @@ static void test_executor_linear_bf16_bias() {
   std::printf("  executor_linear_bf16_bias ok\n");
 }
 
+static void test_executor_tiles_in_place() {
+  // tile_weights(ctx, release_raw = true): the Linear-only weights (gate, up,
+  // down, q) are re-tiled in place -- the tensors adopt 16-row tiles and their
+  // raw bytes are freed -- while the table read by both an Embedding and a
+  // Linear (a tied lm_head, bound to two values) keeps its raw bytes and gets a
+  // copy.  Outputs match the raw run (bitwise on the MFMA paths, 1e-6 relative
+  // L2 where the tiled FP32 GEMV runs, M = 1), also from a second executor that
+  // never tiled anything (the registered Linear kernel reads the layout tag),
+  // and an Embedding on an in-place tiled tensor is rejected.
+  const int K = 128, I = 96, Q = 64, V = 80, T = 4;
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  const Device dev = Device::hip(0);
+  for (int fuse = 0; fuse < 2; ++fuse) {
+    for (int M : {1, 5, 70}) {
+      Graph g;
+      GraphBuilder gb(g);
+      auto x = gb.input("x", Shape({M, K}), DType::Float32, dev);
+      auto ids = gb.input("ids", Shape({T}), DType::Int32, dev);
+      CHECK(x && ids);
+      const char* names[6] = {"wg", "wu", "wd", "wq", "table_e", "table_l"};
+      const int rows[6] = {I, I, K, Q, V, V};
+      const int cols[6] = {K, K, I, K, K, K};
+      std::vector<ValueId> cw;
+      for (int i = 0; i < 6; ++i) {
+        auto c = gb.constant(names[i], Shape({rows[i], cols[i]}), DType::Float32, dev);
+        CHECK(c);
+        cw.push_back(*c);
+      }
+      auto gate = gb.linear(*x, cw[0], std::nullopt, "gate");
+      auto up = gb.linear(*x, cw[1], std::nullopt, "up");
+      CHECK(gate && up);
+      auto act = gb.swiglu(*gate, *up, "swiglu");
+      CHECK(act);
+      auto down = gb.linear(*act, cw[2], std::nullopt, "down");
+      auto q = gb.linear(*x, cw[3], std::nullopt, "q");
+      auto emb = gb.embedding(*ids, cw[4], "embed");
+      auto logits = gb.linear(*x, cw[5], std::nullopt, "lm_head");
+      CHECK(down && q && emb && logits);
+      CHECK(gb.output(*down, "o_down") && gb.output(*q, "o_q") && gb.output(*emb, "o_emb") &&
+            gb.output(*logits, "o_logits"));
+      std::vector<std::unique_ptr<Tensor>> tw;
+      RuntimeContext ctx;
+      for (int i = 0; i < 5; ++i) {
+        tw.push_back(std::make_unique<Tensor>(names[i], Shape({rows[i], cols[i]}), DType::Q8_0,
+                                              dev));
+        const auto hw = synth_q8(rows[i], cols[i], 90 + i);
+        check_status(tw.back()->allocate_hip_bytes(hw.size()));
+        upload(*tw.back(), hw.data(), hw.size());
+        check_status(ctx.bind(cw[i], tw.back().get()));
+      }
+      check_status(ctx.bind(cw[5], tw[4].get()));  // tied: one table, two values
+      std::vector<float> hx(size_t(M) * K);
+      for (size_t i = 0; i < hx.size(); ++i) hx[i] = float(int(i * 37 % 101) - 50) * 0.02f;
+      Tensor tx("x", Shape({M, K}), DType::Float32, dev);
+      check_status(tx.allocate_hip());
+      upload(tx, hx.data(), hx.size() * 4);
+      std::vector<int> hids{3, 0, 79, 41};
+      Tensor tids("ids", Shape({T}), DType::Int32, dev);
+      check_status(tids.allocate_hip());
+      upload(tids, hids.data(), hids.size() * 4);
+      check_status(ctx.bind(*x, &tx));
+      check_status(ctx.bind(*ids, &tids));
+      check_status(ctx.allocate_intermediates(g));
+      const size_t counts[4] = {size_t(M) * K, size_t(M) * Q, size_t(T) * K, size_t(M) * V};
+      const ValueId outs_id[4] = {*down, *q, *emb, *logits};
+      auto outputs = [&]() {
+        std::vector<std::vector<float>> o;
+        for (int i = 0; i < 4; ++i) o.push_back(download(ctx.get(outs_id[i]), counts[i]));
+        return o;
+      };
+      auto same = [&](const std::vector<std::vector<float>>& a,
+                      const std::vector<std::vector<float>>& b) {
+        for (int o = 0; o < 4; ++o) {
+          if (o == 2 || M > 1) {  // embedding always, Linears on the MFMA paths: bitwise
+            CHECK(std::memcmp(a[o].data(), b[o].data(), a[o].size() * 4) == 0);
+            continue;
+          }
+          double num = 0, den = 0;
+          for (size_t i = 0; i < a[o].size(); ++i) {
+            num += double(a[o][i] - b[o][i]) * (a[o][i] - b[o][i]);
+            den += double(a[o][i]) * a[o][i];
+          }
+          CHECK(std::sqrt(num / den) <= 1e-6);
+        }
+      };
+      HipExecutor ex(std::make_shared<HipBackend>(), registry);
+      ex.set_fusion(fuse == 1);
+      check_status(ex.compile(g));
+      check_status(ex.run(ctx));
+      check_hip(hipDeviceSynchronize());
+      const auto ref = outputs();
+
+      check_status(ex.tile_weights(ctx, true));
+      CHECK(ex.tiled_in_place() == 4u);
+      CHECK(ex.tiled_weights() == 1u);  // the tied table: a copy, raw bytes kept
+      for (int i = 0; i < 4; ++i) {
+        CHECK(tw[i]->storage_layout() == StorageLayout::Q8_0Tiled);
+        CHECK(tw[i]->allocated_bytes() == hip::q8_0_tiled_bytes(rows[i], cols[i]));
+      }
+      CHECK(tw[4]->storage_layout() == StorageLayout::Raw);
+      check_status(ex.run(ctx));
+      check_hip(hipDeviceSynchronize());
+      // fused: gate+up+SwiGLU, q+lm_head, down; unfused: five Linears
+      CHECK(ex.tiled_launches() == (fuse ? 3u : 5u));
+      same(ref, outputs());
+
+      // An executor that never tiled: the registered Linear kernel follows the tag.
+      HipExecutor ex2(std::make_shared<HipBackend>(), registry);
+      ex2.set_fusion(fuse == 1);
+      check_status(ex2.compile(g));
+      check_status(ex2.run(ctx));
+      check_hip(hipDeviceSynchronize());
+      same(ref, outputs());
+
+      // Dropping the copies leaves the in-place tiles (the raw bytes are gone).
+      ex.release_tiled_weights();
+      CHECK(tw[0]->storage_layout() == StorageLayout::Q8_0Tiled);
+      check_status(ex.run(ctx));
+      check_hip(hipDeviceSynchronize());
+      same(ref, outputs());
+
+      if (fuse == 0 && M == 1) {
+        // Embedding over an in-place tiled tensor is refused.
+        Graph g2;
+        GraphBuilder gb2(g2);
+        auto ids2 = gb2.input("ids", Shape({T}), DType::Int32, dev);
+        auto tab2 = gb2.constant("wq", Shape({Q, K}), DType::Float32, dev);
+        CHECK(ids2 && tab2);
+        auto e2 = gb2.embedding(*ids2, *tab2, "embed");
+        CHECK(e2 && gb2.output(*e2, "o"));
+        RuntimeContext ctx2;
+        check_status(ctx2.bind(*ids2, &tids));
+        check_status(ctx2.bind(*tab2, tw[3].get()));
+        check_status(ctx2.allocate_intermediates(g2));
+        HipExecutor ex3(std::make_shared<HipBackend>(), registry);
+        check_status(ex3.compile(g2));
+        const Status st = ex3.run(ctx2);
+        CHECK(!st.ok());
+        CHECK(st.to_string().find("16-row tiles") != std::string::npos);
+      }
+    }
+  }
+  std::printf("  PASS test_executor_tiles_in_place\n");
+}
+
 int main() {
   int count = 0;
   check_hip(hipGetDeviceCount(&count));
@@ -1182,6 +1328,7 @@ int main() {
   test_tiled_copy_shape_guard();
   test_loader_dequantizes_q8_0_on_device();
   test_executor_linear_bf16_bias();
+  test_executor_tiles_in_place();
   std::printf("test_hip_q8_0: all passed\n");
   return 0;
 }
