@@ -491,7 +491,7 @@ def test_matmul_known_answers(dev, golden):
 
 
 @pytest.mark.parametrize("M,N,K", [(2, 32, 32), (3, 64, 160), (5, 256, 512), (1, 32, 4096),
-                                   (8, 1024, 96), (33, 96, 64)])
+                                   (8, 1024, 96), (33, 96, 64), (4, 32, 32), (70, 512, 256)])
 def test_matmul_bitexact(dev, orc, M, N, K):
     note(f"matmul M={M} N={N} K={K}")
     b, a = weight(100 + N, K, N), acts(101 + K, M, K)
