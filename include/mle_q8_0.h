@@ -15,9 +15,11 @@
  *     (mle_q8_0_workspace_size + mle_workspace_reserve); otherwise it is
  *     allocated with hipMalloc on first need.  It only grows, each buffer to
  *     max(capacity, need), after a synchronise of that stream, and lives until
- *     process exit.  Nothing else is allocated.  Entry points are re-entrant;
- *     calls writing the same output buffer on different streams race, as with
- *     any kernel.
+ *     process exit.  Nothing else is allocated.  Entry points are re-entrant
+ *     and may be called from several host threads, also on one stream (a call
+ *     that grows a workspace waits until no other call is still enqueuing
+ *     launches on the old buffers); calls writing the same output buffer on
+ *     different streams race, as with any kernel.
  *   - Return value: 0 on success, else a value of the reference's ErrorCode
  *     enum (include/minillm/core/status.h:20-32): 1 InvalidArgument,
  *     2 OutOfRange, 3 ShapeMismatch, 4 Unsupported, 6 RuntimeError.  The

@@ -166,17 +166,22 @@ int ensure_workspace(size_t bytes, size_t counters, hipStream_t stream, StreamWo
   return MLE_OK;
 }
 
-int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWorkspace* out) {
+// `hold` keeps the workspace table locked until the caller has enqueued the
+// launch that uses the buffers, so a concurrent call that grows (frees and
+// reallocates) the same stream's workspace cannot free them in between.
+int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWorkspace* out,
+                  std::unique_lock<std::mutex>* hold) {
   *out = mle::SplitKWorkspace{};
   const size_t bytes = need_bytes(need);
   if (bytes == 0) return MLE_OK;
   const size_t partial_bytes = (need.partial_floats * sizeof(float) + 255) / 256 * 256;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
+  std::unique_lock<std::mutex> lock(g_ws_mu);
   StreamWorkspace* e = nullptr;
   MLE_TRY(ensure_workspace(bytes, need.counters, stream, &e));
   out->partials = reinterpret_cast<float*>(e->buf);
   out->counters = e->counters;
   out->scratch = need.scratch_bytes ? e->buf + partial_bytes : nullptr;
+  *hold = std::move(lock);
   return MLE_OK;
 }
 
@@ -197,7 +202,8 @@ struct Exec {
   bool planning() const { return plan_bytes != nullptr; }
 };
 
-int workspace_for(const mle::SplitKNeed& need, const Exec& ex, mle::SplitKWorkspace* out) {
+int workspace_for(const mle::SplitKNeed& need, const Exec& ex, mle::SplitKWorkspace* out,
+                  std::unique_lock<std::mutex>* hold) {
   if (ex.planning()) {
     *out = mle::SplitKWorkspace{};
     *ex.plan_bytes = std::max(*ex.plan_bytes, need_bytes(need));
@@ -220,7 +226,7 @@ int workspace_for(const mle::SplitKNeed& need, const Exec& ex, mle::SplitKWorksp
     out->scratch = need.scratch_bytes ? ex.fixed_buf + partial_bytes : nullptr;
     return MLE_OK;
   }
-  return get_workspace(need, ex.stream, out);
+  return get_workspace(need, ex.stream, out, hold);
 }
 
 // Linear path numbers (mle_q8_0_linear_ex): 1 FP32 GEMV, 2 bf16-MFMA prefill GEMM,
@@ -282,7 +288,8 @@ int run_linear(const float* x, const uint8_t* w, const void* bias, float* y, int
     if (!mle::gemm_mfma_fits(c, M, N, K))
       return fail(MLE_UNSUPPORTED, "hip sgemm_nt Q8_0: K too large for the MFMA GEMM");
     mle::SplitKWorkspace ws;
-    MLE_TRY(workspace_for(mle::gemm_mfma_workspace(c, M, N, K), ex, &ws));
+    std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
+    MLE_TRY(workspace_for(mle::gemm_mfma_workspace(c, M, N, K), ex, &ws, &hold));
     return check_launch((ex.planning() ? hipSuccess : mle::launch_gemm_mfma_segs(c, x, one, M, K, ws, ex.stream)),
                         "hip sgemm_nt Q8_0 launch failed");
   }
@@ -300,7 +307,8 @@ int run_linear(const float* x, const uint8_t* w, const void* bias, float* y, int
       mle::LinearSegs chunk = one;
       chunk.seg[0].y = y + (int64_t)m0 * N;
       mle::SplitKWorkspace ws;
-      MLE_TRY(workspace_for(mle::decode_mfma_workspace_segs(c, chunk, K), ex, &ws));
+      std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
+      MLE_TRY(workspace_for(mle::decode_mfma_workspace_segs(c, chunk, K), ex, &ws, &hold));
       const hipError_t err =
           (ex.planning() ? hipSuccess : mle::launch_gemv_mfma_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ws, ex.stream));
       if (err != hipSuccess) return check_launch(err, "hip sgemm_nt Q8_0 launch failed");
@@ -342,7 +350,8 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
     if (!mle::gemm_mfma_fits(c, M, 0, K))
       return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": K too large for the MFMA GEMM");
     mle::SplitKWorkspace ws;
-    MLE_TRY(workspace_for(mle::gemm_mfma_workspace_segs(c, M, s, K), ex, &ws));
+    std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
+    MLE_TRY(workspace_for(mle::gemm_mfma_workspace_segs(c, M, s, K), ex, &ws, &hold));
     return check_launch((ex.planning() ? hipSuccess : mle::launch_gemm_mfma_segs(c, x, s, M, K, ws, ex.stream)),
                         "hip Q8_0 fused Linear launch failed");
   }
@@ -369,7 +378,8 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
       chunk.seg[i].y = s.seg[i].y + (int64_t)m0 * s.seg[i].N;
     }
     mle::SplitKWorkspace ws;
-    MLE_TRY(workspace_for(mle::decode_mfma_workspace_segs(c, chunk, K), ex, &ws));
+    std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
+    MLE_TRY(workspace_for(mle::decode_mfma_workspace_segs(c, chunk, K), ex, &ws, &hold));
     const hipError_t err =
         (ex.planning() ? hipSuccess : mle::launch_gemv_mfma_segs(c, x + (int64_t)m0 * K, chunk, mc, K, ws, ex.stream));
     if (err != hipSuccess) return check_launch(err, "hip Q8_0 fused Linear launch failed");
@@ -726,7 +736,8 @@ int mle_argmax_f32(const float* logits, int rows, int n, int32_t* idx, float* va
   mle::SplitKNeed need;
   need.partial_floats = (size_t)rows * mle::argmax_chunks(n) * 2;  // 64-bit keys
   mle::SplitKWorkspace ws;
-  MLE_TRY(get_workspace(need, stream, &ws));
+  std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
+  MLE_TRY(get_workspace(need, stream, &ws, &hold));
   return check_launch(mle::launch_argmax(logits, rows, n, idx, val,
                                          reinterpret_cast<uint64_t*>(ws.partials), stream),
                       "hip argmax launch failed");
@@ -756,7 +767,8 @@ int mle_top_tokens_f32(const float* logits, int rows, int n, int top_n, float te
   mle::SplitKNeed need;
   need.partial_floats = mle::top_tokens_workspace_floats(rows, n, top_n);
   mle::SplitKWorkspace ws;
-  MLE_TRY(get_workspace(need, stream, &ws));
+  std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
+  MLE_TRY(get_workspace(need, stream, &ws, &hold));
   return check_launch(mle::launch_top_tokens(logits, rows, n, top_n, temperature, ids, probs,
                                              ws.partials, stream),
                       "hip top_tokens launch failed");

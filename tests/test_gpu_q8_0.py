@@ -417,6 +417,53 @@ def test_linear_decode_mfma_split_k_after_poisoned_workspace(dev, orc):
         assert np.isnan(to_host(yp)).all()
 
 
+def test_linear_threads_share_one_stream_while_workspace_grows(dev, orc):
+    """Host threads launching on one (new) stream while its workspace grows: each
+    thread runs shapes of increasing workspace need (8 -> 22 splits, then the
+    prefill GEMM with its bf16 copy of X), so some calls free and reallocate the
+    buffers other threads just took.  The workspace table stays locked until a
+    launch is enqueued, so every result equals the oracle's (decode 1e-5, GEMM
+    1e-2) and the workspace ends at the largest need."""
+    import threading
+    import torch
+    shapes = [(8, 1024, 4096), (4, 1024, 11008), (96, 256, 2048)]
+    data = []
+    for i, (M, N, K) in enumerate(shapes):
+        w, x = weight(140 + i, N, K), acts(141 + i, M, K)
+        data.append((M, N, K, to_dev(w, dev), to_dev(x, dev), orc.sgemm_nt(x, w, M, N, K)))
+    stream = torch.cuda.Stream()
+    T, R = 3, 4
+    outs = [[[empty_f32((M, N), dev) for (M, N, K, *_r) in data] for _ in range(R)]
+            for _ in range(T)]
+    errors = []
+
+    def work(t):
+        try:
+            for r in range(R):
+                for i, (M, N, K, dw, dx, _) in enumerate(data):
+                    capi.linear(dx, dw, None, outs[t][r][i], M, N, K, stream=stream)
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    torch.cuda.synchronize()  # inputs and outputs are in place before any launch
+    note("threads share one stream while its workspace grows")
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(T)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    stream.synchronize()
+    assert not errors, errors
+    for t in range(T):
+        for r in range(R):
+            for i, (M, N, K, _dw, _dx, want) in enumerate(data):
+                bar = MFMA_TOL if M >= 64 else GEMV_TOL
+                assert rel_l2(to_host(outs[t][r][i]), want) <= bar, (t, r, i)
+    need = [capi.workspace_size(capi.OP_LINEAR, M, [N], K) for (M, N, K, *_r) in data]
+    b, c, _g = capi.workspace_info(stream)
+    assert b >= max(n[0] for n in need) and c >= max(n[1] for n in need)
+
+
 # ----------------------------------------------------------------------------- linear MFMA
 
 @pytest.mark.parametrize("M,N,K", [(64, 64, 64), (65, 130, 96), (128, 128, 128),
