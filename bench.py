@@ -507,7 +507,20 @@ def main():
                                "GBps": round(eb / med / 1e3, 1),
                                "frac_hbm": round(eb / med / 1e3 / HBM_PEAK_GBS, 4),
                                "rotated_copies": Re}
+        # the same gather from the table in 16-row tiles (a tied lm_head kept tiled only)
+        ttbls = [tiled_copy(capi, t, V, H, stream) for t in tbls]
         del tbls
+        out_t = torch.empty((T, H), dtype=torch.float32, device=dev)
+        med, lo, hi = timer(lambda j: capi.embedding_tiled(ttbls[j % Re], ids, out_t, T, V, H,
+                                                           stream=stream), 100)
+        same_t = bool(torch.equal(out_t.view(torch.int32), out.view(torch.int32)))
+        parity["checks"].append({"what": "embedding configs[4] from the tiled table, full "
+                                         "output vs the raw gather", "bitexact": same_t,
+                                 "ok": same_t})
+        extras["embedding"].update({"us_tiled_table": round(med, 2),
+                                    "us_tiled_table_spread": [round(lo, 2), round(hi, 2)],
+                                    "GBps_tiled_table": round(eb / med / 1e3, 1)})
+        del ttbls
         # ---- Qwen2.5-0.5B-shaped decode Linears at M = 1 and the tied
         # lm_head at M = 1 and 8 (small ones are latency-bound: wall-clock per launch)
         qwen = []

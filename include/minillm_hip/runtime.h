@@ -160,13 +160,13 @@ class HipExecutor final : public Executor {
   // each Linear weight (the raw buffer stays with the caller).
   //
   // release_raw: a weight whose tensor owns its device storage
-  // (allocate_hip*) and whose buffer the graph reads only as Linear weights
-  // (not as an Embedding table, e.g. a tied lm_head, nor a MatMul operand) is
-  // re-tiled in place instead: the tensor adopts the tiled buffer
+  // (allocate_hip*) and whose buffer the graph reads only as Linear weights or
+  // Embedding tables (a tied lm_head), not as a MatMul operand, is re-tiled in
+  // place instead: the tensor adopts the tiled buffer
   // (StorageLayout::Q8_0Tiled) and its raw bytes are freed after a synchronise
   // of this stream, so the weight costs no extra memory.  Such a tensor stays
-  // tiled for good: any executor's Linear kernel runs it on the tiled entry
-  // points, Embedding and MatMul reject it, and it must not be refilled with
+  // tiled for good: any executor's Linear and Embedding kernels run it on the
+  // tiled entry points, MatMul rejects it, and it must not be refilled with
   // raw bytes (reallocate it first).  Other weights get copies as above.
   Status tile_weights(RuntimeContext& ctx, bool release_raw = false);
   void release_tiled_weights();
@@ -222,6 +222,9 @@ Status sgemm(const float* A, const uint8_t* B_q8_0, float* C, int M, int N, int 
              hipStream_t stream = nullptr);
 Status embedding(const uint8_t* weight_q8_0, const int* ids, float* out, int seq_len,
                  int vocab_size, int hidden, hipStream_t stream = nullptr);
+// The same gather from a table in 16-row tiles (mle_q8_0_embedding_tiled).
+Status embedding_tiled(const uint8_t* weight_tiled, const int* ids, float* out, int seq_len,
+                       int vocab_size, int hidden, hipStream_t stream = nullptr);
 // WeightLoader::dequantize_to_f32's Q8_0 case on the device (mle_q8_0_dequantize;
 // reference src/io/gguf_weight_loader.cpp:446-463): out[e] = q * d, e < n.
 Status dequantize_q8_0(const uint8_t* src_q8_0, float* out, int64_t n,

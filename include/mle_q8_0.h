@@ -153,6 +153,16 @@ int mle_q8_0_embedding(const uint8_t* table_q8_0, const int32_t* ids, float* out
                        int seq_len, int vocab, int hidden, hipStream_t stream);
 
 /*
+ * mle_q8_0_embedding on a table in Q8_0 16-row tiles (mle_q8_0_tile of the
+ * [vocab, hidden] table; 16-byte aligned): the same output, bit for bit, so a
+ * table shared with a Linear (a tied lm_head) needs only its tiled copy.  No
+ * counterpart in the reference (its tables are raw GGUF bytes).  Errors as
+ * mle_q8_0_embedding, plus a table not 16-byte aligned -> InvalidArgument.
+ */
+int mle_q8_0_embedding_tiled(const uint8_t* table_tiled, const int32_t* ids, float* out,
+                             int seq_len, int vocab, int hidden, hipStream_t stream);
+
+/*
  * Q8_0 -> fp32 dequantisation of a whole tensor on the device: dst[e] = q * d
  * for the n elements of the raw block stream (ceil(n/32) blocks; a partial last
  * block reads only its first n % 32 quants).  Replaces the Q8_0 case of

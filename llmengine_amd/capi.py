@@ -22,7 +22,7 @@ ERROR_NAMES = {0: "Ok", 1: "InvalidArgument", 2: "OutOfRange", 3: "ShapeMismatch
 
 EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_q8_0_linear_swiglu", "mle_q8_0_linear_multi", "mle_q8_0_matmul",
-            "mle_q8_0_embedding", "mle_argmax_f32", "mle_top_tokens_f32", "mle_swiglu_f32",
+            "mle_q8_0_embedding", "mle_q8_0_embedding_tiled", "mle_argmax_f32", "mle_top_tokens_f32", "mle_swiglu_f32",
             "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode", "mle_q8_0_tiled_bytes",
             "mle_q8_0_tile", "mle_q8_0_linear_tiled", "mle_q8_0_linear_swiglu_tiled",
             "mle_q8_0_linear_multi_tiled", "mle_q8_0_workspace_size", "mle_workspace_reserve",
@@ -70,6 +70,8 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_matmul.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_q8_0_embedding.restype = _i
     lib.mle_q8_0_embedding.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mle_q8_0_embedding_tiled.restype = _i
+    lib.mle_q8_0_embedding_tiled.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_swiglu_f32.restype = _i
     lib.mle_swiglu_f32.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp]
     lib.mle_argmax_f32.restype = _i
@@ -245,6 +247,17 @@ def embedding_status(w, ids, out, seq_len, vocab, hidden, stream=None):
 def embedding(w, ids, out, seq_len, vocab, hidden, stream=None) -> None:
     """out[s,h] = dequantised row ids[s] of a raw Q8_0 [vocab, hidden] table."""
     _raise(embedding_status(w, ids, out, seq_len, vocab, hidden, stream)[0])
+
+
+def embedding_tiled_status(w_tiled, ids, out, seq_len, vocab, hidden, stream=None):
+    rc = load().mle_q8_0_embedding_tiled(_addr(w_tiled), _addr(ids), _addr(out), seq_len,
+                                         vocab, hidden, _stream(stream))
+    return _status(rc)
+
+
+def embedding_tiled(w_tiled, ids, out, seq_len, vocab, hidden, stream=None) -> None:
+    """The embedding gather from a table in 16-row tiles (mle_q8_0_tile of [vocab, hidden])."""
+    _raise(embedding_tiled_status(w_tiled, ids, out, seq_len, vocab, hidden, stream)[0])
 
 
 def swiglu_status(gate, up, y, n, stream=None):

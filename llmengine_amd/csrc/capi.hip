@@ -475,7 +475,7 @@ int noalloc_scratch(hipStream_t stream, uint8_t** base) {
 
 extern "C" {
 
-int mle_q8_0_abi_version(void) { return 6; }
+int mle_q8_0_abi_version(void) { return 7; }
 
 const char* mle_last_error(void) { return g_last_error.c_str(); }
 
@@ -809,6 +809,27 @@ int mle_q8_0_embedding(const uint8_t* table_q8_0, const int32_t* ids, float* out
   return check_launch(
       mle::launch_embedding(table_q8_0, ids, out, seq_len, vocab, hidden, stream),
       "hip embedding Q8_0 launch failed");
+}
+
+int mle_q8_0_embedding_tiled(const uint8_t* table_tiled, const int32_t* ids, float* out,
+                             int seq_len, int vocab, int hidden, hipStream_t stream) {
+  const char* ctx = "embedding_q8_0_tiled";
+  MLE_TRY(check_ptrs(ctx, table_tiled, "weight", ids, "ids", out, "out"));
+  if (seq_len < 0)
+    return fail(MLE_INVALID_ARGUMENT,
+                std::string("hip ") + ctx + ": seq_len must not be negative");
+  MLE_TRY(check_positive(ctx, vocab, "vocab_size"));
+  MLE_TRY(check_positive(ctx, hidden, "hidden"));
+  if (hidden % 32 != 0)
+    return fail(MLE_UNSUPPORTED,
+                "hip embedding Q8_0 requires hidden to be a multiple of 32");
+  MLE_TRY(check_align(ctx, table_tiled, 16, "weight"));
+  MLE_TRY(check_align(ctx, ids, 4, "ids"));
+  MLE_TRY(check_align(ctx, out, 16, "out"));
+  if (seq_len == 0) return ok();
+  return check_launch(
+      mle::launch_embedding_tiled(table_tiled, ids, out, seq_len, vocab, hidden, stream),
+      "hip embedding Q8_0 tiled launch failed");
 }
 
 int mle_q8_0_dequantize(const uint8_t* src_q8_0, float* dst, int64_t n, hipStream_t stream) {

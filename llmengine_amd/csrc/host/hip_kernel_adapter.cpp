@@ -99,13 +99,13 @@ Status check_q8_storage_bytes(const Tensor* t, std::string_view name) {
   return Status::make_ok();
 }
 
-// Embedding and MatMul read GGUF blocks; a Linear weight re-tiled in place by
-// HipExecutor::tile_weights(ctx, true) holds another byte order.
+// MatMul reads GGUF blocks along N; a weight re-tiled in place by
+// HipExecutor::tile_weights(ctx, true) holds 16-row tiles along K.
 Status check_raw_layout(const Tensor* t, std::string_view name) {
   if (t->storage_layout() == StorageLayout::Raw) return Status::make_ok();
   return Status::unsupported(std::string(name) +
-                             " holds Q8_0 16-row tiles (re-tiled in place for Linear); this op "
-                             "reads raw Q8_0 blocks");
+                             " holds Q8_0 16-row tiles (re-tiled in place); this op reads raw "
+                             "Q8_0 blocks");
 }
 
 // Storage of a Q8_0 weight in its layout: raw blocks, or N x K in 16-row tiles.
@@ -167,11 +167,15 @@ Status kernel_embedding(const Node& node, RuntimeContext& ctx) {
   auto hidden = checked_dim((*wt)->shape().dim(1), "embedding hidden");
   if (!hidden) return hidden.error();
   TRY(check_q8_block_aligned(*hidden, "embedding"));
-  TRY(check_raw_layout(*wt, "embedding weight"));
-  TRY(check_q8_storage_bytes(*wt, "embedding weight"));
+  TRY(check_q8_layout_bytes(*wt, *vocab, *hidden, "embedding weight"));
   TRY(check_storage_bytes(*ids, static_cast<size_t>(*seq_len) * 4, "input_ids"));
   TRY(check_storage_bytes(*ot, static_cast<size_t>(*seq_len) * static_cast<size_t>(*hidden) * 4,
                           "output"));
+  if ((*wt)->storage_layout() == StorageLayout::Q8_0Tiled)
+    return hip::embedding_tiled(static_cast<const uint8_t*>((*wt)->data()),
+                                static_cast<const int*>((*ids)->data()),
+                                static_cast<float*>((*ot)->data()), *seq_len, *vocab, *hidden,
+                                ctx.hip_stream());
   return hip::embedding(static_cast<const uint8_t*>((*wt)->data()),
                         static_cast<const int*>((*ids)->data()),
                         static_cast<float*>((*ot)->data()), *seq_len, *vocab, *hidden,
@@ -399,6 +403,12 @@ Status embedding(const uint8_t* weight_q8_0, const int* ids, float* out, int seq
                  int vocab_size, int hidden, hipStream_t stream) {
   return from_capi(mle_q8_0_embedding(weight_q8_0, reinterpret_cast<const int32_t*>(ids), out,
                                       seq_len, vocab_size, hidden, stream));
+}
+
+Status embedding_tiled(const uint8_t* weight_tiled, const int* ids, float* out, int seq_len,
+                       int vocab_size, int hidden, hipStream_t stream) {
+  return from_capi(mle_q8_0_embedding_tiled(weight_tiled, reinterpret_cast<const int32_t*>(ids),
+                                            out, seq_len, vocab_size, hidden, stream));
 }
 
 Status dequantize_q8_0(const uint8_t* src_q8_0, float* out, int64_t n, hipStream_t stream) {

@@ -131,13 +131,14 @@ Status HipExecutor::tile_weights(RuntimeContext& ctx, bool release_raw) {
   // Overwritten weights get fresh copies: drop the old ones first.
   release_tiled_weights();
   in_place_ = 0;
-  // Buffers read other than as a Linear weight (an Embedding table, a MatMul
+  // Buffers read other than as a Linear weight or an Embedding table (a MatMul
   // operand, ...), through any value bound to them, keep their raw bytes.
   std::unordered_set<const void*> other_use;
   if (release_raw)
     for (const Node& n : graph_->nodes())
       for (size_t i = 0; i < n.inputs().size(); ++i) {
-        if (n.op_type() == OpType::Linear && i == 1) continue;
+        if ((n.op_type() == OpType::Linear || n.op_type() == OpType::Embedding) && i == 1)
+          continue;
         if (const Tensor* t = ctx.get(n.inputs()[i]); t && t->data()) other_use.insert(t->data());
       }
   for (const Node& n : graph_->nodes()) {

@@ -1,5 +1,6 @@
-// embedding.hip -- Q8_0 Embedding gather-dequantise for gfx950, and the
-// whole-tensor Q8_0 -> fp32 dequantisation of the weight loader.
+// embedding.hip -- Q8_0 Embedding gather-dequantise for gfx950 (from raw GGUF
+// blocks or from 16-row tiles), and the whole-tensor Q8_0 -> fp32
+// dequantisation of the weight loader.
 //
 // out[s, h] = d * q of element h of table row ids[s]; an id outside [0, vocab)
 // gives a row of +0.0f (device semantics of the reference,
@@ -58,6 +59,42 @@ __global__ __launch_bounds__(256) void embedding_q8_0_kernel(
   __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + s * hidden + h));
 }
 
+// The same gather from a table in Q8_0 16-row tiles (layout of launch.hpp):
+// element h of row n sits in quant piece (n / 16, pair h / 64), slot
+// 16 ((h % 32) / 8) + n % 16, byte 8 ((h / 32) % 2) + h % 8, and its scale in
+// dword n % 16 of the matching scale piece (low half: even block, high half: odd
+// block).  Four consecutive outputs are one aligned dword of quants.  Same value
+// d * q with the same decode, so the output equals the raw gather bit for bit.
+__global__ __launch_bounds__(256) void embedding_q8_0_tiled_kernel(
+    const uint8_t* __restrict__ w, const int32_t* __restrict__ ids,
+    float* __restrict__ out, int64_t total_quads, int quads_per_row, int vocab,
+    int hidden) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= total_quads) return;
+  const int64_t s = g / quads_per_row;
+  const int h = (int)(g - s * quads_per_row) * 4;
+  const int32_t id = ids[s];
+  f32x4 v;
+  if (id < 0 || id >= vocab) {
+    v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  } else {
+    const int64_t KP = (hidden / kBlockElems + 1) / 2;
+    const int64_t G = ((int64_t)vocab + kTileRows - 1) / kTileRows;
+    const int64_t piece = (int64_t)(id / kTileRows) * KP + h / (2 * kBlockElems);
+    const int r = id % kTileRows, e = h % kBlockElems, odd = (h / kBlockElems) & 1;
+    const uint32_t q = *reinterpret_cast<const uint32_t*>(
+        w + piece * kTilePieceBytes + (16 * (e / 8) + r) * 16 + 8 * odd + e % 8);
+    const uint32_t sc = *reinterpret_cast<const uint32_t*>(
+        w + G * KP * kTilePieceBytes + piece * kTileScaleBytes + r * 4);
+    const float d = scale_to_f32(odd ? sc >> 16 : sc & 0xffffu);
+    v.x = d * q_at(q, 0);
+    v.y = d * q_at(q, 1);
+    v.z = d * q_at(q, 2);
+    v.w = d * q_at(q, 3);
+  }
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + s * hidden + h));
+}
+
 __global__ __launch_bounds__(256) void dequantize_q8_0_kernel(const uint8_t* __restrict__ w,
                                                               float* __restrict__ out,
                                                               int64_t n) {
@@ -95,6 +132,17 @@ hipError_t launch_embedding(const uint8_t* w, const int32_t* ids, float* out,
   const int64_t grid = (total + 255) / 256;
   hipLaunchKernelGGL(embedding_q8_0_kernel, dim3((unsigned)grid), dim3(256), 0,
                      stream, w, ids, out, total, quads_per_row, vocab, hidden);
+  return hipGetLastError();
+}
+
+hipError_t launch_embedding_tiled(const uint8_t* w, const int32_t* ids, float* out,
+                                  int64_t seq_len, int vocab, int hidden, hipStream_t stream) {
+  const int quads_per_row = hidden / 4;
+  const int64_t total = seq_len * quads_per_row;
+  if (total == 0) return hipSuccess;
+  const int64_t grid = (total + 255) / 256;
+  hipLaunchKernelGGL(embedding_q8_0_tiled_kernel, dim3((unsigned)grid), dim3(256), 0, stream,
+                     w, ids, out, total, quads_per_row, vocab, hidden);
   return hipGetLastError();
 }
 

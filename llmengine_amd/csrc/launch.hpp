@@ -180,6 +180,11 @@ hipError_t launch_embedding(const uint8_t* w, const int32_t* ids, float* out,
                             int64_t seq_len, int vocab, int hidden,
                             hipStream_t stream);
 
+// The same gather from a [vocab, hidden] table in 16-row tiles (kTiled, 16-byte
+// aligned); bit-identical to launch_embedding on the raw bytes.
+hipError_t launch_embedding_tiled(const uint8_t* w_tiled, const int32_t* ids, float* out,
+                                  int64_t seq_len, int vocab, int hidden, hipStream_t stream);
+
 // dst[e] = q * d over the flat element stream of a Q8_0 tensor of n elements
 // (the weight loader's Float32 branch); dst 16-byte aligned.
 hipError_t launch_dequantize_q8_0(const uint8_t* w, float* out, int64_t n, hipStream_t stream);

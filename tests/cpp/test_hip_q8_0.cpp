@@ -1162,14 +1162,14 @@ static void test_executor_linear_bf16_bias() {
 }
 
 static void test_executor_tiles_in_place() {
-  // tile_weights(ctx, release_raw = true): the Linear-only weights (gate, up,
-  // down, q) are re-tiled in place -- the tensors adopt 16-row tiles and their
-  // raw bytes are freed -- while the table read by both an Embedding and a
-  // Linear (a tied lm_head, bound to two values) keeps its raw bytes and gets a
-  // copy.  Outputs match the raw run (bitwise on the MFMA paths, 1e-6 relative
-  // L2 where the tiled FP32 GEMV runs, M = 1), also from a second executor that
-  // never tiled anything (the registered Linear kernel reads the layout tag),
-  // and an Embedding on an in-place tiled tensor is rejected.
+  // tile_weights(ctx, release_raw = true): every weight here (gate, up, down, q
+  // and the table read by both an Embedding and a Linear -- a tied lm_head,
+  // bound to two values) is re-tiled in place: the tensors adopt 16-row tiles
+  // and their raw bytes are freed.  Outputs match the raw run (bitwise on the
+  // MFMA paths and the embedding, 1e-6 relative L2 where the tiled FP32 GEMV
+  // runs, M = 1), also from a second executor that never tiled anything (the
+  // registered Linear and Embedding kernels read the layout tag), and a MatMul
+  // on an in-place tiled tensor is rejected.
   const int K = 128, I = 96, Q = 64, V = 80, T = 4;
   KernelRegistry registry;
   register_hip_kernels(registry);
@@ -1255,13 +1255,12 @@ static void test_executor_tiles_in_place() {
       const auto ref = outputs();
 
       check_status(ex.tile_weights(ctx, true));
-      CHECK(ex.tiled_in_place() == 4u);
-      CHECK(ex.tiled_weights() == 1u);  // the tied table: a copy, raw bytes kept
-      for (int i = 0; i < 4; ++i) {
+      CHECK(ex.tiled_in_place() == 5u);
+      CHECK(ex.tiled_weights() == 0u);
+      for (int i = 0; i < 5; ++i) {
         CHECK(tw[i]->storage_layout() == StorageLayout::Q8_0Tiled);
         CHECK(tw[i]->allocated_bytes() == hip::q8_0_tiled_bytes(rows[i], cols[i]));
       }
-      CHECK(tw[4]->storage_layout() == StorageLayout::Raw);
       check_status(ex.run(ctx));
       check_hip(hipDeviceSynchronize());
       // fused: gate+up+SwiGLU, q+lm_head, down; unfused: five Linears
@@ -1284,17 +1283,19 @@ static void test_executor_tiles_in_place() {
       same(ref, outputs());
 
       if (fuse == 0 && M == 1) {
-        // Embedding over an in-place tiled tensor is refused.
+        // MatMul over an in-place tiled tensor (read as B [64, 128]) is refused.
         Graph g2;
         GraphBuilder gb2(g2);
-        auto ids2 = gb2.input("ids", Shape({T}), DType::Int32, dev);
-        auto tab2 = gb2.constant("wq", Shape({Q, K}), DType::Float32, dev);
-        CHECK(ids2 && tab2);
-        auto e2 = gb2.embedding(*ids2, *tab2, "embed");
+        auto a2 = gb2.input("a", Shape({2, Q}), DType::Float32, dev);
+        auto b2 = gb2.constant("wq", Shape({Q, K}), DType::Float32, dev);
+        CHECK(a2 && b2);
+        auto e2 = gb2.matmul(*a2, *b2, "mm");
         CHECK(e2 && gb2.output(*e2, "o"));
+        Tensor ta2("a", Shape({2, Q}), DType::Float32, dev);
+        check_status(ta2.allocate_hip());
         RuntimeContext ctx2;
-        check_status(ctx2.bind(*ids2, &tids));
-        check_status(ctx2.bind(*tab2, tw[3].get()));
+        check_status(ctx2.bind(*a2, &ta2));
+        check_status(ctx2.bind(*b2, tw[3].get()));
         check_status(ctx2.allocate_intermediates(g2));
         HipExecutor ex3(std::make_shared<HipBackend>(), registry);
         check_status(ex3.compile(g2));

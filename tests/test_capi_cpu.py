@@ -26,7 +26,7 @@ def declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     lib = capi.load()
-    assert lib.mle_q8_0_abi_version() == 6
+    assert lib.mle_q8_0_abi_version() == 7
     out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH],
                          stdout=subprocess.PIPE, text=True, check=True).stdout
     exported = set(re.findall(r" T (mle_\w+)", out))

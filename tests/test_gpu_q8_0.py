@@ -125,6 +125,66 @@ def test_embedding_special_scales(dev, orc):
     assert_bitexact(to_host(out), orc.embedding(table, ids, 32))
 
 
+def _tiled_table(table, vocab, hidden, dev):
+    import torch
+    dw = to_dev(table, dev)
+    t = torch.empty(capi.tiled_bytes(vocab, hidden), dtype=torch.uint8, device=dev)
+    capi.tile(dw, t, vocab, hidden)
+    return t
+
+
+@pytest.mark.parametrize("vocab,hidden,n", [(1, 32, 1), (3, 96, 7), (257, 64, 100),
+                                            (1000, 896, 513), (77, 4096, 33),
+                                            (151936, 896, 4096)])
+def test_embedding_tiled_table_bitexact(dev, orc, vocab, hidden, n):
+    """The gather from a table in 16-row tiles equals the reference gather bit for
+    bit: ragged vocabularies (rows past the last 16-row group), hidden with an odd
+    number of blocks (96: the pair's second block is padding), out-of-range ids
+    (zero rows), the configs[4] shape."""
+    note(f"embedding tiled vocab={vocab} hidden={hidden} n={n}")
+    w = weight(60 + vocab, vocab, hidden)
+    ids = S.token_ids(61 + n, n, vocab)
+    ids[-1] = vocab - 1
+    if n > 4:
+        ids[1], ids[2] = -1, vocab
+    out = empty_f32((n, hidden), dev)
+    capi.embedding_tiled(_tiled_table(w, vocab, hidden, dev), to_dev(ids, dev), out, n, vocab,
+                         hidden)
+    assert_bitexact(to_host(out), orc.embedding_zero_fill(w, ids, vocab, hidden))
+
+
+def test_embedding_tiled_table_special_scales(dev, orc):
+    """Every binary16 class as a scale through the tiled table (NaN outputs by position)."""
+    specials = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x0400, 0x3C00, 0x7BFF,
+                         0xFBFF, 0x7C00, 0xFC00, 0x7E00, 0x7C01, 0xFE00, 0x13FF, 0x8200,
+                         0x3555, 0x0200], np.uint16)
+    hidden = 64
+    q = S.quants(54, specials.size * hidden)
+    q[::7] = 0
+    table = S.pack_q8_0(q, np.repeat(specials, hidden // 32).view(np.float16))
+    vocab = specials.size
+    ids = np.arange(vocab, dtype=np.int32)[::-1].copy()
+    note("embedding tiled special scales")
+    out = empty_f32((ids.size, hidden), dev)
+    capi.embedding_tiled(_tiled_table(table, vocab, hidden, dev), to_dev(ids, dev), out,
+                         ids.size, vocab, hidden)
+    assert_bitexact(to_host(out), orc.embedding(table, ids, hidden))
+
+
+def test_embedding_tiled_table_errors(dev):
+    import torch
+    w = _tiled_table(weight(55, 16, 64), 16, 64, dev)
+    ids = to_dev(np.zeros(2, np.int32), dev)
+    out = empty_f32((2, 64), dev)
+    code, msg = capi.embedding_tiled_status(w, ids, out, 2, 16, 48)
+    assert code == 4 and "multiple of 32" in msg
+    unaligned = torch.empty(w.numel() + 16, dtype=torch.uint8, device=dev)[8:]
+    code, msg = capi.embedding_tiled_status(unaligned, ids, out, 2, 16, 64)
+    assert code == 1 and "aligned" in msg
+    code, msg = capi.embedding_tiled_status(w, ids, out, -1, 16, 64)
+    assert code == 1
+
+
 def test_embedding_empty_is_noop(dev):
     w = to_dev(weight(54, 4, 32), dev)
     ids = to_dev(np.zeros(1, np.int32), dev)
