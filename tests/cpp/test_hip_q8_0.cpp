@@ -578,6 +578,22 @@ static void test_gguf_model_end_to_end() {
     const double e3 = linear_rel_l2(eo, embd, el, T, V, H);
     std::printf("    T=%d rel L2: up %.2e down %.2e lm_head %.2e (bound %.0e)\n", T, e1, e2, e3, tol);
     CHECK(e1 <= tol && e2 <= tol && e3 <= tol);
+
+    // The loader's tensors re-tiled in place (the tied table too: it is read only
+    // by the Embedding and the lm_head Linear): same bits from every stage.
+    check_status(ex.tile_weights(ctx, true));
+    CHECK(ex.tiled_in_place() == 3u && ex.tiled_weights() == 0u);
+    CHECK(store->get("lm_head.weight")->storage_layout() == StorageLayout::Q8_0Tiled);
+    CHECK(store->get("tok_embeddings.weight")->allocated_bytes() == hip::q8_0_tiled_bytes(V, H));
+    check_status(ex.run(ctx));
+    check_hip(hipDeviceSynchronize());
+    const std::vector<float>* before[4] = {&ex_, &eh, &eo, &el};
+    const ValueId vals[4] = {*x, *h, *o, *logits};
+    const size_t cnt[4] = {size_t(T) * H, size_t(T) * I, size_t(T) * H, size_t(T) * V};
+    for (int i = 0; i < 4; ++i) {
+      const auto after = download(ctx.get(vals[i]), cnt[i]);
+      CHECK(std::memcmp(after.data(), before[i]->data(), cnt[i] * 4) == 0);
+    }
   }
   std::remove(path.c_str());
   std::printf("  PASS test_gguf_model_end_to_end\n");
