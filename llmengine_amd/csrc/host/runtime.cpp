@@ -131,14 +131,16 @@ Status HipExecutor::tile_weights(RuntimeContext& ctx, bool release_raw) {
   // Overwritten weights get fresh copies: drop the old ones first.
   release_tiled_weights();
   in_place_ = 0;
-  // Buffers read other than as a Linear weight or an Embedding table (a MatMul
-  // operand, ...), through any value bound to them, keep their raw bytes.
+  // Buffers read other than as a Linear weight, through any value bound to
+  // them, keep their raw bytes: a MatMul operand cannot be read from tiles, and
+  // an Embedding table (a tied lm_head) gathers twice as fast from raw bytes
+  // (each row's quants share their 16-byte tile slots' cache lines with 15
+  // other rows), which HBM capacity makes the better trade.
   std::unordered_set<const void*> other_use;
   if (release_raw)
     for (const Node& n : graph_->nodes())
       for (size_t i = 0; i < n.inputs().size(); ++i) {
-        if ((n.op_type() == OpType::Linear || n.op_type() == OpType::Embedding) && i == 1)
-          continue;
+        if (n.op_type() == OpType::Linear && i == 1) continue;
         if (const Tensor* t = ctx.get(n.inputs()[i]); t && t->data()) other_use.insert(t->data());
       }
   for (const Node& n : graph_->nodes()) {

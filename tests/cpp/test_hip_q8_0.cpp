@@ -579,12 +579,14 @@ static void test_gguf_model_end_to_end() {
     std::printf("    T=%d rel L2: up %.2e down %.2e lm_head %.2e (bound %.0e)\n", T, e1, e2, e3, tol);
     CHECK(e1 <= tol && e2 <= tol && e3 <= tol);
 
-    // The loader's tensors re-tiled in place (the tied table too: it is read only
-    // by the Embedding and the lm_head Linear): same bits from every stage.
+    // The loader's Linear-only tensors re-tiled in place, the tied table tiled
+    // by copy (its raw bytes stay for the gather): same bits from every stage.
     check_status(ex.tile_weights(ctx, true));
-    CHECK(ex.tiled_in_place() == 3u && ex.tiled_weights() == 0u);
-    CHECK(store->get("lm_head.weight")->storage_layout() == StorageLayout::Q8_0Tiled);
-    CHECK(store->get("tok_embeddings.weight")->allocated_bytes() == hip::q8_0_tiled_bytes(V, H));
+    CHECK(ex.tiled_in_place() == 2u && ex.tiled_weights() == 1u);
+    CHECK(store->get("layer_0.up_proj.weight")->storage_layout() == StorageLayout::Q8_0Tiled);
+    CHECK(store->get("layer_0.up_proj.weight")->allocated_bytes() ==
+          hip::q8_0_tiled_bytes(I, H));
+    CHECK(store->get("lm_head.weight")->storage_layout() == StorageLayout::Raw);
     check_status(ex.run(ctx));
     check_hip(hipDeviceSynchronize());
     const std::vector<float>* before[4] = {&ex_, &eh, &eo, &el};
@@ -1178,14 +1180,15 @@ static void test_executor_linear_bf16_bias() {
 }
 
 static void test_executor_tiles_in_place() {
-  // tile_weights(ctx, release_raw = true): every weight here (gate, up, down, q
-  // and the table read by both an Embedding and a Linear -- a tied lm_head,
-  // bound to two values) is re-tiled in place: the tensors adopt 16-row tiles
-  // and their raw bytes are freed.  Outputs match the raw run (bitwise on the
-  // MFMA paths and the embedding, 1e-6 relative L2 where the tiled FP32 GEMV
-  // runs, M = 1), also from a second executor that never tiled anything (the
-  // registered Linear and Embedding kernels read the layout tag), and a MatMul
-  // on an in-place tiled tensor is rejected.
+  // tile_weights(ctx, release_raw = true): the Linear-only weights (gate, up,
+  // down, q) are re-tiled in place -- the tensors adopt 16-row tiles and their
+  // raw bytes are freed -- while the table read by both an Embedding and a
+  // Linear (a tied lm_head, bound to two values) keeps its raw bytes and gets a
+  // copy.  Outputs match the raw run (bitwise on the MFMA paths and the
+  // embedding, 1e-6 relative L2 where the tiled FP32 GEMV runs, M = 1), also
+  // from a second executor that never tiled anything (the registered Linear
+  // kernel reads the layout tag); an Embedding over an in-place tiled tensor
+  // gives the raw gather's bits, and a MatMul over one is rejected.
   const int K = 128, I = 96, Q = 64, V = 80, T = 4;
   KernelRegistry registry;
   register_hip_kernels(registry);
@@ -1271,12 +1274,13 @@ static void test_executor_tiles_in_place() {
       const auto ref = outputs();
 
       check_status(ex.tile_weights(ctx, true));
-      CHECK(ex.tiled_in_place() == 5u);
-      CHECK(ex.tiled_weights() == 0u);
-      for (int i = 0; i < 5; ++i) {
+      CHECK(ex.tiled_in_place() == 4u);
+      CHECK(ex.tiled_weights() == 1u);  // the tied table: a copy, raw bytes kept
+      for (int i = 0; i < 4; ++i) {
         CHECK(tw[i]->storage_layout() == StorageLayout::Q8_0Tiled);
         CHECK(tw[i]->allocated_bytes() == hip::q8_0_tiled_bytes(rows[i], cols[i]));
       }
+      CHECK(tw[4]->storage_layout() == StorageLayout::Raw);
       check_status(ex.run(ctx));
       check_hip(hipDeviceSynchronize());
       // fused: gate+up+SwiGLU, q+lm_head, down; unfused: five Linears
@@ -1299,6 +1303,35 @@ static void test_executor_tiles_in_place() {
       same(ref, outputs());
 
       if (fuse == 0 && M == 1) {
+        // An Embedding over an in-place tiled tensor (wq read as a [64, 128]
+        // table) gives the bits of the raw gather, computed before tiling.
+        {
+          Graph g3;
+          GraphBuilder gb3(g3);
+          auto ids3 = gb3.input("ids", Shape({T}), DType::Int32, dev);
+          auto tab3 = gb3.constant("wq", Shape({Q, K}), DType::Float32, dev);
+          CHECK(ids3 && tab3);
+          auto e3 = gb3.embedding(*ids3, *tab3, "embed");
+          CHECK(e3 && gb3.output(*e3, "o"));
+          const auto hq = synth_q8(Q, K, 93);
+          std::vector<int> qids{5, 0, 63, 17};
+          upload(tids, qids.data(), qids.size() * 4);
+          RuntimeContext ctx3;
+          check_status(ctx3.bind(*ids3, &tids));
+          check_status(ctx3.bind(*tab3, tw[3].get()));
+          check_status(ctx3.allocate_intermediates(g3));
+          HipExecutor ex4(std::make_shared<HipBackend>(), registry);
+          check_status(ex4.compile(g3));
+          check_status(ex4.run(ctx3));
+          check_hip(hipDeviceSynchronize());
+          const auto got = download(ctx3.get(*e3), size_t(T) * K);
+          for (int t = 0; t < T; ++t)
+            for (int c = 0; c < K; ++c) {
+              const float want = q8_at(hq, K, qids[t], c);
+              CHECK(std::memcmp(&got[size_t(t) * K + c], &want, 4) == 0);
+            }
+          upload(tids, hids.data(), hids.size() * 4);
+        }
         // MatMul over an in-place tiled tensor (read as B [64, 128]) is refused.
         Graph g2;
         GraphBuilder gb2(g2);
