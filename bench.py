@@ -1,10 +1,9 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X Q8_0 path on the BASELINE workload (one JSON line).
+"""Benchmark of the MI355X Q8_0 path on its headline workload (one JSON line).
 
-Metric: "Q8_0 Linear decode GB/s (% HBM peak); prefill TFLOP/s (% MFMA)
-@M=512".
+Metric: "Q8_0 Linear decode GB/s (% HBM peak); prefill TFLOP/s (% MFMA) @M=512".
 
-Workload of one step (the Llama-7B-shaped decode set): for each
+Workload of one step (configs[1], the Llama-7B-shaped decode set): for each
 M in {1, 4, 8}, the five Q8_0 Linears [4096->12288] QKV, [4096->4096] o_proj,
 [4096->11008] gate, [4096->11008] up and [11008->4096] down, each a separate launch
 (15 launches), FP32 activations ~N(0,1), synthetic Q8_0 weights (int8 uniform in
@@ -644,7 +643,7 @@ def main():
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
-        "data": "synthetic (seeded BASELINE distributions; random Q8_0 weights)",
+        "data": "synthetic (seeded benchmark distributions; random Q8_0 weights)",
         "config": {"workload": "configs[1]: Llama-7B decode Q8_0 Linear set, M in {1,4,8} x "
                                "{QKV 4096->12288, o_proj 4096->4096, gate/up 4096->11008, "
                                "down 11008->4096}, 15 launches per step",

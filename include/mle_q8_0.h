@@ -302,7 +302,7 @@ int mle_workspace_plan_growth(size_t cap_bytes, size_t cap_counters, size_t need
  * array per GPU (32 MiB + 65536 counters, held from library load until process
  * exit) instead of the per-stream workspace; nothing is allocated or freed.
  * A shape needing more scratch than that is rejected with Unsupported before
- * any launch (every BASELINE shape fits: prefill [512 x 4096 x 11008] takes
+ * any launch (every benchmark shape fits: prefill [512 x 4096 x 11008] takes
  * 28 MB).  All calls on one GPU share the array: calls that overlap in time on
  * one GPU (different streams, or threads without ordering) race and give wrong
  * results; calls ordered on one stream do not.

@@ -712,7 +712,7 @@ int decode_mfma_tile(int M) {
 }
 
 DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
-  // Measured on MI355X over the BASELINE decode shapes: 16-block K slices
+  // Measured on MI355X over the Llama-7B decode shapes: 16-block K slices
   // (one-shot workgroups of ~35 KB) beat 32 unless K fits one 32-block slice
   // (no split-K hand-off at all); 8 waves per workgroup pay off for 4+ tokens
   // on wide weights (qkv / gate at M = 4: 16.9 / 16.4 us vs 18.4 / 17.6 with 4

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs with the BASELINE value distributions (numpy, portable).
+"""Seeded synthetic inputs with the benchmark's value distributions (numpy, portable).
 
 Every tensor is drawn from a counter-based SplitMix64 stream, so any slice of any tensor
 can be regenerated on any machine without replaying a sequential generator:

@@ -450,7 +450,7 @@ static void test_executor_prefill_linear() {
 }
 
 // Seeded Q8_0 blocks: q uniform in [-127, 127], scale |z| * 0.02 / 127 rounded
-// to binary16 (the BASELINE weight distribution, here from a small LCG).
+// to binary16 (the benchmark's weight distribution, here from a small LCG).
 static std::vector<uint8_t> synth_q8(size_t rows, size_t cols, uint32_t seed) {
   std::vector<uint8_t> out(rows * (cols / 32) * 34);
   uint32_t s = seed;

@@ -28,7 +28,7 @@ import oracle as O  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "q8_0_golden.json")
 
-# (name, M, N, K, seed) for Linear; weights [N,K] with BASELINE distributions.
+# (name, M, N, K, seed) for Linear; weights [N,K] with the benchmark's distributions.
 LINEAR = [
     ("linear_1x64x256", 1, 64, 256, 101),
     ("linear_3x96x4096", 3, 96, 4096, 102),

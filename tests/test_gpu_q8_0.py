@@ -2,7 +2,7 @@
 
 Bars (stated per test): Embedding and MatMul bit-exact; Linear on the FP32 GEMV path
 (M <= 63) relative L2 <= 1e-5; Linear on the bf16-MFMA path (M >= 64) relative L2
-<= 1e-2.  Full BASELINE sizes are covered either directly against the oracle (where it
+<= 1e-2.  The benchmark's full sizes are covered either directly against the oracle (where it
 finishes in seconds) or through size-independent properties (agreement of the two
 Linear paths, determinism, linearity).
 """
