@@ -1,0 +1,78 @@
+"""Linear launches captured in a HIP graph (torch.cuda.CUDAGraph) on a stream whose
+workspace was reserved beforehand (mle_q8_0_workspace_size + mle_workspace_reserve):
+capture allocates and synchronises nothing, and every replay -- with eager launches of
+other shapes on the same stream and host synchronisations between replays -- gives the
+eager results bit for bit.  Shapes: the split-K MFMA decode (M = 8, 22 splits), the
+tiled FP32 GEMV (M = 1) and the bf16 GEMM with its X pre-pass (M = 96).  The kernels
+reset their split-K counters themselves and the workspace counters were cleared by a
+fill kernel at allocation, so no memset node enters the graph.
+"""
+import numpy as np
+import pytest
+
+from helpers import empty_f32, note, rel_l2, to_dev, to_host
+from llmengine_amd import capi
+from llmengine_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+
+def test_linear_graph_replays_match_eager(dev, orc):
+    import torch
+    shapes = [(8, 1024, 11008, False), (1, 512, 4096, True), (96, 384, 1024, False)]
+    stream = torch.cuda.Stream()
+    need_b = need_c = 0
+    cases = []
+    for i, (M, N, K, tiled) in enumerate(shapes):
+        w = S.q8_0_weight(150 + i, N, K)[0]
+        x = S.activations(151 + i, (M, K))
+        dw = to_dev(w, dev)
+        if tiled:
+            t = torch.empty(capi.tiled_bytes(N, K), dtype=torch.uint8, device=dev)
+            capi.tile(dw, t, N, K)
+            dw = t
+        b, c = capi.workspace_size(capi.OP_LINEAR, M, [N], K, tiled)
+        need_b, need_c = max(need_b, b), max(need_c, c)
+        cases.append((M, N, K, tiled, dw, to_dev(x, dev), orc.sgemm_nt(x, w, M, N, K)))
+    # The eager launch made between replays must fit the reservation too: a growth
+    # would free the buffers the graph's kernels hold.
+    b, c = capi.workspace_size(capi.OP_LINEAR, 4, [2048], 4096)
+    need_b, need_c = max(need_b, b), max(need_c, c)
+    capi.workspace_reserve(need_b, need_c, stream=stream)
+    torch.cuda.synchronize()
+    gen0 = capi.workspace_info(stream)[2]
+
+    def run_all(outs):
+        for (M, N, K, tiled, dw, dx, _), y in zip(cases, outs):
+            (capi.linear_tiled if tiled else capi.linear)(dx, dw, None, y, M, N, K,
+                                                          stream=stream)
+
+    eager = [empty_f32((M, N), dev) for (M, N, *_r) in cases]
+    with torch.cuda.stream(stream):
+        run_all(eager)
+    stream.synchronize()
+    for (M, N, K, tiled, _dw, _dx, want), y in zip(cases, eager):
+        assert rel_l2(to_host(y), want) <= (1e-2 if M >= 64 else 1e-5), (M, N, K)
+
+    note("capture Linear launches in a HIP graph")
+    graph_out = [empty_f32((M, N), dev) for (M, N, *_r) in cases]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run_all(graph_out)
+    assert capi.workspace_info(stream)[2] == gen0  # nothing (re)allocated
+
+    other = empty_f32((4, 2048), dev)
+    wo = to_dev(S.q8_0_weight(160, 2048, 4096)[0], dev)
+    xo = to_dev(S.activations(161, (4, 4096)), dev)
+    for rep in range(4):
+        for y in graph_out:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        # eager work of another shape on the same stream between replays
+        capi.linear(xo, wo, None, other, 4, 2048, 4096, stream=stream)
+        torch.cuda.synchronize()
+        assert capi.workspace_info(stream)[2] == gen0
+        for (M, N, *_r), a, b in zip(cases, eager, graph_out):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32)), (rep, M, N)
+    assert capi.workspace_info(stream)[2] == gen0
