@@ -13,13 +13,14 @@
  *     split-K workspace (partial sums + tile counters) per (device, stream).
  *     A caller that must not allocate on its hot path reserves it beforehand
  *     (mle_q8_0_workspace_size + mle_workspace_reserve); otherwise it is
- *     allocated with hipMalloc on first need.  It only grows, each buffer to
- *     max(capacity, need), after a synchronise of that stream, and lives until
- *     process exit.  Nothing else is allocated.  Entry points are re-entrant
- *     and may be called from several host threads, also on one stream (a call
- *     that grows a workspace waits until no other call is still enqueuing
- *     launches on the old buffers); calls writing the same output buffer on
- *     different streams race, as with any kernel.
+ *     allocated with hipMalloc on first need.  It only grows: a buffer too
+ *     small for a call is replaced by one of max(need, 2 x capacity) bytes and
+ *     the old one is kept (launches already enqueued, or captured in a HIP
+ *     graph, still use it), so growth never synchronises; everything lives
+ *     until process exit.  Nothing else is allocated.  Entry points are
+ *     re-entrant and may be called from several host threads, also on one
+ *     stream; calls writing the same output buffer on different streams race,
+ *     as with any kernel.
  *   - Return value: 0 on success, else a value of the reference's ErrorCode
  *     enum (include/minillm/core/status.h:20-32): 1 InvalidArgument,
  *     2 OutOfRange, 3 ShapeMismatch, 4 Unsupported, 6 RuntimeError.  The
@@ -279,8 +280,9 @@ int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const*
  *   number of (re)allocations it has had (0 / 0 / 0 when it has none yet).
  * mle_workspace_plan_growth (test hook): the growth rule, applied to
  *   capacities and a need without allocating: returns 1 and the new capacities
- *   (each max(capacity, need, minimum)) when the need does not fit, else 0 and
- *   the capacities unchanged; -1 for NULL outputs.
+ *   when the need does not fit (a buffer too small takes max(need,
+ *   2 x capacity, minimum), the other keeps its capacity), else 0 and the
+ *   capacities unchanged; -1 for NULL outputs.
  */
 #define MLE_OP_LINEAR 0
 #define MLE_OP_LINEAR_SWIGLU 1

@@ -12,6 +12,7 @@
 #include <climits>
 #include <cstdint>
 #include <map>
+#include <vector>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -93,15 +94,19 @@ int validate_linear(const float* x, const uint8_t* w, const void* bias, float* y
 // stream run in order, so the workspace is never used by two launches at once.
 // It is reserved ahead of the hot path (mle_workspace_reserve, which
 // minillm::HipExecutor calls from compile() and tile_weights() for its graph's
-// largest shapes), or allocated on the first call that needs it; it only ever
-// grows, to max(capacity, need) for each of its two buffers, and lives until
-// the process ends.
+// largest shapes), or allocated on the first call that needs it.  A buffer that
+// must grow is replaced by a new one of at least twice its capacity; the old
+// one is kept (launches already enqueued on the stream, or captured in a HIP
+// graph, may still use it), so growth never synchronises, and the kept buffers
+// add up to less than the live capacity.  Everything lives until the process
+// ends.
 struct StreamWorkspace {
   uint8_t* buf = nullptr;  // partial sums, then scratch
   size_t buf_cap = 0;      // bytes
   uint32_t* counters = nullptr;
   size_t counter_cap = 0;  // uint32 entries
   uint64_t generation = 0;  // (re)allocations so far
+  std::vector<void*> retired;  // replaced buffers, never freed (see above)
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, StreamWorkspace> g_ws;
@@ -109,16 +114,17 @@ std::map<std::pair<int, hipStream_t>, StreamWorkspace> g_ws;
 constexpr size_t kMinWorkspaceBytes = size_t(4) << 20;
 constexpr size_t kMinWorkspaceCounters = 4096;
 
-// Growth rule: capacities never shrink, and a buffer that must grow takes
-// max(capacity, need, minimum).  Returns whether an allocation is needed.
+// Growth rule, per buffer: capacities never shrink, and a buffer too small for
+// the need takes max(need, 2 x capacity, minimum).  Returns whether either
+// buffer must grow.
 bool plan_growth(size_t cap_bytes, size_t cap_counters, size_t need_bytes, size_t need_counters,
                  size_t* new_bytes, size_t* new_counters) {
-  *new_bytes = cap_bytes;
-  *new_counters = cap_counters;
-  if (need_bytes <= cap_bytes && need_counters <= cap_counters) return false;
-  *new_bytes = std::max({cap_bytes, need_bytes, kMinWorkspaceBytes});
-  *new_counters = std::max({cap_counters, need_counters, kMinWorkspaceCounters});
-  return true;
+  *new_bytes = need_bytes > cap_bytes ? std::max({need_bytes, 2 * cap_bytes, kMinWorkspaceBytes})
+                                      : cap_bytes;
+  *new_counters = need_counters > cap_counters
+                      ? std::max({need_counters, 2 * cap_counters, kMinWorkspaceCounters})
+                      : cap_counters;
+  return *new_bytes != cap_bytes || *new_counters != cap_counters;
 }
 
 // Bytes of the workspace buffer a launch needs: partial sums (256-byte
@@ -135,29 +141,24 @@ int ensure_workspace(size_t bytes, size_t counters, hipStream_t stream, StreamWo
   StreamWorkspace& e = g_ws[{dev, stream}];
   size_t nb = 0, nc = 0;
   if (plan_growth(e.buf_cap, e.counter_cap, bytes, counters, &nb, &nc)) {
-    if (e.buf != nullptr || e.counters != nullptr) {
-      // Earlier launches on this stream may still read the old buffers.
-      err = hipStreamSynchronize(stream);
-      if (err != hipSuccess) return check_launch(err, "hip Q8_0 workspace");
-      (void)hipFree(e.buf);
-      (void)hipFree(e.counters);
-      e.buf = nullptr;
-      e.counters = nullptr;
-      e.buf_cap = e.counter_cap = 0;
+    uint8_t* buf = e.buf;
+    uint32_t* cnt = e.counters;
+    if (nb != e.buf_cap) err = hipMalloc(&buf, nb);
+    if (err == hipSuccess && nc != e.counter_cap) {
+      err = hipMalloc(&cnt, nc * sizeof(uint32_t));
+      // Counters start at zero (the kernels leave them at zero); cleared by a
+      // kernel rather than a memset node, so a captured first call replays too.
+      if (err == hipSuccess) err = mle::launch_fill_u32(cnt, nc, 0u, stream);
     }
-    err = hipMalloc(&e.buf, nb);
-    if (err == hipSuccess) err = hipMalloc(&e.counters, nc * sizeof(uint32_t));
-    // Counters start at zero (the kernels leave them at zero); cleared by a
-    // kernel rather than a memset node, so a captured first call replays too.
-    if (err == hipSuccess) err = mle::launch_fill_u32(e.counters, nc, 0u, stream);
     if (err != hipSuccess) {
-      (void)hipFree(e.buf);
-      (void)hipFree(e.counters);
-      e.buf = nullptr;
-      e.counters = nullptr;
-      e.buf_cap = e.counter_cap = 0;
+      if (buf != e.buf) (void)hipFree(buf);
+      if (cnt != e.counters) (void)hipFree(cnt);
       return check_launch(err, "hip Q8_0 workspace allocation failed");
     }
+    if (buf != e.buf && e.buf != nullptr) e.retired.push_back(e.buf);
+    if (cnt != e.counters && e.counters != nullptr) e.retired.push_back(e.counters);
+    e.buf = buf;
+    e.counters = cnt;
     e.buf_cap = nb;
     e.counter_cap = nc;
     ++e.generation;
@@ -167,8 +168,8 @@ int ensure_workspace(size_t bytes, size_t counters, hipStream_t stream, StreamWo
 }
 
 // `hold` keeps the workspace table locked until the caller has enqueued the
-// launch that uses the buffers, so a concurrent call that grows (frees and
-// reallocates) the same stream's workspace cannot free them in between.
+// launch that uses the buffers, so launches from several host threads take the
+// buffers in the order they enqueue.
 int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWorkspace* out,
                   std::unique_lock<std::mutex>* hold) {
   *out = mle::SplitKWorkspace{};

@@ -937,7 +937,7 @@ static void test_workspace_no_regrowth() {
     CHECK(gen == uint64_t(it < 2 ? it + 1 : 2));  // grows on the first a and the first b only
     CHECK(cap_b >= (it == 0 ? ab : bb) && cap_c >= ac);
   }
-  CHECK(cap_b == bb && cap_c == ac);
+  CHECK(cap_b >= bb && cap_c == ac);
   CHECK(y[0]->get() == first);  // deterministic
   for (auto* p : w) delete p;
   for (auto* p : x) delete p;

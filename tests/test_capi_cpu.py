@@ -293,6 +293,10 @@ def test_workspace_growth_rule():
         grows += grow
         caps = (b, c)
     assert grows == 2 and caps == (8 << 20, 50000)
+    # a buffer that must grow at least doubles, so retained old buffers stay bounded
+    assert capi.workspace_plan_growth(8 << 20, MIN_C, 9 << 20, 10) == (True, 16 << 20, MIN_C)
+    assert capi.workspace_plan_growth(8 << 20, MIN_C, 40 << 20, 3 * MIN_C) == (
+        True, 40 << 20, 3 * MIN_C)
 
 
 def test_workspace_size_matches_launch_plan():
