@@ -1,8 +1,8 @@
 """Linear launches captured in a HIP graph (torch.cuda.CUDAGraph) on a stream whose
 workspace was reserved beforehand (mle_q8_0_workspace_size + mle_workspace_reserve):
 capture allocates and synchronises nothing, and every replay -- with eager launches of
-other shapes on the same stream and host synchronisations between replays -- gives the
-eager results bit for bit.  Shapes: the split-K MFMA decode (M = 8, 22 splits), the
+other shapes on the same stream and host synchronisations between replays, and after a
+later call has outgrown the reservation -- gives the eager results bit for bit.  Shapes: the split-K MFMA decode (M = 8, 22 splits), the
 tiled FP32 GEMV (M = 1) and the bf16 GEMM with its X pre-pass (M = 96).  The kernels
 reset their split-K counters themselves and the workspace counters were cleared by a
 fill kernel at allocation, so no memset node enters the graph.
@@ -76,3 +76,25 @@ def test_linear_graph_replays_match_eager(dev, orc):
         for (M, N, *_r), a, b in zip(cases, eager, graph_out):
             assert torch.equal(a.view(torch.int32), b.view(torch.int32)), (rep, M, N)
     assert capi.workspace_info(stream)[2] == gen0
+
+    # A call that outgrows the reservation replaces the workspace buffers but keeps
+    # the old ones, which the graph's kernels still point to: replays stay exact.
+    note("grow the workspace after capture, then replay")
+    Mb, Nb, Kb = 512, 256, 11008
+    xb = S.activations(162, (Mb, Kb))
+    wb = S.q8_0_weight(163, Nb, Kb)[0]
+    yb = empty_f32((Mb, Nb), dev)
+    capi.linear(to_dev(xb, dev), to_dev(wb, dev), None, yb, Mb, Nb, Kb, stream=stream)
+    torch.cuda.synchronize()
+    assert capi.workspace_info(stream)[2] > gen0
+    rows = np.arange(0, Nb, 17)
+    w_rows = np.ascontiguousarray(wb.reshape(Nb, -1)[rows]).reshape(-1)  # rows are contiguous
+    want_b = orc.sgemm_nt(xb, w_rows, Mb, rows.size, Kb)
+    assert rel_l2(to_host(yb)[:, rows], want_b) <= 1e-2
+    for y in graph_out:
+        y.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    for (M, N, *_r), a, b in zip(cases, eager, graph_out):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), ("after growth", M, N)
