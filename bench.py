@@ -310,7 +310,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
-              "supported (no multi-GPU path exists in this round)", file=sys.stderr)
+              "supported (the path has no multi-GPU form; see the sharding design)",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
