@@ -310,7 +310,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
-              "supported (the path has no multi-GPU form; see the sharding design)",
+              "supported (the form sharded over several GPUs is not built)",
               file=sys.stderr)
         sys.exit(2)
 
