@@ -141,6 +141,14 @@ int ensure_workspace(size_t bytes, size_t counters, hipStream_t stream, StreamWo
   StreamWorkspace& e = g_ws[{dev, stream}];
   size_t nb = 0, nc = 0;
   if (plan_growth(e.buf_cap, e.counter_cap, bytes, counters, &nb, &nc)) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+      return fail(MLE_RUNTIME_ERROR,
+                  "hip Q8_0 workspace: this call needs " + std::to_string(bytes) + " bytes and " +
+                      std::to_string(counters) +
+                      " counters, more than the stream's workspace holds, while the stream is "
+                      "capturing a graph; reserve it before capture (mle_q8_0_workspace_size, "
+                      "mle_workspace_reserve)");
     uint8_t* buf = e.buf;
     uint32_t* cnt = e.counters;
     if (nb != e.buf_cap) err = hipMalloc(&buf, nb);

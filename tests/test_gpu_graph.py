@@ -98,3 +98,23 @@ def test_linear_graph_replays_match_eager(dev, orc):
     torch.cuda.synchronize()
     for (M, N, *_r), a, b in zip(cases, eager, graph_out):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32)), ("after growth", M, N)
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_capture_without_reservation_is_refused(dev):
+    """A Linear that would have to allocate its workspace while its stream is capturing
+    returns RuntimeError with a message naming the reservation, instead of calling
+    hipMalloc inside the capture."""
+    import torch
+    M, N, K = 8, 512, 11008
+    dw = to_dev(S.q8_0_weight(170, N, K)[0], dev)
+    dx = to_dev(S.activations(171, (M, K)), dev)
+    y = empty_f32((M, N), dev)
+    stream = torch.cuda.Stream()  # fresh: no workspace yet
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(capi.Q8_0Error) as err:
+        with torch.cuda.graph(g, stream=stream):
+            capi.linear(dx, dw, None, y, M, N, K, stream=stream)
+    assert err.value.code == 6 and "reserve it before capture" in str(err.value)
+    assert capi.workspace_info(stream)[2] == 0
