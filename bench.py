@@ -92,12 +92,21 @@ def tiled_gemv_wins(M, N, K):
     return M == 1 or (M == 2 and N < 65536) or (M <= 4 and K <= 1024 and N <= 32768)
 
 
+def rows_decode_wins(M, N, K):
+    """mle_q8_0_linear_tiled's choice of its row-range MFMA decode (mle::decode_mfma_pick)."""
+    G = (N + 15) // 16
+    return (M in (3, 4) or 6 <= M <= 8) and K % 64 == 0 and 2048 <= K <= 4096 and 512 <= G <= 1024
+
+
 def decode_kernel_name(M, layout="raw", N=4096, K=4096):
     """Kernel the C ABI runs for an M-token Linear (mle_q8_0_linear[_tiled] path choice)."""
     if M == 1 and layout == "raw":
         return "gemv_q8_0_kernel (FP32 GEMV)"
     if layout == "tiled" and tiled_gemv_wins(M, N, K):
         return "gemv_tiled_kernel (FP32 GEMV, tiled weights)"
+    if layout == "tiled" and rows_decode_wins(M, N, K):
+        return ("gemv_mfma_rows_kernel (MFMA decode without split K, exact bf16 activation "
+                "split, tiled weights)")
     if M < 64:
         return ("gemv_q8_0_mfma_kernel (MFMA decode, exact bf16 activation split"
                 + (", tiled weights)" if layout == "tiled" else ")"))

@@ -626,6 +626,264 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   write_out(total);
 }
 
+// Row-range decode (below): K blocks per phase, so that one phase's B fragments
+// fit in LDS next to the scales (MT = 8: 64 x 1552 B; MT = 4: 128 x 1 KB), and
+// 16-row groups per workgroup for G groups on the GPU's 256 CUs.
+template <int MT>
+struct RowsPhase {
+  static constexpr int kBlocks = MT == 8 ? 64 : 128;
+};
+int rows_groups_per_workgroup(int64_t G) { return (int)((G + 255) / 256); }
+
+// Row-range MFMA decode on tiled weights, without split K (2 <= M <= 8, tall
+// weights).  The split-K kernel above needs a hand-off between the workgroups of
+// a row tile (partial stores, their completion, a counter, the read-back), about
+// 3 us at the end of every launch.  Here a workgroup owns whole rows instead:
+// NG 16-row groups (4 waves each) and all of K, so its waves add their sums in
+// LDS and nothing crosses workgroups.  The price is that every workgroup splits
+// all of K's activations; that pays where each workgroup has 2-4 groups to
+// share them (11008 or 12288 outputs over 256 CUs), not for 4096 outputs.
+//
+// K is walked in phases of PHB blocks: the phase's activations are split once
+// into LDS B fragments (same layout and arithmetic as above) shared by every
+// group; wave (group lg, quarter qw) multiplies block pairs
+// [PHB/2 ph + PHB/8 qw, +PHB/8) of its group, 4 pairs (one 16-byte quant slot
+// and one scale dword per lane each) at a time.  Two 4-pair chunks of quant and
+// scale loads are in flight ahead of the chunk being multiplied: issuing a whole
+// share up front stalls a wave on the full request queue before its first
+// multiply (measured 10-15% slower).  Per block and wave the arithmetic is the
+// split-K kernel's (P chained MFMAs, fp32 scale FMA into even/odd accumulators);
+// the 4 waves of a group then add their sums in wave order, so results are
+// deterministic (rel-L2 ~1e-7 from the split-K kernel, which groups the K sum
+// differently).
+template <int MT, int NG, int NPH>
+__global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
+    const float* __restrict__ x, const uint8_t* __restrict__ w, const void* bias, int bias_bf16,
+    float* __restrict__ y, int M, int N, int K) {
+  constexpr int WG = 4;                 // waves per 16-row group
+  constexpr int W = WG * NG;
+  constexpr int NT = 64 * W;
+  constexpr int P = Cols<MT>::P;
+  using C = Cols<MT, 4>;                // half-size last fragment when it fits
+  constexpr int PHB = RowsPhase<MT>::kBlocks;
+  constexpr int PHP = PHB / 2;          // block pairs per phase
+  constexpr int WPP = PHP / WG;         // pairs per wave per phase
+  static_assert(WPP % 4 == 0, "whole 4-pair chunks per wave");
+  constexpr int NCK = WPP / 4;          // chunks per wave per phase
+  constexpr int TC = NPH * NCK;         // chunks per wave
+  constexpr int RING = 2;               // chunks in flight ahead
+  constexpr int BBUF = PHB * C::FB;
+  constexpr int XITEMS = MT * PHB * 4;  // (token, k quarter, block) per phase
+  static_assert(XITEMS % 64 == 0, "activation items fill whole waves");
+  constexpr int XPT = (XITEMS + NT - 1) / NT;
+  constexpr int OUTS = 16 * MT;
+  constexpr int OPL = (OUTS + 63) / 64;
+  static_assert(W * 16 * 17 * 4 <= BBUF, "the group reduction fits the B area");
+  __shared__ __attribute__((aligned(16))) uint8_t bfr[BBUF];
+  __shared__ __attribute__((aligned(16))) float scl[W][8][16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r16 = lane & 15;
+  const int lg = wave / WG, qw = wave % WG;
+  const int KB = K / kBlockElems;
+  const int KP = (KB + 1) >> 1;
+  const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
+  const int64_t rg = (int64_t)blockIdx.x * NG + lg;
+  const bool live_g = rg < G;
+  const int64_t rgc = live_g ? rg : 0;
+
+  // Activations of one phase: item (token m fastest, k quarter, block), 8 fp32.
+  // Items past M or K read zeros through the range check of the per-lane offset.
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)((int64_t)M * K * 4));
+  f32x4 xv[NPH][XPT][2];
+  auto load_x = [&](int ph) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int it = tid + NT * i;
+      const int m = it % MT, q = it / MT;
+      const int kb = ph * PHB + (q >> 2);
+      uint32_t off = it < XITEMS && kb < KB && m < M
+                         ? (uint32_t)((m * K + kb * kBlockElems + 8 * (q & 3)) * 4)
+                         : 0x80000000u;
+      asm volatile("" : "+v"(off));  // the load stays where it is written
+      xv[ph][i][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+      xv[ph][i][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16, 0, 0));
+    }
+  };
+
+  // Quant slots (lane l: rows l % 16, quants 8 (l/16) .. +7 of both blocks of a
+  // pair) and scale dwords (lane l: pair l/16 of the chunk, row l % 16) of this
+  // wave's group; a group past N reads zeros (empty buffer).
+  const uint8_t* qb = w + rgc * KP * kTilePieceBytes;
+  const uint8_t* sb = w + G * KP * kTilePieceBytes + rgc * KP * kTileScaleBytes;
+  const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qb, live_g ? (uint32_t)KP * kTilePieceBytes : 0u);
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, live_g ? (uint32_t)KP * kTileScaleBytes : 0u);
+  u32x4 tq[TC][4];
+  uint32_t ts[TC];
+  auto load_chunk = [&](int cg) {  // chunk cg = ph * NCK + ck
+    const int ph = cg / NCK, ck = cg % NCK;
+    const int p0 = ph * PHP + qw * WPP + 4 * ck;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int pr = p0 + u;
+      uint32_t off = pr < KP ? (uint32_t)pr * kTilePieceBytes + (uint32_t)lane * 16 : 0x80000000u;
+      asm volatile("" : "+v"(off));
+      tq[cg][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0);
+    }
+    const int ps = p0 + g;
+    uint32_t soff = ps < KP ? (uint32_t)ps * kTileScaleBytes + (uint32_t)r16 * 4 : 0x80000000u;
+    asm volatile("" : "+v"(soff));
+    ts[cg] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff, 0, 0);
+  };
+  load_x(0);  // first: the split waits only for these
+#pragma unroll
+  for (int cg = 0; cg < RING && cg < TC; ++cg) load_chunk(cg);
+
+  // Stored virtual columns past 3 MT are never written by the split: zero once.
+  if constexpr (C::HALF) {
+    for (int kb = tid; kb < PHB; kb += NT)
+      *reinterpret_cast<u32x4*>(bfr + kb * C::FB + (P - 1) * 1024 + 512) = u32x4{0u, 0u, 0u, 0u};
+  }
+  if constexpr (C::PADC > 0) {
+    constexpr int PADC = C::PADC;
+    for (int it = tid; it < PHB * 4 * PADC; it += NT) {
+      const int kb = it / (4 * PADC), q = it % (4 * PADC);
+      const int c = q / PADC, vc = 3 * MT + q % PADC;
+      *reinterpret_cast<u32x4*>(bfr + bslot<MT, 4, P>(kb, vc >> 4, c, vc & 15)) =
+          u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  f32x4 accs[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  auto block_mma = [&](int kc, int kb, const bf16x8_t a, f32x4& a4) {
+    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, 4, P>(kb, 0, g, r16)),
+        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+    for (int p = 1; p < P; ++p)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, 4, P>(kb, p, g, r16)), d, 0,
+          0, 0);
+    const f32x4 sc = *reinterpret_cast<const f32x4*>(&scl[wave][kc][4 * g]);
+    a4.x = __builtin_fmaf(sc.x, d.x, a4.x);
+    a4.y = __builtin_fmaf(sc.y, d.y, a4.y);
+    a4.z = __builtin_fmaf(sc.z, d.z, a4.z);
+    a4.w = __builtin_fmaf(sc.w, d.w, a4.w);
+  };
+
+#pragma unroll
+  for (int ph = 0; ph < NPH; ++ph) {
+    if (ph > 0) {
+      // The previous phase's sums are complete before the barrier: otherwise the
+      // compiler defers its scale FMAs past the split below and holds every MFMA
+      // result of the phase in registers (spills).
+      asm volatile("" : "+v"(accs[0]), "+v"(accs[1]));
+      __syncthreads();  // every wave is done with the previous phase's fragments
+    }
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int it = tid + NT * i;
+      if (XITEMS % NT != 0 && it >= XITEMS) continue;  // whole waves
+      const int m = it % MT, q = it / MT;
+      const int kb = q >> 2, c = q & 3;
+      float v[8] = {xv[ph][i][0].x, xv[ph][i][0].y, xv[ph][i][0].z, xv[ph][i][0].w,
+                    xv[ph][i][1].x, xv[ph][i][1].y, xv[ph][i][1].z, xv[ph][i][1].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(v[j]));  // the split stays in its phase
+      bool finite = true;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) finite &= !__builtin_amdgcn_class(v[j], 0x207);  // NaN, +-Inf
+      uint32_t parts[3][4];
+      if (__builtin_expect(finite, 1))
+        split3_finite(v, parts[0], parts[1], parts[2]);
+      else
+        split3_any(v, parts[0], parts[1], parts[2]);
+#pragma unroll
+      for (int part = 0; part < 3; ++part) {
+        const int vc = part * MT + m;
+        *reinterpret_cast<u32x4*>(bfr + bslot<MT, 4, P>(kb, vc >> 4, c, vc & 15)) =
+            u32x4{parts[part][0], parts[part][1], parts[part][2], parts[part][3]};
+      }
+    }
+    __syncthreads();
+    // The next phase's activations go out before its quant pieces, so its split
+    // waits only for pieces this phase has used.
+    if (ph + 1 < NPH) load_x(ph + 1);
+#pragma unroll
+    for (int ck = 0; ck < NCK; ++ck) {
+      const int cg = ph * NCK + ck;
+      scl[wave][2 * g][r16] = scale_to_f32_fast(ts[cg] & 0xffffu);
+      scl[wave][2 * g + 1][r16] = scale_to_f32_fast(ts[cg] >> 16);
+      const int kb0 = 2 * (qw * WPP + 4 * ck);  // first block of the chunk in the phase
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u32x4 q = tq[cg][u];
+        block_mma(2 * u, kb0 + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
+        block_mma(2 * u + 1, kb0 + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
+      }
+      if (cg + RING < TC) load_chunk(cg + RING);
+    }
+  }
+  const f32x4 acc = accs[0] + accs[1];
+
+  // The group's 4 waves add their sums in LDS (the B area is free after the
+  // barrier), then the first wave of the group writes y.
+  __syncthreads();
+  float (*red)[16][17] = reinterpret_cast<float (*)[16][17]>(bfr);
+  red[wave][4 * g + 0][r16] = acc.x;
+  red[wave][4 * g + 1][r16] = acc.y;
+  red[wave][4 * g + 2][r16] = acc.z;
+  red[wave][4 * g + 3][r16] = acc.w;
+  __syncthreads();
+  if (qw != 0 || !live_g) return;
+#pragma unroll
+  for (int o = 0; o < OPL; ++o) {
+    const int idx = lane + 64 * o;  // (token m, row rr), rows fastest
+    const int m = idx >> 4, rr = idx & 15;
+    const int64_t n = rg * 16 + rr;
+    if (idx >= OUTS || m >= M || n >= N) continue;
+    const int c0 = m, c1 = (MT + m) & 15, c2 = (2 * MT + m) & 15;
+    float t = 0.0f;
+#pragma unroll
+    for (int q4 = 0; q4 < WG; ++q4) {
+      const int wv = WG * lg + q4;
+      float s = red[wv][rr][c0];
+      if (c1 != c0) s += red[wv][rr][c1];
+      if (c2 != c0 && c2 != c1) s += red[wv][rr][c2];
+      t = q4 == 0 ? s : t + s;
+    }
+    y[(int64_t)m * N + n] = t + (bias ? bias_at(bias, bias_bf16, n) : 0.0f);
+  }
+}
+
+template <int MT, int NG>
+hipError_t launch_rows_ng(const float* x, const LinearSeg& sg, int M, int K, hipStream_t stream) {
+  const int64_t G = ((int64_t)sg.N + kTileRows - 1) / kTileRows;
+  const dim3 grid((unsigned)((G + NG - 1) / NG));
+  const int nph = (K / kBlockElems + RowsPhase<MT>::kBlocks - 1) / RowsPhase<MT>::kBlocks;
+  if (nph == 1)
+    hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, 1>), grid, dim3(256 * NG), 0, stream, x,
+                       sg.w, sg.bias, sg.bias_bf16, sg.y, M, sg.N, K);
+  else if (nph == 2)
+    hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, 2>), grid, dim3(256 * NG), 0, stream, x,
+                       sg.w, sg.bias, sg.bias_bf16, sg.y, M, sg.N, K);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_rows(const float* x, const LinearSeg& sg, int M, int K, hipStream_t stream) {
+  const int64_t G = ((int64_t)sg.N + kTileRows - 1) / kTileRows;
+  switch (rows_groups_per_workgroup(G)) {
+    case 2: return launch_rows_ng<MT, 2>(x, sg, M, K, stream);
+    case 3: return launch_rows_ng<MT, 3>(x, sg, M, K, stream);
+    case 4: return launch_rows_ng<MT, 4>(x, sg, M, K, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
 struct Grid {
   unsigned tiles, splits;
   DecodeArgs args;
@@ -733,6 +991,15 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
       c.waves = (c.mt >= 16 || (c.mt >= 8 && N >= 65536)) ? 8 : 4;
     else
       c.waves = (c.mt == 8 && N >= 12288) ? 4 : 8;
+    // The row-range kernel where it was measured to win (MI355X, Llama-7B
+    // gate / up / qkv at K = 4096: M = 4 0.85-0.89x, M = 8 0.96-0.99x the
+    // split-K kernel's time): 512-1024 row groups, so that 2-4 of them share
+    // each workgroup's activation split, and K in one or two LDS phases.  With
+    // 4096 outputs (o_proj, down) it loses (1.16-1.31x).
+    const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
+    if ((c.mt == 4 || c.mt == 8) && K % 64 == 0 && K >= 2048 && K <= 4096 && G >= 512 &&
+        G <= 1024)
+      c.rows = 1;
     return c;
   }
   c.waves = (c.mt >= 4 && N >= 8192) ? 8 : 4;
@@ -743,7 +1010,14 @@ SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K) {
   return decode_mfma_workspace_segs(c, single(nullptr, nullptr, nullptr, N), K);
 }
 
+// The launches the row-range kernel takes: one plain output on tiled weights.
+static bool rows_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
+  return c.rows == 1 && s.count == 1 && s.mode == Epilogue::kPlain &&
+         s.layout == WeightLayout::kTiled;
+}
+
 SplitKNeed decode_mfma_workspace_segs(const DecodeMfmaConfig& c, const LinearSegs& s, int K) {
+  if (rows_takes(c, s)) return SplitKNeed{};  // no split K, no workspace
   const Grid gr = grid_of(c, s, K);
   SplitKNeed need;
   need.splits = (int)gr.splits;
@@ -776,6 +1050,12 @@ hipError_t launch_gemv_mfma_segs(const DecodeMfmaConfig& c, const float* x,
     return hipErrorInvalidValue;
   for (int i = 0; i < s.count; ++i)
     if (!decode_mfma_fits(c, M, s.seg[i].N, K) || s.seg[i].N <= 0) return hipErrorInvalidValue;
+  if (rows_takes(c, s)) {
+    if (M > c.mt || K % 64 != 0) return hipErrorInvalidValue;
+    if (c.mt == 4) return launch_rows<4>(x, s.seg[0], M, K, stream);
+    if (c.mt == 8) return launch_rows<8>(x, s.seg[0], M, K, stream);
+    return hipErrorInvalidValue;
+  }
   const Grid gr = grid_of(c, s, K);
   switch (c.mt) {
     case 1: return dispatch_shape<1>(c, gr, s.mode, s.layout, x, M, K, ws, stream);

@@ -26,9 +26,12 @@ hipError_t launch_gemv(const GemvConfig& cfg, const float* x, const uint8_t* w,
 // rows and a K slice of `kslice` blocks; the K slices of a row tile meet in a
 // split-K workspace.
 struct DecodeMfmaConfig {
-  int mt;      // token tile: 1, 2, 4, 5, 8 or 16 (>= M)
-  int waves;   // waves per workgroup: 2, 4 or 8
-  int kslice;  // K blocks per workgroup: 16 or 32 (32 only for mt <= 8)
+  int mt;        // token tile: 1, 2, 4, 5, 8 or 16 (>= M)
+  int waves;     // waves per workgroup: 2, 4 or 8
+  int kslice;    // K blocks per workgroup: 16 or 32 (32 only for mt <= 8)
+  int rows = 0;  // 1: row-range kernel, no split K (tiled single-output Linears,
+                 // mt 4 or 8, see decode_mfma_pick); the fields above then serve
+                 // launches it does not take (multi-output, SwiGLU)
 };
 struct SplitKNeed {
   int splits = 1;             // workgroups along K

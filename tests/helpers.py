@@ -45,6 +45,15 @@ def rel_l2(a, ref) -> float:
     return float(np.linalg.norm(a - ref) / (den if den > 0 else 1.0))
 
 
+def rows_decode(M, N, K):
+    """The C ABI's choice of the row-range MFMA decode for a tiled single-output
+    Linear (mle::decode_mfma_pick): 3-8 tokens, 512-1024 16-row groups, K 2048-4096
+    in steps of 64 (M = 5 keeps the split-K kernel's 5-token tile)."""
+    G = (N + 15) // 16
+    mt = M in (3, 4) or 6 <= M <= 8
+    return mt and K % 64 == 0 and 2048 <= K <= 4096 and 512 <= G <= 1024
+
+
 def assert_bitexact(got, want, what=""):
     got = np.asarray(got, np.float32)
     want = np.asarray(want, np.float32)

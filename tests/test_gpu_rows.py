@@ -1,0 +1,115 @@
+"""GPU parity of the row-range MFMA decode: tiled weights, 3-8 tokens, 512-1024
+16-row groups, K 2048-4096 in steps of 64 (the launches for which
+mle::decode_mfma_pick sets DecodeMfmaConfig::rows).  Each workgroup owns whole
+16-row groups and all of K, so there is no split-K hand-off and no workspace.
+
+Checked against the CPU oracle (reference cpu_kernels.cpp:208-218) at the decode
+bar, relative L2 <= 1e-5; against the raw entry point, which runs the split-K
+MFMA decode, within relative L2 1e-6 with equal non-finite entries (both sum the
+same exact block products, grouped differently over K); repeatable bit for bit;
+and with a zero workspace need reported by the C ABI.  Cases cover 2, 3 and 4
+groups per workgroup, one and two K phases, N not a multiple of 16 (a partial
+last group), K/32 odd within a pair, fp32 and bf16 bias, and Inf / NaN / large
+activations.
+"""
+import functools
+
+import numpy as np
+import pytest
+
+from helpers import assert_bitexact, empty_f32, note, rel_l2, rows_decode, to_dev, to_host
+from llmengine_amd import capi
+from llmengine_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+DECODE_TOL = 1e-5
+
+
+@functools.lru_cache(maxsize=None)
+def weight(seed, rows, cols):
+    return S.q8_0_weight(seed, rows, cols)[0]
+
+
+def tiled_dev(raw_dev, N, K, dev):
+    import torch
+    t = torch.empty(capi.tiled_bytes(N, K), dtype=torch.uint8, device=dev)
+    capi.tile(raw_dev, t, N, K)
+    return t
+
+
+def close_to_raw(got, raw, what):
+    fin = np.isfinite(raw)
+    assert np.array_equal(np.isfinite(got), fin), what
+    assert_bitexact(got[~fin], raw[~fin], what + " (non-finite)")
+    assert rel_l2(got[fin], raw[fin]) <= 1e-6, what
+
+
+# (M, N, K, bias): groups per workgroup 2 (G = 512), 3 (G = 513, 688, 768) and
+# 4 (G = 1024); MT 4 (one K phase) and MT 8 (two phases; K = 3072 and 2112 leave
+# the second phase part empty, K = 2112 ends on an odd block of a pair).
+CASES = [(3, 8192, 2048, None), (4, 11008, 4096, "f32"), (4, 16384, 4096, None),
+         (4, 8200, 2112, "bf16"), (6, 8200, 2112, None), (7, 12288, 4096, "bf16"),
+         (8, 11008, 4096, None), (8, 16384, 3072, "f32"), (8, 8192, 4096, None)]
+
+
+@pytest.mark.parametrize("M,N,K,bias", CASES)
+def test_rows_decode_matches_oracle_and_split_k(dev, orc, M, N, K, bias):
+    import torch
+    assert rows_decode(M, N, K)
+    note(f"rows decode M={M} N={N} K={K} bias={bias}")
+    raw = weight(N + K, N, K)
+    x = S.activations(K + 5 * M, (M, K))
+    b32 = S.activations(N + 2, (N,), tag=S.TAG_BIAS) if bias else None
+    dx, dw = to_dev(x, dev), to_dev(raw, dev)
+    dt = tiled_dev(dw, N, K, dev)
+    y_t, y_t2, y_raw = (empty_f32((M, N), dev) for _ in range(3))
+    if bias == "bf16":
+        b16 = torch.from_numpy(b32).to(dev).to(torch.bfloat16)
+        b32 = b16.float().cpu().numpy()  # the widened bias the oracle adds
+        capi.linear_bias_bf16(dx, dt, b16, y_t, M, N, K, tiled=True)
+        capi.linear_bias_bf16(dx, dt, b16, y_t2, M, N, K, tiled=True)
+        capi.linear_bias_bf16(dx, dw, b16, y_raw, M, N, K)
+    else:
+        db = to_dev(b32, dev) if bias else None
+        capi.linear_tiled(dx, dt, db, y_t, M, N, K)
+        capi.linear_tiled(dx, dt, db, y_t2, M, N, K)
+        capi.linear(dx, dw, db, y_raw, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(y_t, y_t2)  # deterministic
+    got = to_host(y_t)
+    close_to_raw(got, to_host(y_raw), "rows vs split-K")
+    rows = np.array(sorted({0, 1, N // 2, N - 17, N - 1}))
+    w_rows = np.ascontiguousarray(raw.reshape(N, -1)[rows]).reshape(-1)
+    want = orc.linear(x, w_rows, b32[rows] if bias else None, M, rows.size, K)
+    assert rel_l2(got[:, rows], want) <= DECODE_TOL
+    if M * N * K <= 8 * 8192 * 2048:  # the whole output on the smaller shapes
+        assert rel_l2(got, orc.linear(x, raw, b32, M, N, K)) <= DECODE_TOL
+    assert capi.workspace_size(capi.OP_LINEAR, M, [N], K, True) == (0, 0)
+
+
+def test_rows_decode_special_values(dev):
+    """Inf, NaN, zero rows and large finite activations: the same non-finite
+    entries as the split-K kernel on raw weights, the finite ones within 1e-6."""
+    M, N, K = 8, 8192, 2048
+    assert rows_decode(M, N, K)
+    raw = weight(91, N, K)
+    x = S.activations(92, (M, K))
+    x[1, 5] = np.inf
+    x[2, 100] = -np.inf
+    x[3, 7] = np.nan
+    x[4, :] = 0.0
+    x[5, 3] = 1.0e30
+    x[6, 1500] = np.inf
+    x[6, 1501] = -np.inf
+    note("rows decode special values")
+    dx, dw = to_dev(x, dev), to_dev(raw, dev)
+    dt = tiled_dev(dw, N, K, dev)
+    y_raw, y_t = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    capi.linear(dx, dw, None, y_raw, M, N, K)
+    capi.linear_tiled(dx, dt, None, y_t, M, N, K)
+    got, want = to_host(y_t), to_host(y_raw)
+    assert np.isnan(got[3]).all()
+    assert (got[4] == 0).all()
+    assert not np.isfinite(got[[1, 2, 6]]).any()
+    close_to_raw(got, want, "special values")
