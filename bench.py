@@ -95,7 +95,10 @@ def tiled_gemv_wins(M, N, K):
 def rows_decode_wins(M, N, K):
     """mle_q8_0_linear_tiled's choice of its row-range MFMA decode (mle::decode_mfma_pick)."""
     G = (N + 15) // 16
-    return (M in (3, 4) or 6 <= M <= 8) and K % 64 == 0 and 2048 <= K <= 4096 and 512 <= G <= 1024
+    if K % 64 != 0 or not 2048 <= K <= 4096:
+        return False
+    four = M in (3, 4)
+    return ((four or 6 <= M <= 8) and 512 <= G <= 1024) or (four and 240 <= G <= 256)
 
 
 def decode_kernel_name(M, layout="raw", N=4096, K=4096):

@@ -626,52 +626,47 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   write_out(total);
 }
 
-// Row-range decode (below): K blocks per phase, so that one phase's B fragments
-// fit in LDS next to the scales (MT = 8: 64 x 1552 B; MT = 4: 128 x 1 KB), and
-// 16-row groups per workgroup for G groups on the GPU's 256 CUs.
-template <int MT>
-struct RowsPhase {
-  static constexpr int kBlocks = MT == 8 ? 64 : 128;
-};
+// Row-range decode (below): 16-row groups per workgroup for G groups on the
+// GPU's 256 CUs.
 int rows_groups_per_workgroup(int64_t G) { return (int)((G + 255) / 256); }
 
-// Row-range MFMA decode on tiled weights, without split K (2 <= M <= 8, tall
-// weights).  The split-K kernel above needs a hand-off between the workgroups of
-// a row tile (partial stores, their completion, a counter, the read-back), about
-// 3 us at the end of every launch.  Here a workgroup owns whole rows instead:
-// NG 16-row groups (4 waves each) and all of K, so its waves add their sums in
-// LDS and nothing crosses workgroups.  The price is that every workgroup splits
-// all of K's activations; that pays where each workgroup has 2-4 groups to
-// share them (11008 or 12288 outputs over 256 CUs), not for 4096 outputs.
+// Row-range MFMA decode on tiled weights, without split K (3-8 tokens).  The
+// split-K kernel above needs a hand-off between the workgroups of a row tile
+// (partial stores, their completion, a counter, the read-back), about 3 us at
+// the end of every launch.  Here a workgroup owns whole rows instead: NG 16-row
+// groups of WG waves each and all of K, so its waves add their sums in LDS and
+// nothing crosses workgroups.  The price is that every workgroup splits all of
+// K's activations: that pays where 2-4 groups share each workgroup's split
+// (11008 or 12288 outputs over 256 CUs), or for 4096 outputs at 4 tokens with 16
+// waves on the one group (o_proj); not for K = 11008 (down).
 //
-// K is walked in phases of PHB blocks: the phase's activations are split once
-// into LDS B fragments (same layout and arithmetic as above) shared by every
-// group; wave (group lg, quarter qw) multiplies block pairs
-// [PHB/2 ph + PHB/8 qw, +PHB/8) of its group, 4 pairs (one 16-byte quant slot
-// and one scale dword per lane each) at a time.  Two 4-pair chunks of quant and
-// scale loads are in flight ahead of the chunk being multiplied: issuing a whole
-// share up front stalls a wave on the full request queue before its first
-// multiply (measured 10-15% slower).  Per block and wave the arithmetic is the
-// split-K kernel's (P chained MFMAs, fp32 scale FMA into even/odd accumulators);
-// the 4 waves of a group then add their sums in wave order, so results are
-// deterministic (rel-L2 ~1e-7 from the split-K kernel, which groups the K sum
-// differently).
-template <int MT, int NG, int NPH>
-__global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
+// K is walked in phases of PHB blocks: a phase's activations are split once into
+// LDS B fragments (the layout and arithmetic of the kernel above) shared by every
+// group; wave (group lg, index qw) multiplies block pairs
+// [PHB/2 ph + PHB/(2 WG) qw, + PHB/(2 WG)) of its group, 4 pairs (one 16-byte
+// quant slot and one scale dword per lane each) at a time.  RING 4-pair chunks of
+// loads are in flight ahead of the chunk being multiplied: issuing a whole share
+// up front stalls a wave on the full request queue before its first multiply
+// (10-15% slower), and deeper rings measured slower too.  With NBUF = 2 the
+// fragments of phase ph + 1 are split into the second buffer while phase ph is
+// multiplied (one barrier per phase); with NBUF = 1 the split waits for the
+// phase before it.  Per block and wave the arithmetic is the split-K kernel's
+// (P chained MFMAs, fp32 scale FMA into even/odd accumulators); the WG waves of
+// a group then add their sums in wave order, so results are deterministic
+// (rel-L2 ~1e-7 from the split-K kernel, which groups the K sum differently).
+template <int MT, int NG, int NPH, int PHB, int NBUF, int RING, int WG>
+__global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const void* bias, int bias_bf16,
     float* __restrict__ y, int M, int N, int K) {
-  constexpr int WG = 4;                 // waves per 16-row group
   constexpr int W = WG * NG;
   constexpr int NT = 64 * W;
   constexpr int P = Cols<MT>::P;
   using C = Cols<MT, 4>;                // half-size last fragment when it fits
-  constexpr int PHB = RowsPhase<MT>::kBlocks;
   constexpr int PHP = PHB / 2;          // block pairs per phase
   constexpr int WPP = PHP / WG;         // pairs per wave per phase
   static_assert(WPP % 4 == 0, "whole 4-pair chunks per wave");
   constexpr int NCK = WPP / 4;          // chunks per wave per phase
   constexpr int TC = NPH * NCK;         // chunks per wave
-  constexpr int RING = 2;               // chunks in flight ahead
   constexpr int BBUF = PHB * C::FB;
   constexpr int XITEMS = MT * PHB * 4;  // (token, k quarter, block) per phase
   static_assert(XITEMS % 64 == 0, "activation items fill whole waves");
@@ -679,7 +674,7 @@ __global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
   constexpr int OUTS = 16 * MT;
   constexpr int OPL = (OUTS + 63) / 64;
   static_assert(W * 16 * 17 * 4 <= BBUF, "the group reduction fits the B area");
-  __shared__ __attribute__((aligned(16))) uint8_t bfr[BBUF];
+  __shared__ __attribute__((aligned(16))) uint8_t bfr[NBUF * BBUF];
   __shared__ __attribute__((aligned(16))) float scl[W][8][16];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -737,17 +732,20 @@ __global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
     ts[cg] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff, 0, 0);
   };
   load_x(0);  // first: the split waits only for these
+  if constexpr (NBUF == 2) {
+    if (NPH > 1) load_x(1);
+  }
 #pragma unroll
   for (int cg = 0; cg < RING && cg < TC; ++cg) load_chunk(cg);
 
   // Stored virtual columns past 3 MT are never written by the split: zero once.
   if constexpr (C::HALF) {
-    for (int kb = tid; kb < PHB; kb += NT)
+    for (int kb = tid; kb < NBUF * PHB; kb += NT)
       *reinterpret_cast<u32x4*>(bfr + kb * C::FB + (P - 1) * 1024 + 512) = u32x4{0u, 0u, 0u, 0u};
   }
   if constexpr (C::PADC > 0) {
     constexpr int PADC = C::PADC;
-    for (int it = tid; it < PHB * 4 * PADC; it += NT) {
+    for (int it = tid; it < NBUF * PHB * 4 * PADC; it += NT) {
       const int kb = it / (4 * PADC), q = it % (4 * PADC);
       const int c = q / PADC, vc = 3 * MT + q % PADC;
       *reinterpret_cast<u32x4*>(bfr + bslot<MT, 4, P>(kb, vc >> 4, c, vc & 15)) =
@@ -756,14 +754,14 @@ __global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
   }
 
   f32x4 accs[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  auto block_mma = [&](int kc, int kb, const bf16x8_t a, f32x4& a4) {
+  auto block_mma = [&](const uint8_t* bb, int kc, int kb, const bf16x8_t a, f32x4& a4) {
     f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-        a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, 4, P>(kb, 0, g, r16)),
+        a, *reinterpret_cast<const bf16x8_t*>(bb + bslot_rd<MT, 4, P>(kb, 0, g, r16)),
         f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
     for (int p = 1; p < P; ++p)
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, 4, P>(kb, p, g, r16)), d, 0,
+          a, *reinterpret_cast<const bf16x8_t*>(bb + bslot_rd<MT, 4, P>(kb, p, g, r16)), d, 0,
           0, 0);
     const f32x4 sc = *reinterpret_cast<const f32x4*>(&scl[wave][kc][4 * g]);
     a4.x = __builtin_fmaf(sc.x, d.x, a4.x);
@@ -772,15 +770,8 @@ __global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
     a4.w = __builtin_fmaf(sc.w, d.w, a4.w);
   };
 
-#pragma unroll
-  for (int ph = 0; ph < NPH; ++ph) {
-    if (ph > 0) {
-      // The previous phase's sums are complete before the barrier: otherwise the
-      // compiler defers its scale FMAs past the split below and holds every MFMA
-      // result of the phase in registers (spills).
-      asm volatile("" : "+v"(accs[0]), "+v"(accs[1]));
-      __syncthreads();  // every wave is done with the previous phase's fragments
-    }
+  auto split_phase = [&](int ph) {
+    uint8_t* bb = bfr + (ph % NBUF) * BBUF;
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int it = tid + NT * i;
@@ -793,7 +784,7 @@ __global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
       for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(v[j]));  // the split stays in its phase
       bool finite = true;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) finite &= !__builtin_amdgcn_class(v[j], 0x207);  // NaN, +-Inf
+      for (int j = 0; j < 8; ++j) finite &= !__builtin_amdgcn_class(v[j], 0x207);
       uint32_t parts[3][4];
       if (__builtin_expect(finite, 1))
         split3_finite(v, parts[0], parts[1], parts[2]);
@@ -802,32 +793,60 @@ __global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
 #pragma unroll
       for (int part = 0; part < 3; ++part) {
         const int vc = part * MT + m;
-        *reinterpret_cast<u32x4*>(bfr + bslot<MT, 4, P>(kb, vc >> 4, c, vc & 15)) =
+        *reinterpret_cast<u32x4*>(bb + bslot<MT, 4, P>(kb, vc >> 4, c, vc & 15)) =
             u32x4{parts[part][0], parts[part][1], parts[part][2], parts[part][3]};
       }
     }
-    __syncthreads();
-    // The next phase's activations go out before its quant pieces, so its split
-    // waits only for pieces this phase has used.
-    if (ph + 1 < NPH) load_x(ph + 1);
+  };
+  auto compute_phase = [&](int ph) {
+    const uint8_t* bb = bfr + (ph % NBUF) * BBUF;
 #pragma unroll
     for (int ck = 0; ck < NCK; ++ck) {
       const int cg = ph * NCK + ck;
       scl[wave][2 * g][r16] = scale_to_f32_fast(ts[cg] & 0xffffu);
       scl[wave][2 * g + 1][r16] = scale_to_f32_fast(ts[cg] >> 16);
-      const int kb0 = 2 * (qw * WPP + 4 * ck);  // first block of the chunk in the phase
+      const int kb0 = 2 * (qw * WPP + 4 * ck);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const u32x4 q = tq[cg][u];
-        block_mma(2 * u, kb0 + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
-        block_mma(2 * u + 1, kb0 + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
+        block_mma(bb, 2 * u, kb0 + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
+        block_mma(bb, 2 * u + 1, kb0 + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
       }
       if (cg + RING < TC) load_chunk(cg + RING);
+    }
+  };
+  if constexpr (NBUF == 1) {
+#pragma unroll
+    for (int ph = 0; ph < NPH; ++ph) {
+      if (ph > 0) {
+        // The previous phase's sums are complete before the barrier: otherwise the
+        // compiler defers its scale FMAs past the split and holds every MFMA
+        // result of the phase in registers (spills).
+        asm volatile("" : "+v"(accs[0]), "+v"(accs[1]));
+        __syncthreads();  // every wave is done with the phase's fragments
+      }
+      split_phase(ph);
+      __syncthreads();
+      if (ph + 1 < NPH) load_x(ph + 1);
+      compute_phase(ph);
+    }
+  } else {
+    split_phase(0);
+    __syncthreads();
+#pragma unroll
+    for (int ph = 0; ph < NPH; ++ph) {
+      if (ph + 1 < NPH) split_phase(ph + 1);  // the other buffer: last read in phase ph - 1
+      if (ph + 2 < NPH) load_x(ph + 2);
+      compute_phase(ph);
+      if (ph + 1 < NPH) {
+        asm volatile("" : "+v"(accs[0]), "+v"(accs[1]));  // as above
+        __syncthreads();  // phase ph + 1 split, phase ph fragments no longer read
+      }
     }
   }
   const f32x4 acc = accs[0] + accs[1];
 
-  // The group's 4 waves add their sums in LDS (the B area is free after the
+  // The group's WG waves add their sums in LDS (the B area is free after the
   // barrier), then the first wave of the group writes y.
   __syncthreads();
   float (*red)[16][17] = reinterpret_cast<float (*)[16][17]>(bfr);
@@ -857,29 +876,48 @@ __global__ __launch_bounds__(256 * NG) void gemv_mfma_rows_kernel(
   }
 }
 
-template <int MT, int NG>
-hipError_t launch_rows_ng(const float* x, const LinearSeg& sg, int M, int K, hipStream_t stream) {
+// Launch shapes of the row-range decode (MI355X, Llama-7B shapes at K = 4096):
+//  * 4 tokens, 512-1024 groups: NG = ceil(G / 256) groups of 4 waves, K in one
+//    128-block phase (128 KB of fragments), 2 chunks in flight;
+//  * 4 tokens, 240-256 groups (o_proj): one group of 16 waves per workgroup;
+//  * 8 tokens, 512-1024 groups: 4 waves per group, 32-block phases in two
+//    buffers (2 x 50 KB), 1 chunk in flight (0.95-0.97x the 64-block single
+//    buffer with 2 chunks).
+template <int MT, int NG, int WG, int PHB, int NBUF, int RING>
+hipError_t launch_rows_k(const float* x, const LinearSeg& sg, int M, int K, hipStream_t stream) {
   const int64_t G = ((int64_t)sg.N + kTileRows - 1) / kTileRows;
-  const dim3 grid((unsigned)((G + NG - 1) / NG));
-  const int nph = (K / kBlockElems + RowsPhase<MT>::kBlocks - 1) / RowsPhase<MT>::kBlocks;
-  if (nph == 1)
-    hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, 1>), grid, dim3(256 * NG), 0, stream, x,
-                       sg.w, sg.bias, sg.bias_bf16, sg.y, M, sg.N, K);
-  else if (nph == 2)
-    hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, 2>), grid, dim3(256 * NG), 0, stream, x,
-                       sg.w, sg.bias, sg.bias_bf16, sg.y, M, sg.N, K);
-  else
-    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((G + NG - 1) / NG)), block(64 * WG * NG);
+  const int nph = (K / kBlockElems + PHB - 1) / PHB;
+#define MLE_ROWS(NPH)                                                                        \
+  hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, NPH, PHB, NBUF, RING, WG>), grid, block, \
+                     0, stream, x, sg.w, sg.bias, sg.bias_bf16, sg.y, M, sg.N, K)
+  switch (nph) {
+    case 1: MLE_ROWS(1); break;
+    case 2: if constexpr (PHB < 128) MLE_ROWS(2); else return hipErrorInvalidValue; break;
+    case 3: if constexpr (PHB < 64) MLE_ROWS(3); else return hipErrorInvalidValue; break;
+    case 4: if constexpr (PHB < 64) MLE_ROWS(4); else return hipErrorInvalidValue; break;
+    default: return hipErrorInvalidValue;
+  }
+#undef MLE_ROWS
   return hipGetLastError();
 }
 
 template <int MT>
 hipError_t launch_rows(const float* x, const LinearSeg& sg, int M, int K, hipStream_t stream) {
   const int64_t G = ((int64_t)sg.N + kTileRows - 1) / kTileRows;
-  switch (rows_groups_per_workgroup(G)) {
-    case 2: return launch_rows_ng<MT, 2>(x, sg, M, K, stream);
-    case 3: return launch_rows_ng<MT, 3>(x, sg, M, K, stream);
-    case 4: return launch_rows_ng<MT, 4>(x, sg, M, K, stream);
+  if constexpr (MT == 4) {
+    switch (rows_groups_per_workgroup(G)) {
+      case 1: return launch_rows_k<4, 1, 16, 128, 1, 1>(x, sg, M, K, stream);
+      case 2: return launch_rows_k<4, 2, 4, 128, 1, 2>(x, sg, M, K, stream);
+      case 3: return launch_rows_k<4, 3, 4, 128, 1, 2>(x, sg, M, K, stream);
+      case 4: return launch_rows_k<4, 4, 4, 128, 1, 2>(x, sg, M, K, stream);
+    }
+  } else {
+    switch (rows_groups_per_workgroup(G)) {
+      case 2: return launch_rows_k<8, 2, 4, 32, 2, 1>(x, sg, M, K, stream);
+      case 3: return launch_rows_k<8, 3, 4, 32, 2, 1>(x, sg, M, K, stream);
+      case 4: return launch_rows_k<8, 4, 4, 32, 2, 1>(x, sg, M, K, stream);
+    }
   }
   return hipErrorInvalidValue;
 }
@@ -992,14 +1030,15 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
     else
       c.waves = (c.mt == 8 && N >= 12288) ? 4 : 8;
     // The row-range kernel where it was measured to win (MI355X, Llama-7B
-    // gate / up / qkv at K = 4096: M = 4 0.85-0.89x, M = 8 0.96-0.99x the
-    // split-K kernel's time): 512-1024 row groups, so that 2-4 of them share
-    // each workgroup's activation split, and K in one or two LDS phases.  With
-    // 4096 outputs (o_proj, down) it loses (1.16-1.31x).
+    // shapes at K = 4096, time against the split-K kernel): gate / up / qkv
+    // (512-1024 row groups, 2-4 per workgroup sharing its activation split) at
+    // M = 4 0.83-0.86x and M = 8 0.91-0.93x; o_proj (256 groups, one per
+    // workgroup) at M = 4 0.91x.  o_proj at M = 8 (1.06x) and down (K = 11008:
+    // 1.07x at M = 4, 1.35x at M = 8) keep the split-K kernel.
     const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
-    if ((c.mt == 4 || c.mt == 8) && K % 64 == 0 && K >= 2048 && K <= 4096 && G >= 512 &&
-        G <= 1024)
-      c.rows = 1;
+    const bool k_ok = K % 64 == 0 && K >= 2048 && K <= 4096;
+    if (k_ok && (c.mt == 4 || c.mt == 8) && G >= 512 && G <= 1024) c.rows = 1;
+    if (k_ok && c.mt == 4 && G >= 240 && G <= 256) c.rows = 1;
     return c;
   }
   c.waves = (c.mt >= 4 && N >= 8192) ? 8 : 4;

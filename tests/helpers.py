@@ -47,11 +47,14 @@ def rel_l2(a, ref) -> float:
 
 def rows_decode(M, N, K):
     """The C ABI's choice of the row-range MFMA decode for a tiled single-output
-    Linear (mle::decode_mfma_pick): 3-8 tokens, 512-1024 16-row groups, K 2048-4096
-    in steps of 64 (M = 5 keeps the split-K kernel's 5-token tile)."""
+    Linear (mle::decode_mfma_pick): K 2048-4096 in steps of 64, and 3-8 tokens on
+    512-1024 16-row groups or 3-4 tokens on 240-256 groups (M = 5 keeps the
+    split-K kernel's 5-token tile)."""
     G = (N + 15) // 16
-    mt = M in (3, 4) or 6 <= M <= 8
-    return mt and K % 64 == 0 and 2048 <= K <= 4096 and 512 <= G <= 1024
+    if K % 64 != 0 or not 2048 <= K <= 4096:
+        return False
+    four = M in (3, 4)
+    return ((four or 6 <= M <= 8) and 512 <= G <= 1024) or (four and 240 <= G <= 256)
 
 
 def assert_bitexact(got, want, what=""):

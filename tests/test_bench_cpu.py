@@ -46,4 +46,6 @@ def test_kernel_names_follow_the_path_choice():
     assert "gemv_mfma_rows_kernel" in bench.decode_kernel_name(4, "tiled", 11008, 4096)
     assert "gemv_q8_0_mfma_kernel" in bench.decode_kernel_name(5, "tiled", 11008, 4096)
     assert "gemv_q8_0_mfma_kernel" in bench.decode_kernel_name(8, "raw", 12288, 4096)
+    assert "gemv_mfma_rows_kernel" in bench.decode_kernel_name(4, "tiled", 4096, 4096)
+    assert "gemv_q8_0_mfma_kernel" in bench.decode_kernel_name(8, "tiled", 4096, 4096)
     assert "GEMM" in bench.decode_kernel_name(512, "tiled")

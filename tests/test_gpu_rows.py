@@ -1,16 +1,16 @@
-"""GPU parity of the row-range MFMA decode: tiled weights, 3-8 tokens, 512-1024
-16-row groups, K 2048-4096 in steps of 64 (the launches for which
-mle::decode_mfma_pick sets DecodeMfmaConfig::rows).  Each workgroup owns whole
+"""GPU parity of the row-range MFMA decode: tiled weights, K 2048-4096 in steps of
+64, 3-8 tokens on 512-1024 16-row groups or 3-4 tokens on 240-256 groups (the
+launches for which mle::decode_mfma_pick sets DecodeMfmaConfig::rows).  Each workgroup owns whole
 16-row groups and all of K, so there is no split-K hand-off and no workspace.
 
 Checked against the CPU oracle (reference cpu_kernels.cpp:208-218) at the decode
 bar, relative L2 <= 1e-5; against the raw entry point, which runs the split-K
 MFMA decode, within relative L2 1e-6 with equal non-finite entries (both sum the
 same exact block products, grouped differently over K); repeatable bit for bit;
-and with a zero workspace need reported by the C ABI.  Cases cover 2, 3 and 4
-groups per workgroup, one and two K phases, N not a multiple of 16 (a partial
-last group), K/32 odd within a pair, fp32 and bf16 bias, and Inf / NaN / large
-activations.
+and with a zero workspace need reported by the C ABI.  Cases cover 1 to 4
+groups per workgroup, one to four K phases (single and double buffered), N not
+a multiple of 16 (a partial last group), K/32 odd within a pair, fp32 and bf16
+bias, and Inf / NaN / large activations.
 """
 import functools
 
@@ -45,12 +45,15 @@ def close_to_raw(got, raw, what):
     assert rel_l2(got[fin], raw[fin]) <= 1e-6, what
 
 
-# (M, N, K, bias): groups per workgroup 2 (G = 512), 3 (G = 513, 688, 768) and
-# 4 (G = 1024); MT 4 (one K phase) and MT 8 (two phases; K = 3072 and 2112 leave
-# the second phase part empty, K = 2112 ends on an odd block of a pair).
+# (M, N, K, bias): groups per workgroup 1 (G = 240-256, 16 waves on the group),
+# 2 (G = 512), 3 (G = 513, 688, 768) and 4 (G = 1024); MT 4 (K in one phase) and
+# MT 8 (32-block phases in two buffers: 2, 3 and 4 phases; K = 2112 leaves the
+# last phase with two blocks, one pair).
 CASES = [(3, 8192, 2048, None), (4, 11008, 4096, "f32"), (4, 16384, 4096, None),
-         (4, 8200, 2112, "bf16"), (6, 8200, 2112, None), (7, 12288, 4096, "bf16"),
-         (8, 11008, 4096, None), (8, 16384, 3072, "f32"), (8, 8192, 4096, None)]
+         (4, 8200, 2112, "bf16"), (4, 4096, 4096, None), (3, 3900, 3072, "f32"),
+         (4, 3840, 2048, None), (6, 8200, 2112, None), (7, 12288, 4096, "bf16"),
+         (8, 11008, 4096, None), (8, 16384, 3072, "f32"), (8, 8192, 4096, None),
+         (8, 8192, 2048, None)]
 
 
 @pytest.mark.parametrize("M,N,K,bias", CASES)

@@ -240,7 +240,8 @@ def test_multi_tiled(dev, orc, M):
 def test_llama_decode_set_tiled(dev, M):
     """The four Llama-7B projection shapes of the decode benchmark, tiled against
     raw on the fused qkv, the fused gate/up and o_proj / down: bit for bit on the
-    MFMA decode (M = 4, 8), within 1e-6 on the tiled GEMV (M = 1, 2)."""
+    split-K MFMA decode (M = 4, 8), within 1e-6 on the tiled GEMV (M = 1, 2) and on
+    the row-range decode (o_proj at M = 4)."""
     import torch
     K, H, F = 4096, 4096, 11008
     note(f"llama decode set tiled M={M}")
@@ -269,4 +270,6 @@ def test_llama_decode_set_tiled(dev, M):
     for a, b, what in [(ys_r[0], ys_t[0], "q"), (ys_r[1], ys_t[1], "k"),
                        (ys_r[2], ys_t[2], "v"), (g_r, g_t, "gate/up"), (o_r, o_t, "o"),
                        (d_r, d_t, "down")]:
-        same_or_close(to_host(b), to_host(a), M > 2, what)
+        # o_proj at M = 4 runs the row-range decode on tiled weights
+        exact = M > 2 and not (what == "o" and rows_decode(M, H, K))
+        same_or_close(to_host(b), to_host(a), exact, what)
