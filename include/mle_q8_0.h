@@ -271,7 +271,9 @@ int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const*
  *   MLE_OP_LINEAR_SWIGLU (count 2, N[0] == N[1], mle_q8_0_linear_swiglu) or
  *   MLE_OP_LINEAR_MULTI (count 1..3, mle_q8_0_linear_multi), with M tokens,
  *   output sizes N[0..count), input size K, on raw (tiled == 0) or 16-row
- *   tiled weights.  Launches nothing.  Errors: NULL outputs / N, M or K or an
+ *   tiled weights (0 / 0 for launches that need none: the FP32 GEMVs, and the
+ *   decode of tiled single-output Linears by whole row ranges).  Launches
+ *   nothing.  Errors: NULL outputs / N, M or K or an
  *   N <= 0, a bad count or op -> InvalidArgument; K % 32 != 0 -> Unsupported.
  * mle_workspace_reserve: grows the workspace of (current device, stream) to
  *   hold at least `bytes` and `counters` (a no-op when it already does); later
