@@ -654,10 +654,17 @@ int rows_groups_per_workgroup(int64_t G) { return (int)((G + 255) / 256); }
 // (P chained MFMAs, fp32 scale FMA into even/odd accumulators); the WG waves of
 // a group then add their sums in wave order, so results are deterministic
 // (rel-L2 ~1e-7 from the split-K kernel, which groups the K sum differently).
+// Output segments of a row-range launch: segment i owns the 16-row groups
+// [grp_end[i-1], grp_end[i]) of the grid (multi-output Linear: q, k, v).
+struct RowsArgs {
+  LinearSeg seg[3];
+  unsigned grp_end[3];
+  int count;
+};
+
 template <int MT, int NG, int NPH, int PHB, int NBUF, int RING, int WG>
 __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ w, const void* bias, int bias_bf16,
-    float* __restrict__ y, int M, int N, int K) {
+    const float* __restrict__ x, const RowsArgs args, int M, int K) {
   constexpr int W = WG * NG;
   constexpr int NT = 64 * W;
   constexpr int P = Cols<MT>::P;
@@ -683,10 +690,25 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
   const int lg = wave / WG, qw = wave % WG;
   const int KB = K / kBlockElems;
   const int KP = (KB + 1) >> 1;
+  // This wave's group: global index -> segment (uniform selects: no indexing
+  // into the argument) and its group within the segment's weight.
+  const unsigned grp = blockIdx.x * NG + lg;
+  const int si = (args.count > 1 && grp >= args.grp_end[0])
+                     ? ((args.count > 2 && grp >= args.grp_end[1]) ? 2 : 1)
+                     : 0;
+  const unsigned grp0 = si == 0 ? 0u : si == 1 ? args.grp_end[0] : args.grp_end[1];
+  const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
+  const void* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const int bias_bf16 =
+      si == 0 ? args.seg[0].bias_bf16 : si == 1 ? args.seg[1].bias_bf16 : args.seg[2].bias_bf16;
+  float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
+  const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
   const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
-  const int64_t rg = (int64_t)blockIdx.x * NG + lg;
-  const bool live_g = rg < G;
-  const int64_t rgc = live_g ? rg : 0;
+  const unsigned grp_total =
+      args.count == 1 ? args.grp_end[0] : args.count == 2 ? args.grp_end[1] : args.grp_end[2];
+  const bool live_g = grp < grp_total;
+  const int64_t rg = live_g ? (int64_t)(grp - grp0) : 0;  // group within the segment's weight
+  const int64_t rgc = rg;
 
   // Activations of one phase: item (token m fastest, k quarter, block), 8 fp32.
   // Items past M or K read zeros through the range check of the per-lane offset.
@@ -884,13 +906,13 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
 //    buffers (2 x 50 KB), 1 chunk in flight (0.95-0.97x the 64-block single
 //    buffer with 2 chunks).
 template <int MT, int NG, int WG, int PHB, int NBUF, int RING>
-hipError_t launch_rows_k(const float* x, const LinearSeg& sg, int M, int K, hipStream_t stream) {
-  const int64_t G = ((int64_t)sg.N + kTileRows - 1) / kTileRows;
-  const dim3 grid((unsigned)((G + NG - 1) / NG)), block(64 * WG * NG);
+hipError_t launch_rows_k(const float* x, const RowsArgs& a, int M, int K, hipStream_t stream) {
+  const unsigned groups = a.grp_end[a.count - 1];
+  const dim3 grid((groups + NG - 1) / NG), block(64 * WG * NG);
   const int nph = (K / kBlockElems + PHB - 1) / PHB;
 #define MLE_ROWS(NPH)                                                                        \
   hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, NPH, PHB, NBUF, RING, WG>), grid, block, \
-                     0, stream, x, sg.w, sg.bias, sg.bias_bf16, sg.y, M, sg.N, K)
+                     0, stream, x, a, M, K)
   switch (nph) {
     case 1: MLE_ROWS(1); break;
     case 2: if constexpr (PHB < 128) MLE_ROWS(2); else return hipErrorInvalidValue; break;
@@ -902,21 +924,35 @@ hipError_t launch_rows_k(const float* x, const LinearSeg& sg, int M, int K, hipS
   return hipGetLastError();
 }
 
+// The 16-row groups of 1-3 output segments, numbered segment after segment.
+RowsArgs rows_args(const LinearSegs& s) {
+  RowsArgs a{};
+  unsigned end = 0;
+  for (int i = 0; i < 3; ++i) {
+    a.seg[i] = s.seg[i];
+    if (i < s.count) end += (unsigned)((s.seg[i].N + kTileRows - 1) / kTileRows);
+    a.grp_end[i] = end;
+  }
+  a.count = s.count;
+  return a;
+}
+
 template <int MT>
-hipError_t launch_rows(const float* x, const LinearSeg& sg, int M, int K, hipStream_t stream) {
-  const int64_t G = ((int64_t)sg.N + kTileRows - 1) / kTileRows;
+hipError_t launch_rows(const float* x, const LinearSegs& s, int M, int K, hipStream_t stream) {
+  const RowsArgs a = rows_args(s);
+  const int64_t G = a.grp_end[a.count - 1];
   if constexpr (MT == 4) {
     switch (rows_groups_per_workgroup(G)) {
-      case 1: return launch_rows_k<4, 1, 16, 128, 1, 1>(x, sg, M, K, stream);
-      case 2: return launch_rows_k<4, 2, 4, 128, 1, 2>(x, sg, M, K, stream);
-      case 3: return launch_rows_k<4, 3, 4, 128, 1, 2>(x, sg, M, K, stream);
-      case 4: return launch_rows_k<4, 4, 4, 128, 1, 2>(x, sg, M, K, stream);
+      case 1: return launch_rows_k<4, 1, 16, 128, 1, 1>(x, a, M, K, stream);
+      case 2: return launch_rows_k<4, 2, 4, 128, 1, 2>(x, a, M, K, stream);
+      case 3: return launch_rows_k<4, 3, 4, 128, 1, 2>(x, a, M, K, stream);
+      case 4: return launch_rows_k<4, 4, 4, 128, 1, 2>(x, a, M, K, stream);
     }
   } else {
     switch (rows_groups_per_workgroup(G)) {
-      case 2: return launch_rows_k<8, 2, 4, 32, 2, 1>(x, sg, M, K, stream);
-      case 3: return launch_rows_k<8, 3, 4, 32, 2, 1>(x, sg, M, K, stream);
-      case 4: return launch_rows_k<8, 4, 4, 32, 2, 1>(x, sg, M, K, stream);
+      case 2: return launch_rows_k<8, 2, 4, 32, 2, 1>(x, a, M, K, stream);
+      case 3: return launch_rows_k<8, 3, 4, 32, 2, 1>(x, a, M, K, stream);
+      case 4: return launch_rows_k<8, 4, 4, 32, 2, 1>(x, a, M, K, stream);
     }
   }
   return hipErrorInvalidValue;
@@ -1049,10 +1085,15 @@ SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K) {
   return decode_mfma_workspace_segs(c, single(nullptr, nullptr, nullptr, N), K);
 }
 
-// The launches the row-range kernel takes: one plain output on tiled weights.
+// The launches the row-range kernel takes: 1-3 plain outputs on tiled weights.
 static bool rows_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
-  return c.rows == 1 && s.count == 1 && s.mode == Epilogue::kPlain &&
-         s.layout == WeightLayout::kTiled;
+  if (c.rows != 1 || s.count < 1 || s.count > 3 || s.mode != Epilogue::kPlain ||
+      s.layout != WeightLayout::kTiled)
+    return false;
+  // The launch shapes exist for these group counts (segments rounded up to whole
+  // groups each, as the grid numbers them).
+  const int64_t G = rows_args(s).grp_end[s.count - 1];
+  return (G >= 512 && G <= 1024) || (c.mt == 4 && G >= 240 && G <= 256);
 }
 
 SplitKNeed decode_mfma_workspace_segs(const DecodeMfmaConfig& c, const LinearSegs& s, int K) {
@@ -1091,8 +1132,8 @@ hipError_t launch_gemv_mfma_segs(const DecodeMfmaConfig& c, const float* x,
     if (!decode_mfma_fits(c, M, s.seg[i].N, K) || s.seg[i].N <= 0) return hipErrorInvalidValue;
   if (rows_takes(c, s)) {
     if (M > c.mt || K % 64 != 0) return hipErrorInvalidValue;
-    if (c.mt == 4) return launch_rows<4>(x, s.seg[0], M, K, stream);
-    if (c.mt == 8) return launch_rows<8>(x, s.seg[0], M, K, stream);
+    if (c.mt == 4) return launch_rows<4>(x, s, M, K, stream);
+    if (c.mt == 8) return launch_rows<8>(x, s, M, K, stream);
     return hipErrorInvalidValue;
   }
   const Grid gr = grid_of(c, s, K);

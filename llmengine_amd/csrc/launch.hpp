@@ -29,9 +29,9 @@ struct DecodeMfmaConfig {
   int mt;        // token tile: 1, 2, 4, 5, 8 or 16 (>= M)
   int waves;     // waves per workgroup: 2, 4 or 8
   int kslice;    // K blocks per workgroup: 16 or 32 (32 only for mt <= 8)
-  int rows = 0;  // 1: row-range kernel, no split K (tiled single-output Linears,
-                 // mt 4 or 8, see decode_mfma_pick); the fields above then serve
-                 // launches it does not take (multi-output, SwiGLU)
+  int rows = 0;  // 1: row-range kernel, no split K (tiled Linears with 1-3 plain
+                 // outputs, mt 4 or 8, see decode_mfma_pick); the fields above then
+                 // serve launches it does not take (SwiGLU, other group counts)
 };
 struct SplitKNeed {
   int splits = 1;             // workgroups along K

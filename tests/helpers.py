@@ -57,6 +57,13 @@ def rows_decode(M, N, K):
     return ((four or 6 <= M <= 8) and 512 <= G <= 1024) or (four and 240 <= G <= 256)
 
 
+def rows_decode_multi(M, Ns, K):
+    """rows_decode for a tiled multi-output Linear: the outputs' 16-row groups
+    (each output rounded up to whole groups) counted together."""
+    G = sum((n + 15) // 16 for n in Ns)
+    return rows_decode(M, 16 * G, K)
+
+
 def assert_bitexact(got, want, what=""):
     got = np.asarray(got, np.float32)
     want = np.asarray(want, np.float32)

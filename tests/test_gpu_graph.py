@@ -68,8 +68,10 @@ def test_linear_graph_replays_match_eager(dev, orc):
         for y in graph_out:
             y.fill_(float("nan"))
         torch.cuda.synchronize()
-        g.replay()
-        # eager work of another shape on the same stream between replays
+        with torch.cuda.stream(stream):  # replay() launches on the current stream
+            g.replay()
+        # eager work of another shape on the same stream between replays (ordered
+        # after the replay: both use this stream's workspace)
         capi.linear(xo, wo, None, other, 4, 2048, 4096, stream=stream)
         torch.cuda.synchronize()
         assert capi.workspace_info(stream)[2] == gen0
@@ -94,7 +96,8 @@ def test_linear_graph_replays_match_eager(dev, orc):
     for y in graph_out:
         y.fill_(float("nan"))
     torch.cuda.synchronize()
-    g.replay()
+    with torch.cuda.stream(stream):
+        g.replay()
     torch.cuda.synchronize()
     for (M, N, *_r), a, b in zip(cases, eager, graph_out):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32)), ("after growth", M, N)

@@ -9,7 +9,7 @@ MFMA decode, within relative L2 1e-6 with equal non-finite entries (both sum the
 same exact block products, grouped differently over K); repeatable bit for bit;
 and with a zero workspace need reported by the C ABI.  Cases cover 1 to 4
 groups per workgroup, one to four K phases (single and double buffered), N not
-a multiple of 16 (a partial last group), K/32 odd within a pair, fp32 and bf16
+a multiple of 16 (a partial last group), an odd number of block pairs, fp32 and bf16
 bias, and Inf / NaN / large activations.
 """
 import functools
@@ -17,7 +17,8 @@ import functools
 import numpy as np
 import pytest
 
-from helpers import assert_bitexact, empty_f32, note, rel_l2, rows_decode, to_dev, to_host
+from helpers import (assert_bitexact, empty_f32, note, rel_l2, rows_decode, rows_decode_multi,
+                     to_dev, to_host)
 from llmengine_amd import capi
 from llmengine_amd import synthetic as S
 
@@ -116,3 +117,40 @@ def test_rows_decode_special_values(dev):
     assert (got[4] == 0).all()
     assert not np.isfinite(got[[1, 2, 6]]).any()
     close_to_raw(got, want, "special values")
+
+
+@pytest.mark.parametrize("M,Ns,K", [(4, (4096, 4096, 4096), 4096), (8, (4096, 4096, 4096), 4096),
+                                    (3, (4000, 4000, 4100), 2048), (7, (8192, 192), 3072),
+                                    (4, (3000, 900), 2112)])
+def test_rows_decode_multi_output(dev, orc, M, Ns, K):
+    """The multi-output Linear (q/k/v) on the row-range decode: segment boundaries
+    inside workgroups (250 + 250 + 257 groups over 3-group workgroups), two outputs,
+    and 240 groups in one-group workgroups.  Each output against the oracle (sampled
+    rows on the larger shapes), against the single tiled Linear within 1e-6, with
+    its own bias; repeatable bit for bit; no workspace."""
+    import torch
+    assert rows_decode_multi(M, Ns, K)
+    note(f"rows decode multi M={M} Ns={Ns} K={K}")
+    raws = [weight(300 + 7 * i + n, n, K) for i, n in enumerate(Ns)]
+    x = S.activations(301 + M, (M, K))
+    biases = [S.activations(302 + i, (n,), tag=S.TAG_BIAS) if i != 1 else None
+              for i, n in enumerate(Ns)]
+    dx = to_dev(x, dev)
+    dts = [tiled_dev(to_dev(w, dev), n, K, dev) for w, n in zip(raws, Ns)]
+    dbs = [to_dev(b, dev) if b is not None else None for b in biases]
+    ys = [empty_f32((M, n), dev) for n in Ns]
+    ys2 = [empty_f32((M, n), dev) for n in Ns]
+    capi.linear_multi_tiled(dx, dts, dbs, ys, Ns, M, K)
+    capi.linear_multi_tiled(dx, dts, dbs, ys2, Ns, M, K)
+    torch.cuda.synchronize()
+    for i, n in enumerate(Ns):
+        assert torch.equal(ys[i], ys2[i]), i
+        got = to_host(ys[i])
+        single = empty_f32((M, n), dev)
+        capi.linear_tiled(dx, dts[i], dbs[i], single, M, n, K)
+        close_to_raw(got, to_host(single), f"multi {i} vs single")
+        rows = np.array(sorted({0, n // 3, n - 1}))
+        w_rows = np.ascontiguousarray(raws[i].reshape(n, -1)[rows]).reshape(-1)
+        b = biases[i][rows] if biases[i] is not None else None
+        assert rel_l2(got[:, rows], orc.linear(x, w_rows, b, M, rows.size, K)) <= DECODE_TOL, i
+    assert capi.workspace_size(capi.OP_LINEAR_MULTI, M, list(Ns), K, True) == (0, 0)

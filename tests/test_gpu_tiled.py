@@ -19,8 +19,8 @@ import functools
 import numpy as np
 import pytest
 
-from helpers import (assert_bitexact, empty_f32, note, rel_l2, rows_decode, tile_ref, to_dev,
-                     to_host)
+from helpers import (assert_bitexact, empty_f32, note, rel_l2, rows_decode, rows_decode_multi,
+                     tile_ref, to_dev, to_host)
 from llmengine_amd import capi
 from llmengine_amd import synthetic as S
 
@@ -241,7 +241,7 @@ def test_llama_decode_set_tiled(dev, M):
     """The four Llama-7B projection shapes of the decode benchmark, tiled against
     raw on the fused qkv, the fused gate/up and o_proj / down: bit for bit on the
     split-K MFMA decode (M = 4, 8), within 1e-6 on the tiled GEMV (M = 1, 2) and on
-    the row-range decode (o_proj at M = 4)."""
+    the row-range decode (o_proj at M = 4, the fused q/k/v at M = 4 and 8)."""
     import torch
     K, H, F = 4096, 4096, 11008
     note(f"llama decode set tiled M={M}")
@@ -270,6 +270,8 @@ def test_llama_decode_set_tiled(dev, M):
     for a, b, what in [(ys_r[0], ys_t[0], "q"), (ys_r[1], ys_t[1], "k"),
                        (ys_r[2], ys_t[2], "v"), (g_r, g_t, "gate/up"), (o_r, o_t, "o"),
                        (d_r, d_t, "down")]:
-        # o_proj at M = 4 runs the row-range decode on tiled weights
-        exact = M > 2 and not (what == "o" and rows_decode(M, H, K))
+        # the row-range decode on tiled weights: o_proj at M = 4, q/k/v at M = 4 and 8
+        rows = (rows_decode(M, H, K) if what == "o" else
+                rows_decode_multi(M, (H, H, H), K) if what in "qkv" else False)
+        exact = M > 2 and not rows
         same_or_close(to_host(b), to_host(a), exact, what)
