@@ -2,15 +2,17 @@
 workspace was reserved beforehand (mle_q8_0_workspace_size + mle_workspace_reserve):
 capture allocates and synchronises nothing, and every replay -- with eager launches of
 other shapes on the same stream and host synchronisations between replays, and after a
-later call has outgrown the reservation -- gives the eager results bit for bit.  Shapes: the split-K MFMA decode (M = 8, 22 splits), the
-tiled FP32 GEMV (M = 1) and the bf16 GEMM with its X pre-pass (M = 96).  The kernels
+later call has outgrown the reservation -- gives the eager results bit for bit.  Shapes:
+the split-K MFMA decode (M = 8, 22 splits), the tiled FP32 GEMV (M = 1), the bf16 GEMM
+with its X pre-pass (M = 96) and the row-range MFMA decode (M = 4 on 512 tiled row
+groups, no workspace).  The kernels
 reset their split-K counters themselves and the workspace counters were cleared by a
 fill kernel at allocation, so no memset node enters the graph.
 """
 import numpy as np
 import pytest
 
-from helpers import empty_f32, note, rel_l2, to_dev, to_host
+from helpers import empty_f32, note, rel_l2, rows_decode, to_dev, to_host
 from llmengine_amd import capi
 from llmengine_amd import synthetic as S
 
@@ -19,7 +21,9 @@ pytestmark = pytest.mark.gpu
 
 def test_linear_graph_replays_match_eager(dev, orc):
     import torch
-    shapes = [(8, 1024, 11008, False), (1, 512, 4096, True), (96, 384, 1024, False)]
+    shapes = [(8, 1024, 11008, False), (1, 512, 4096, True), (96, 384, 1024, False),
+              (4, 8192, 4096, True)]
+    assert rows_decode(4, 8192, 4096)  # the last shape takes the row-range kernel
     stream = torch.cuda.Stream()
     need_b = need_c = 0
     cases = []
