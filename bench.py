@@ -433,6 +433,32 @@ def main():
 
     per_launch = launches("tiled")
     per_launch_raw = launches("raw")
+
+    # ---- streaming-read floor: a kernel that only reads each op's tiled weight
+    # copies (same buffers, same rotation, same launch pattern) -- what a decode
+    # launch of those bytes could take on this GPU with no arithmetic at all
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    floor_us = {}
+    for name, N, K in LLAMA_SET:
+        R, nbytes = rot[name], tdev[name][0].numel()
+        med, _, _ = timer(lambda j: capi.probe_stream_read(tdev[name][j % R], nbytes, sink,
+                                                           stream=stream), args.launch_iters)
+        floor_us[name] = med
+    for r in per_launch:
+        r["stream_floor_us"] = round(floor_us[r["op"]], 3)
+        r["frac_of_stream_floor"] = round(floor_us[r["op"]] / r["us"], 4)
+    floor_step_us = len(MS) * sum(floor_us.values())
+    stream_floor = {
+        "kernel": "stream_read_kernel (mle_probe_stream_read: non-temporal 16-byte loads, "
+                  "4096 x 256 threads, no arithmetic)",
+        "us": {k: round(v, 3) for k, v in floor_us.items()},
+        "GBps": {name: round(tdev[name][0].numel() / floor_us[name] / 1e3, 1)
+                 for name, _, _ in LLAMA_SET},
+        "step_us": round(floor_step_us, 2),
+        "step_GBps": round(step_bytes / floor_step_us / 1e3, 1),
+        "value_frac_of_floor": round(value / (step_bytes / floor_step_us / 1e3), 4),
+        "note": "15 reads of the step's weight bytes, one launch each, back to back: the "
+                "practical ceiling for a one-launch-per-Linear decode step on this GPU"}
     dom = max(per_launch, key=lambda r: r["us"])
     dom_bytes = gemv_bytes(dom["M"], dom["N"], dom["K"])
     achieved = dom_bytes / dom["us"] / 1e3
@@ -672,6 +698,7 @@ def main():
         "raw_ms_per_step": round(raw_elapsed * 1e3 / args.steps, 4),
         "per_launch": per_launch,
         "per_launch_raw": per_launch_raw,
+        "stream_floor": stream_floor,
     }
     line.update(extras)
     print(json.dumps(line), flush=True)

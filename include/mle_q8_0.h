@@ -354,6 +354,18 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
                        float* y, int M, int N, int K, int path, int t0, int t1,
                        int t2, int t3, hipStream_t stream);
 
+/*
+ * Streaming-read probe, a measurement aid with no counterpart in the reference:
+ * reads `bytes` of src once from HBM with nothing else to do (non-temporal
+ * 16-byte loads over a fixed grid).  The benchmark times it over the same weight
+ * buffers a decode Linear reads, so the Linear's time can be set against a pure
+ * read of the same bytes as well as against the HBM peak.  `sink` is one device
+ * word, practically never written.
+ * Errors: NULL src / sink, bytes < 0 or not a multiple of 16, src not 16-byte
+ * aligned -> InvalidArgument.  bytes == 0: no launch.
+ */
+int mle_probe_stream_read(const void* src, int64_t bytes, uint32_t* sink, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -28,7 +28,7 @@ EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_q8_0_linear_multi_tiled", "mle_q8_0_workspace_size", "mle_workspace_reserve",
             "mle_workspace_info", "mle_workspace_plan_growth", "mle_q8_0_linear_noalloc",
             "mle_q8_0_dequantize", "mle_q8_0_linear_bias_bf16",
-            "mle_q8_0_linear_tiled_bias_bf16")
+            "mle_q8_0_linear_tiled_bias_bf16", "mle_probe_stream_read")
 
 OP_LINEAR, OP_LINEAR_SWIGLU, OP_LINEAR_MULTI = 0, 1, 2
 
@@ -74,6 +74,8 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_embedding_tiled.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_swiglu_f32.restype = _i
     lib.mle_swiglu_f32.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp]
+    lib.mle_probe_stream_read.restype = _i
+    lib.mle_probe_stream_read.argtypes = [_vp, ctypes.c_int64, _vp, _vp]
     lib.mle_argmax_f32.restype = _i
     lib.mle_argmax_f32.argtypes = [_vp, _i, _i, _vp, _vp, _vp]
     lib.mle_top_tokens_f32.restype = _i
@@ -268,6 +270,16 @@ def swiglu_status(gate, up, y, n, stream=None):
 def swiglu(gate, up, y, n, stream=None) -> None:
     """y[i] = silu(gate[i]) * up[i] for n fp32 elements."""
     _raise(swiglu_status(gate, up, y, n, stream)[0])
+
+
+def probe_stream_read_status(src, nbytes, sink, stream=None):
+    rc = load().mle_probe_stream_read(_addr(src), nbytes, _addr(sink), _stream(stream))
+    return _status(rc)
+
+
+def probe_stream_read(src, nbytes, sink, stream=None) -> None:
+    """Reads nbytes of src once (a measurement aid: the pure-read time of a buffer)."""
+    _raise(probe_stream_read_status(src, nbytes, sink, stream)[0])
 
 
 def argmax_status(logits, rows, n, idx, val=None, stream=None):

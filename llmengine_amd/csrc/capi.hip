@@ -731,6 +731,18 @@ int mle_swiglu_f32(const float* gate, const float* up, float* y, int64_t n,
   return check_launch(mle::launch_swiglu(gate, up, y, n, stream), "hip swiglu launch failed");
 }
 
+int mle_probe_stream_read(const void* src, int64_t bytes, uint32_t* sink, hipStream_t stream) {
+  const char* ctx = "probe_stream_read";
+  MLE_TRY(check_ptrs(ctx, src, "src", sink, "sink", sink, "sink"));
+  if (bytes < 0 || bytes % 16 != 0)
+    return fail(MLE_INVALID_ARGUMENT,
+                std::string("hip ") + ctx + ": bytes must be a non-negative multiple of 16");
+  MLE_TRY(check_align(ctx, src, 16, "src"));
+  MLE_TRY(check_align(ctx, sink, 4, "sink"));
+  return check_launch(mle::launch_stream_read(src, bytes, sink, stream),
+                      "hip stream-read probe launch failed");
+}
+
 int mle_argmax_f32(const float* logits, int rows, int n, int32_t* idx, float* val,
                    hipStream_t stream) {
   const char* ctx = "argmax_f32";

@@ -177,6 +177,10 @@ hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t stream
 // y = silu(g) * u over n fp32 elements.
 hipError_t launch_swiglu(const float* g, const float* u, float* y, int64_t n,
                          hipStream_t stream);
+// Streaming-read probe: reads `bytes` (a multiple of 16) of src once; `sink` is
+// one device word that is practically never written.
+hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* sink,
+                              hipStream_t stream);
 
 // Embedding gather-dequantise; ids outside [0, vocab) give rows of +0.0f.
 hipError_t launch_embedding(const uint8_t* w, const int32_t* ids, float* out,

@@ -99,6 +99,20 @@ def test_swiglu_validation_errors():
     assert code == 1 and "up must be 4-byte aligned" in msg
 
 
+def test_probe_stream_read_validation_errors():
+    st = capi.probe_stream_read_status
+    code, msg = st(None, 64, FAKE, stream=0)
+    assert code == 1 and "src pointer" in msg
+    code, msg = st(FAKE, 64, None, stream=0)
+    assert code == 1 and "sink pointer" in msg
+    code, msg = st(FAKE, 40, FAKE, stream=0)
+    assert code == 1 and "multiple of 16" in msg
+    code, msg = st(FAKE, -16, FAKE, stream=0)
+    assert code == 1 and "multiple of 16" in msg
+    code, msg = st(FAKE + 8, 64, FAKE, stream=0)
+    assert code == 1 and "src must be 16-byte aligned" in msg
+
+
 def test_top_tokens_validation_errors():
     st = capi.top_tokens_status
     code, msg = st(None, 1, 10, 5, FAKE, FAKE, stream=0)
