@@ -903,8 +903,9 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
 //    128-block phase (128 KB of fragments), 2 chunks in flight;
 //  * 4 tokens, 240-256 groups (o_proj): one group of 16 waves per workgroup;
 //  * 8 tokens, 512-1024 groups: 4 waves per group, 32-block phases in two
-//    buffers (2 x 50 KB), 1 chunk in flight (0.95-0.97x the 64-block single
-//    buffer with 2 chunks).
+//    buffers (2 x 50 KB; 0.95-0.97x the 64-block single buffer), 2 chunks in
+//    flight (0.98-0.99x one chunk on the Llama qkv / gate shapes; 3 or 4 chunks
+//    1.01-1.12x).
 template <int MT, int NG, int WG, int PHB, int NBUF, int RING>
 hipError_t launch_rows_k(const float* x, const RowsArgs& a, int M, int K, hipStream_t stream) {
   const unsigned groups = a.grp_end[a.count - 1];
@@ -950,9 +951,9 @@ hipError_t launch_rows(const float* x, const LinearSegs& s, int M, int K, hipStr
     }
   } else {
     switch (rows_groups_per_workgroup(G)) {
-      case 2: return launch_rows_k<8, 2, 4, 32, 2, 1>(x, a, M, K, stream);
-      case 3: return launch_rows_k<8, 3, 4, 32, 2, 1>(x, a, M, K, stream);
-      case 4: return launch_rows_k<8, 4, 4, 32, 2, 1>(x, a, M, K, stream);
+      case 2: return launch_rows_k<8, 2, 4, 32, 2, 2>(x, a, M, K, stream);
+      case 3: return launch_rows_k<8, 3, 4, 32, 2, 2>(x, a, M, K, stream);
+      case 4: return launch_rows_k<8, 4, 4, 32, 2, 2>(x, a, M, K, stream);
     }
   }
   return hipErrorInvalidValue;
