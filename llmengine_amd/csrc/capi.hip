@@ -807,7 +807,14 @@ int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M, int 
   MLE_TRY(check_align(ctx, a, 4, "A"));
   MLE_TRY(check_align(ctx, b_q8_0, 2, "B"));
   MLE_TRY(check_align(ctx, c, 16, "C"));
-  return check_launch(mle::launch_matmul(a, b_q8_0, c, M, N, K, stream),
+  if ((M + 7) / 8 > 65535)
+    return fail(MLE_UNSUPPORTED, "hip sgemm Q8_0: at most 524280 rows of A per call");
+  mle::SplitKNeed need;
+  need.partial_floats = mle::matmul_workspace_floats(M, N, K);
+  mle::SplitKWorkspace ws;
+  std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
+  MLE_TRY(get_workspace(need, stream, &ws, &hold));
+  return check_launch(mle::launch_matmul(a, b_q8_0, c, M, N, K, ws.partials, stream),
                       "hip sgemm Q8_0 launch failed");
 }
 

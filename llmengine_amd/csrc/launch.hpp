@@ -148,9 +148,12 @@ SplitKNeed gemm_mfma_workspace_segs(const GemmConfig& c, int M, const LinearSegs
 hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const LinearSegs& s,
                                  int M, int K, const SplitKWorkspace& ws, hipStream_t stream);
 
-// MatMul C[M,N] = A[M,K] . B[K,N] with B in Q8_0 blocks along N.
-hipError_t launch_matmul(const float* a, const uint8_t* b, float* c, int M,
-                         int N, int K, hipStream_t stream);
+// MatMul C[M,N] = A[M,K] . B[K,N] with B in Q8_0 blocks along N.  When the
+// launch spreads K over several workgroups per tile it needs
+// matmul_workspace_floats(M, N, K) floats of workspace in `partials` (0: none).
+size_t matmul_workspace_floats(int M, int N, int K);
+hipError_t launch_matmul(const float* a, const uint8_t* b, float* c, int M, int N, int K,
+                         float* partials, hipStream_t stream);
 
 // Greedy argmax of `rows` rows of n fp32 logits: idx (and val, if non-null) per
 // row; `keys` is a workspace of rows * argmax_chunks(n) 64-bit entries.
