@@ -277,9 +277,11 @@ int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const*
  *   MLE_OP_LINEAR_MULTI (count 1..3, mle_q8_0_linear_multi), with M tokens,
  *   output sizes N[0..count), input size K, on raw (tiled == 0) or 16-row
  *   tiled weights (0 / 0 for launches that need none: the FP32 GEMVs, and the
- *   decode of tiled single-output Linears by whole row ranges).  Launches
+ *   decode of tiled plain Linears by whole row ranges), or MLE_OP_MATMUL
+ *   (count 1, mle_q8_0_matmul: A [M, K], B [K, N[0]]; tiled ignored).  Launches
  *   nothing.  Errors: NULL outputs / N, M or K or an
- *   N <= 0, a bad count or op -> InvalidArgument; K % 32 != 0 -> Unsupported.
+ *   N <= 0, a bad count or op -> InvalidArgument; K % 32 != 0 (MatMul: or
+ *   N % 32 != 0) -> Unsupported.
  * mle_workspace_reserve: grows the workspace of (current device, stream) to
  *   hold at least `bytes` and `counters` (a no-op when it already does); later
  *   calls within those sizes allocate and synchronise nothing.
@@ -294,6 +296,7 @@ int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const*
 #define MLE_OP_LINEAR 0
 #define MLE_OP_LINEAR_SWIGLU 1
 #define MLE_OP_LINEAR_MULTI 2
+#define MLE_OP_MATMUL 3
 int mle_q8_0_workspace_size(int op, int M, int count, const int* N, int K, int tiled,
                             size_t* bytes, size_t* counters);
 int mle_workspace_reserve(size_t bytes, size_t counters, hipStream_t stream);

@@ -30,7 +30,7 @@ EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
             "mle_q8_0_dequantize", "mle_q8_0_linear_bias_bf16",
             "mle_q8_0_linear_tiled_bias_bf16", "mle_probe_stream_read")
 
-OP_LINEAR, OP_LINEAR_SWIGLU, OP_LINEAR_MULTI = 0, 1, 2
+OP_LINEAR, OP_LINEAR_SWIGLU, OP_LINEAR_MULTI, OP_MATMUL = 0, 1, 2, 3
 
 
 class Q8_0Error(RuntimeError):

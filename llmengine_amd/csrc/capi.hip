@@ -685,6 +685,16 @@ int mle_q8_0_workspace_size(int op, int M, int count, const int* N, int K, int t
     }
     return run_segs(ctx, nullptr, s, M, K, ex);
   }
+  if (op == MLE_OP_MATMUL) {
+    if (count != 1) return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": a MatMul has count 1");
+    MLE_TRY(check_positive(ctx, N[0], "N"));
+    if (N[0] % 32 != 0)
+      return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + " requires a MatMul's N to be a multiple of 32");
+    mle::SplitKNeed need;
+    need.partial_floats = mle::matmul_workspace_floats(M, N[0], K);
+    *bytes = need_bytes(need);
+    return ok();
+  }
   return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": unknown op " + std::to_string(op));
 }
 

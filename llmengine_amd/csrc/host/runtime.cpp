@@ -192,6 +192,32 @@ Status HipExecutor::tile_weights(RuntimeContext& ctx, bool release_raw) {
 namespace {
 // M, N, K of a Linear node from the tensors bound in ctx, else the graph's
 // static value shapes (false when unknown or dynamic).
+// M, N, K of a MatMul node: A [M, K] . B [K, N] (rank 2, static shapes).
+bool matmul_dims(const Graph& g, const Node& n, const RuntimeContext* ctx, int64_t* M,
+                 int64_t* N, int64_t* K) {
+  if (n.op_type() != OpType::MatMul || n.inputs().size() < 2) return false;
+  Shape as, bs;
+  auto shape_of = [&](ValueId id, Shape* out) {
+    if (ctx) {
+      if (const Tensor* t = ctx->get(id)) {
+        *out = t->shape();
+        return !out->has_dynamic_dim();
+      }
+    }
+    auto v = g.value(id);
+    if (!v) return false;
+    *out = (*v)->shape;
+    return !out->has_dynamic_dim();
+  };
+  if (!shape_of(n.inputs()[0], &as) || !shape_of(n.inputs()[1], &bs)) return false;
+  if (as.rank() != 2 || bs.rank() != 2) return false;
+  *M = as.dim(0);
+  *K = as.dim(1);
+  *N = bs.dim(1);
+  return *M > 0 && *N > 0 && *K > 0 && *M <= INT32_MAX && *N <= INT32_MAX && *K <= INT32_MAX &&
+         *K % 32 == 0 && *N % 32 == 0;
+}
+
 bool linear_dims(const Graph& g, const Node& n, const RuntimeContext* ctx, int64_t* M,
                  int64_t* N, int64_t* K) {
   if (n.op_type() != OpType::Linear || n.inputs().size() < 2) return false;
@@ -238,13 +264,18 @@ Status HipExecutor::reserve_workspace(const RuntimeContext* ctx) {
       auto nd = graph_->node(nid);
       if (nd) nodes.push_back(*nd);
     }
-    // Every Linear also on its own (a fused group that does not fit its kernel
-    // runs node by node), then the fused launch of its group.
+    // Every MatMul, and every Linear also on its own (a fused group that does
+    // not fit its kernel runs node by node), then the fused launch of its group.
     std::vector<int> Ns;
     int64_t M0 = 0, K0 = 0;
     bool same = true;
     for (const Node* n : nodes) {
       int64_t M, N, K;
+      if (matmul_dims(*graph_, *n, ctx, &M, &N, &K)) {
+        const int n32 = static_cast<int>(N);
+        need(MLE_OP_MATMUL, static_cast<int>(M), 1, &n32, static_cast<int>(K));
+        continue;
+      }
       if (!linear_dims(*graph_, *n, ctx, &M, &N, &K)) continue;
       const int n32 = static_cast<int>(N);
       need(MLE_OP_LINEAR, static_cast<int>(M), 1, &n32, static_cast<int>(K));

@@ -1096,6 +1096,66 @@ static void test_executor_reserves_workspace() {
   std::printf("  executor_reserves_workspace ok\n");
 }
 
+static void test_executor_reserves_matmul_workspace() {
+  // A decode-size MatMul (A [1, 4096] . B [4096, 4096]) spreads K over several
+  // workgroups per column tile and needs workspace: compile() reserves it, run()
+  // allocates nothing, and sampled outputs match an fp64 sum within 1e-5.
+  const int M = 1, K = 4096, N = 4096;
+  hipStream_t stream;
+  check_hip(hipStreamCreate(&stream));
+  Graph g;
+  GraphBuilder gb(g);
+  const Device dev = Device::hip(0);
+  auto a = gb.input("a", Shape({M, K}), DType::Float32, dev);
+  auto b = gb.constant("b", Shape({K, N}), DType::Float32, dev);
+  CHECK(a && b);
+  auto y = gb.matmul(*a, *b, "mm");
+  CHECK(y && gb.output(*y, "out"));
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  HipExecutor ex(std::make_shared<HipBackend>(), registry, stream);
+  check_status(ex.compile(g));
+  size_t need_b = 0, need_c = 0, cap_b = 0, cap_c = 0;
+  CHECK(mle_q8_0_workspace_size(MLE_OP_MATMUL, M, 1, &N, K, 0, &need_b, &need_c) == 0);
+  CHECK(need_b > 0 && need_c == 0);
+  CHECK(ex.workspace_bytes() >= need_b);
+  uint64_t gen = 0, gen2 = 0;
+  CHECK(mle_workspace_info(stream, &cap_b, &cap_c, &gen) == 0);
+  CHECK(gen >= 1 && cap_b >= need_b);
+  const auto hb = random_q8(K, N, 77);  // K rows of N: blocks along N
+  Tensor tb("b", Shape({K, N}), DType::Q8_0, dev);
+  check_status(tb.allocate_hip_bytes(hb.size()));
+  upload(tb, hb.data(), hb.size());
+  std::vector<float> ha(size_t(M) * K);
+  for (size_t i = 0; i < ha.size(); ++i) ha[i] = float(int(i * 29 % 113) - 56) * 0.02f;
+  Tensor ta("a", Shape({M, K}), DType::Float32, dev);
+  check_status(ta.allocate_hip());
+  upload(ta, ha.data(), ha.size() * 4);
+  RuntimeContext ctx;
+  check_status(ctx.bind(*a, &ta));
+  check_status(ctx.bind(*b, &tb));
+  check_status(ctx.allocate_intermediates(g));
+  for (int r = 0; r < 3; ++r) check_status(ex.run(ctx));
+  check_hip(hipStreamSynchronize(stream));
+  CHECK(mle_workspace_info(stream, &cap_b, &cap_c, &gen2) == 0);
+  CHECK(gen2 == gen);
+  const auto got = download(ctx.get(*y), size_t(M) * N);
+  double num = 0, den = 0;
+  for (int n : {0, 31, 32, 1000, N / 2, N - 1}) {
+    double e = 0;
+    for (int k = 0; k < K; ++k) {
+      const uint8_t* blk = hb.data() + (size_t(k) * (N / 32) + n / 32) * 34;
+      e += double(ha[k]) * host_half(uint16_t(blk[0] | (blk[1] << 8))) *
+           double(int8_t(blk[2 + n % 32]));
+    }
+    num += (got[n] - e) * (got[n] - e);
+    den += e * e;
+  }
+  CHECK(std::sqrt(num / den) <= 1e-5);
+  check_hip(hipStreamDestroy(stream));
+  std::printf("  executor_reserves_matmul_workspace ok\n");
+}
+
 static void test_tiled_copy_shape_guard() {
   // A tiled copy is used only for the weight shape it was made for: after the
   // executor is recompiled for a graph that views the same weight buffer as
@@ -1464,6 +1524,7 @@ int main() {
   test_executor_rows_decode();
   test_workspace_no_regrowth();
   test_executor_reserves_workspace();
+  test_executor_reserves_matmul_workspace();
   test_tiled_copy_shape_guard();
   test_loader_dequantizes_q8_0_on_device();
   test_executor_linear_bf16_bias();

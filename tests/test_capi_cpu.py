@@ -99,6 +99,19 @@ def test_swiglu_validation_errors():
     assert code == 1 and "up must be 4-byte aligned" in msg
 
 
+def test_matmul_workspace_size():
+    """MLE_OP_MATMUL: decode-size MatMuls spread K over workgroups and need
+    workspace ([S][M][N] partial floats); large M or wide N need none."""
+    b, c = capi.workspace_size(capi.OP_MATMUL, 1, [4096], 4096)
+    assert b >= 16 * 4096 * 4 and c == 0
+    assert capi.workspace_size(capi.OP_MATMUL, 512, [4096], 4096) == (0, 0)
+    assert capi.workspace_size(capi.OP_MATMUL, 1, [151936], 896) == (0, 0)
+    code, msg, _, _ = capi.workspace_size_status(capi.OP_MATMUL, 1, [48], 64)
+    assert code == 4 and "multiple of 32" in msg
+    code, msg, _, _ = capi.workspace_size_status(capi.OP_MATMUL, 1, [64, 64], 64)
+    assert code == 1 and "count 1" in msg
+
+
 def test_probe_stream_read_validation_errors():
     st = capi.probe_stream_read_status
     code, msg = st(None, 64, FAKE, stream=0)
