@@ -352,7 +352,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
         const uint32_t off = 2 * pr < nblk
                                  ? (uint32_t)(p0 + pr) * kTilePieceBytes + (uint32_t)lane * 16
                                  : 0x80000000u;
-        tq[c][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0);
+        tq[c][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, kNonTemporal);
       }
       const int ps = (KS / 2) * c + g;  // scale pair of this lane
       ts[c] = __builtin_amdgcn_raw_buffer_load_b32(
@@ -746,7 +746,7 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
       const int pr = p0 + u;
       uint32_t off = pr < KP ? (uint32_t)pr * kTilePieceBytes + (uint32_t)lane * 16 : 0x80000000u;
       asm volatile("" : "+v"(off));
-      tq[cg][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0);
+      tq[cg][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, kNonTemporal);
     }
     const int ps = p0 + g;
     uint32_t soff = ps < KP ? (uint32_t)ps * kTileScaleBytes + (uint32_t)r16 * 4 : 0x80000000u;

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(1024) void gemv_tiled_kernel(const float* __restric
       const bool live = p0 + j < KP;
       q[j] = __builtin_amdgcn_raw_buffer_load_b128(
           qrs, live ? (uint32_t)(p0 + j) * kTilePieceBytes + (uint32_t)lane * 16 : 0x80000000u,
-          0, 0);
+          0, kNonTemporal);
       sc[j] = __builtin_amdgcn_raw_buffer_load_b32(
           srs, live ? (uint32_t)(p0 + j) * kTileScaleBytes + (uint32_t)r * 4 : 0x80000000u, 0,
           0);
