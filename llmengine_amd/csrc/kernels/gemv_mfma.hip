@@ -1060,12 +1060,15 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
     // in 4-wave workgroups, except at 16 tokens and for a vocabulary-sized
     // weight from 8 tokens (lm_head M = 8: 33.0 us vs 38.4); long rows in 8-wave
     // workgroups, except 4 for 12288+ outputs at 8 tokens (fused q/k/v 15.9 us
-    // vs 16.6, gate/up 24.1 vs 24.3).  The K slice follows the raw rule, so raw
-    // and tiled launches accumulate in the same order.
+    // vs 16.6, gate/up 24.1 vs 24.3) and for rows of 8192+ elements, where twice
+    // the row tiles balance better (down 4096 x 11008 with non-temporal weight
+    // loads: 14.7-15.0 us vs 15.8-15.9 at M = 8, 12.85 vs 13.15 at M = 4; o_proj
+    // at K = 4096 stays faster with 8: 7.8 vs 8.55).  The K slice follows the raw
+    // rule, so raw and tiled launches accumulate in the same order.
     if (KB <= 32)
       c.waves = (c.mt >= 16 || (c.mt >= 8 && N >= 65536)) ? 8 : 4;
     else
-      c.waves = (c.mt == 8 && N >= 12288) ? 4 : 8;
+      c.waves = ((c.mt == 8 && N >= 12288) || K >= 8192) ? 4 : 8;
     // The row-range kernel where it was measured to win (MI355X, Llama-7B
     // shapes at K = 4096, time against the split-K kernel): gate / up / qkv
     // (512-1024 row groups, 2-4 per workgroup sharing its activation split) at

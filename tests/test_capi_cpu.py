@@ -335,9 +335,12 @@ def test_workspace_size_matches_launch_plan():
     assert ws(capi.OP_LINEAR, 1, [4096], 4096, tiled=True) == (0, 0)  # tiled GEMV
     b, c = ws(capi.OP_LINEAR, 8, [4096], 11008)                       # MFMA decode, 22 splits
     # every row x 22 K slices x 8 tokens of partial floats; 32 counters per row tile
-    # (4-wave tiles of 64 rows on raw weights, 8-wave tiles of 128 rows when tiled)
+    # (4-wave tiles of 64 rows, raw and tiled: rows this long take 4-wave tiles when
+    # tiled too; o_proj's 4096-element rows take 8-wave tiles of 128 rows when tiled)
     assert b == 4096 * 22 * 8 * 4 and c == (4096 // 64) * 32
-    assert ws(capi.OP_LINEAR, 8, [4096], 11008, tiled=True) == (b, (4096 // 128) * 32)
+    assert ws(capi.OP_LINEAR, 8, [4096], 11008, tiled=True) == (b, (4096 // 64) * 32)
+    bo, co = ws(capi.OP_LINEAR, 8, [4096], 4096, tiled=True)         # o_proj: 8 splits
+    assert bo == 4096 * 8 * 8 * 4 and co == (4096 // 128) * 32
     bg, cg = ws(capi.OP_LINEAR, 512, [11008], 4096)                   # prefill GEMM
     assert bg >= 512 * 4096 * 2                                       # bf16 copy of X
     b3, c3 = ws(capi.OP_LINEAR_MULTI, 8, [4096, 4096, 4096], 4096)
