@@ -66,7 +66,7 @@ PARITY_ROWS = 64                 # output rows (n) sampled per shape for the par
 # `bench.py --profile-kernel M,N,K[,tiled]` (FETCH_SIZE scaled by a device copy's
 # read/write ratio), keyed by (layout, M, N, K); the summaries are in profiles/.
 MEASURED_TRAFFIC = {("raw", 8, 4096, 11008): 57.242e6, ("raw", 8, 12288, 4096): 61.358e6,
-                    ("tiled", 8, 4096, 11008): 56.746e6, ("tiled", 8, 12288, 4096): 55.104e6,
+                    ("tiled", 8, 4096, 11008): 56.787e6, ("tiled", 8, 12288, 4096): 55.104e6,
                     ("tiled", 4, 11008, 4096): 48.734e6, ("tiled", 1, 4096, 11008): 48.306e6,
                     ("raw", 512, 11008, 4096): 152.297e6, ("tiled", 512, 11008, 4096): 152.287e6}
 
