@@ -160,8 +160,9 @@ class HipExecutor final : public Executor {
   // each Linear weight (the raw buffer stays with the caller).
   //
   // release_raw: a weight whose tensor owns its device storage
-  // (allocate_hip*) and whose buffer the graph reads only as Linear weights is
-  // re-tiled in place instead: the tensor adopts the tiled buffer
+  // (allocate_hip*), whose buffer the graph reads only as Linear weights and
+  // whose bytes no other tensor bound in `ctx` views (bind_hip_data on the same
+  // or an overlapping range) is re-tiled in place instead: the tensor adopts the tiled buffer
   // (StorageLayout::Q8_0Tiled) and its raw bytes are freed after a synchronise
   // of this stream, so the weight costs no extra memory.  Such a tensor stays
   // tiled for good: any executor's Linear and Embedding kernels run it on the

@@ -135,14 +135,33 @@ Status HipExecutor::tile_weights(RuntimeContext& ctx, bool release_raw) {
   // them, keep their raw bytes: a MatMul operand cannot be read from tiles, and
   // an Embedding table (a tied lm_head) gathers twice as fast from raw bytes
   // (each row's quants share their 16-byte tile slots' cache lines with 15
-  // other rows), which HBM capacity makes the better trade.
+  // other rows), which HBM capacity makes the better trade.  So does a buffer
+  // that another tensor bound in `ctx` also views (the same bytes, or a range
+  // overlapping them): freeing its raw bytes would leave that view dangling.
   std::unordered_set<const void*> other_use;
-  if (release_raw)
+  struct Span {
+    const Tensor* t;
+    uintptr_t lo, hi;
+  };
+  std::vector<Span> spans;
+  if (release_raw) {
     for (const Node& n : graph_->nodes())
       for (size_t i = 0; i < n.inputs().size(); ++i) {
         if (n.op_type() == OpType::Linear && i == 1) continue;
         if (const Tensor* t = ctx.get(n.inputs()[i]); t && t->data()) other_use.insert(t->data());
       }
+    for (const Value& v : graph_->values())
+      if (const Tensor* t = ctx.get(v.id); t && t->data() && t->allocated_bytes() > 0) {
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(t->data());
+        spans.push_back(Span{t, lo, lo + t->allocated_bytes()});
+      }
+  }
+  auto viewed_by_other = [&](const Tensor* w) {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(w->data()), hi = lo + w->allocated_bytes();
+    for (const Span& s : spans)
+      if (s.t != w && s.lo < hi && lo < s.hi) return true;
+    return false;
+  };
   for (const Node& n : graph_->nodes()) {
     if (n.op_type() != OpType::Linear || n.inputs().size() < 2) continue;
     Tensor* w = ctx.get(n.inputs()[1]);
@@ -162,18 +181,24 @@ Status HipExecutor::tile_weights(RuntimeContext& ctx, bool release_raw) {
       return Status::runtime_error(std::string("tiled weight allocation failed: ") +
                                    hipGetErrorString(err));
     }
-    const bool in_place = release_raw && w->owns_hip_storage() && !other_use.count(w->data());
+    const bool in_place = release_raw && w->owns_hip_storage() && !other_use.count(w->data()) &&
+                          !viewed_by_other(w);
     if (!in_place) tiled_bufs_.push_back(buf);
     Status st = hip::tile_q8_0(static_cast<const uint8_t*>(w->data()),
                                static_cast<uint8_t*>(buf), static_cast<int>(N),
                                static_cast<int>(K), stream_);
-    if (st.ok() && in_place) {
-      // The tile kernel must be done with the raw bytes before they are freed.
-      const hipError_t e = hipStreamSynchronize(stream_);
-      st = e == hipSuccess ? w->adopt_hip_bytes(buf, bytes, StorageLayout::Q8_0Tiled)
-                           : Status::runtime_error(std::string("hipStreamSynchronize failed: ") +
-                                                   hipGetErrorString(e));
-      if (!st.ok()) (void)hipFree(buf);
+    if (in_place) {
+      if (st.ok()) {
+        // The tile kernel must be done with the raw bytes before they are freed.
+        const hipError_t e = hipStreamSynchronize(stream_);
+        st = e == hipSuccess ? w->adopt_hip_bytes(buf, bytes, StorageLayout::Q8_0Tiled)
+                             : Status::runtime_error(std::string("hipStreamSynchronize failed: ") +
+                                                     hipGetErrorString(e));
+      }
+      if (!st.ok()) {
+        (void)hipStreamSynchronize(stream_);  // a launched tile kernel may still write buf
+        (void)hipFree(buf);                   // not adopted: still this function's
+      }
     }
     if (!st.ok()) {
       release_tiled_weights();

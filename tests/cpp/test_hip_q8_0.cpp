@@ -1505,6 +1505,85 @@ static void test_executor_tiles_in_place() {
   std::printf("  PASS test_executor_tiles_in_place\n");
 }
 
+static void test_tile_in_place_skips_viewed_buffers() {
+  // tile_weights(ctx, release_raw = true) re-tiles in place only a weight whose
+  // bytes no other tensor bound in the context views.  Here weight A owns its
+  // buffer and tensor B views A's bytes (bind_hip_data), each the weight of a
+  // Linear; tensor C views the second half of D's buffer, and D is a Linear
+  // weight.  Freeing A's or D's raw bytes would leave B or C dangling, so both
+  // get copies (A and B share one: same bytes), while E, owned and viewed by
+  // nothing else, is re-tiled in place.  Every output equals the raw run bit for
+  // bit (M = 8: the MFMA decode), before and after.
+  const int M = 8, K = 256, N = 64;
+  KernelRegistry registry;
+  register_hip_kernels(registry);
+  const Device dev = Device::hip(0);
+  Graph g;
+  GraphBuilder gb(g);
+  auto x = gb.input("x", Shape({M, K}), DType::Float32, dev);
+  CHECK(x);
+  const char* names[5] = {"wa", "wb", "wc", "wd", "we"};
+  const int rows[5] = {N, N, N / 2, N, N};
+  std::vector<ValueId> cw;
+  for (int i = 0; i < 5; ++i) {
+    auto c = gb.constant(names[i], Shape({rows[i], K}), DType::Float32, dev);
+    CHECK(c);
+    cw.push_back(*c);
+  }
+  std::vector<ValueId> outs;
+  for (int i = 0; i < 5; ++i) {
+    auto y = gb.linear(*x, cw[i], std::nullopt, std::string("lin_") + names[i]);
+    CHECK(y && gb.output(*y, std::string("o_") + names[i]));
+    outs.push_back(*y);
+  }
+  const size_t row_bytes = size_t(K / 32) * 34;
+  Tensor ta("wa", Shape({N, K}), DType::Q8_0, dev), td("wd", Shape({N, K}), DType::Q8_0, dev),
+      te("we", Shape({N, K}), DType::Q8_0, dev);
+  Tensor tb("wb", Shape({N, K}), DType::Q8_0, dev), tc("wc", Shape({N / 2, K}), DType::Q8_0, dev);
+  Tensor* owners[3] = {&ta, &td, &te};
+  for (int i = 0; i < 3; ++i) {
+    const auto hw = synth_q8(N, K, 300 + i);
+    check_status(owners[i]->allocate_hip_bytes(hw.size()));
+    upload(*owners[i], hw.data(), hw.size());
+  }
+  check_status(tb.bind_hip_data(ta.data(), ta.allocated_bytes()));
+  check_status(tc.bind_hip_data(static_cast<uint8_t*>(td.data()) + row_bytes * (N / 2),
+                                row_bytes * (N / 2)));
+  RuntimeContext ctx;
+  Tensor* bound[5] = {&ta, &tb, &tc, &td, &te};
+  for (int i = 0; i < 5; ++i) check_status(ctx.bind(cw[i], bound[i]));
+  std::vector<float> hx(size_t(M) * K);
+  for (size_t i = 0; i < hx.size(); ++i) hx[i] = float(int(i * 53 % 97) - 48) * 0.03f;
+  Tensor tx("x", Shape({M, K}), DType::Float32, dev);
+  check_status(tx.allocate_hip());
+  upload(tx, hx.data(), hx.size() * 4);
+  check_status(ctx.bind(*x, &tx));
+  check_status(ctx.allocate_intermediates(g));
+  auto outputs = [&]() {
+    std::vector<std::vector<float>> o;
+    for (int i = 0; i < 5; ++i) o.push_back(download(ctx.get(outs[i]), size_t(M) * rows[i]));
+    return o;
+  };
+  HipExecutor ex(std::make_shared<HipBackend>(), registry);
+  ex.set_fusion(false);
+  check_status(ex.compile(g));
+  check_status(ex.run(ctx));
+  check_hip(hipDeviceSynchronize());
+  const auto ref = outputs();
+  check_status(ex.tile_weights(ctx, true));
+  CHECK(ex.tiled_in_place() == 1u);  // E
+  CHECK(ex.tiled_weights() == 3u);   // A (shared with B), C, D
+  CHECK(te.storage_layout() == StorageLayout::Q8_0Tiled);
+  for (const Tensor* t : {&ta, &tb, &tc, &td}) CHECK(t->storage_layout() == StorageLayout::Raw);
+  check_status(ex.run(ctx));
+  check_hip(hipDeviceSynchronize());
+  CHECK(ex.tiled_launches() == 5u);
+  const auto got = outputs();
+  for (int i = 0; i < 5; ++i)
+    CHECK(std::memcmp(ref[i].data(), got[i].data(), ref[i].size() * 4) == 0);
+  std::printf("  PASS test_tile_in_place_skips_viewed_buffers\n");
+}
+
 int main() {
   int count = 0;
   check_hip(hipGetDeviceCount(&count));
@@ -1529,6 +1608,7 @@ int main() {
   test_loader_dequantizes_q8_0_on_device();
   test_executor_linear_bf16_bias();
   test_executor_tiles_in_place();
+  test_tile_in_place_skips_viewed_buffers();
   std::printf("test_hip_q8_0: all passed\n");
   return 0;
 }
