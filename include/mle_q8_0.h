@@ -61,7 +61,8 @@ int mle_q8_0_abi_version(void);
  * minillm::cuda::add_bias(float*, const float*, int, int) (cuda_kernels.h:22),
  * which this entry point fuses when `bias` is non-NULL (NULL = no bias).
  *
- * Paths: M == 1, and M <= 4 with K <= 1024 and N <= 32768, run the FP32 decode GEMV; other
+ * Paths: M == 1, M <= 4 with K <= 1024 and N <= 32768, and M == 2 with
+ * 2048 <= K <= 4096 and N <= 32768, run the FP32 decode GEMV; other
  * M < 64 run the MFMA decode kernel in chunks of up to 16 tokens (FP32
  * activations split exactly into three bf16 parts, so it matches FP32 to about
  * 1e-7 relative L2);

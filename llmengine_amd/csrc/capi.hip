@@ -242,11 +242,17 @@ int workspace_for(const mle::SplitKNeed& need, const Exec& ex, mle::SplitKWorksp
 // 3 MFMA decode with FP32-exact activations.
 // The FP32 GEMV also wins for a few tokens on short rows (K <= 1024, e.g. the
 // 896-wide Qwen projections: 4.5-5.1 us vs 5.5-7.0 us at M = 2..4, MI355X),
-// but not on a vocabulary-sized weight (the [151936, 896] lm_head at M = 4:
-// 50.9 us vs 34.5 us for the MFMA decode).
+// and for two tokens on rows of 2048-4096 elements (Llama qkv / gate / o_proj
+// at M = 2: 15.9 / 15.1 / 8.4 us vs 17.2 / 16.4 / 8.5 for the MFMA decode; not
+// down at K = 11008, 19.8 vs 15.6).  The rule looks at M and K only (and the
+// vocabulary bound), so a fused q/k/v launch and its three single Linears take
+// the same path and agree bit for bit.  Not on a vocabulary-sized weight (the
+// [151936, 896] lm_head at M = 4: 50.9 us vs 34.5 us for the MFMA decode).
 int pick_path(int M, int N, int K) {
   if (M >= 64) return 2;
-  if (M == 1 || (M <= 4 && K <= 1024 && N <= 32768)) return 1;
+  if (M == 1 || (M <= 4 && K <= 1024 && N <= 32768) ||
+      (M == 2 && K >= 2048 && K <= 4096 && N <= 32768))
+    return 1;
   return 3;
 }
 
@@ -346,7 +352,8 @@ int run_linear(const float* x, const uint8_t* w, const void* bias, float* y, int
 
 // One launch over 1-3 output segments (multi-output Linear) or a gate/up pair
 // (SwiGLU): the same path choice as a single Linear (bf16 MFMA GEMM for
-// M >= 64, FP32 GEMV for M == 1 and for M <= 4 on short rows, else the MFMA
+// M >= 64, FP32 GEMV for M == 1, for M <= 4 on short rows and for M == 2 on
+// rows of 2048-4096 elements, else the MFMA
 // decode kernel in chunks of up to 16 tokens with FP32-exact activations);
 // SwiGLU takes the GEMV for M == 1 only.
 int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, int K,

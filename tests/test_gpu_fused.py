@@ -105,7 +105,8 @@ def test_multi_output_matches_oracle_and_single(dev, orc, M):
             assert torch.equal(single, ys[i]), i
 
 
-@pytest.mark.parametrize("M,Ns", [(1, (4096, 1024, 1024)), (4, (4096, 1024, 1024)),
+@pytest.mark.parametrize("M,Ns", [(1, (4096, 1024, 1024)), (2, (4096, 1024, 1024)),
+                                  (2, (4096, 4096, 4096)), (4, (4096, 1024, 1024)),
                                   (4, (4096, 4096, 4096)), (8, (4096, 4096, 4096))])
 def test_multi_output_llama_qkv(dev, orc, M, Ns):
     """q/k/v of a grouped-query ([4096, 4096], [1024, 4096] x 2) and a multi-head

@@ -322,6 +322,25 @@ def test_linear_gemv_deterministic_and_linear(dev):
     assert rel_l2(to_host(y12), to_host(y1a) + to_host(y2)) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("N,K", [(12288, 4096), (11008, 4096), (4096, 4096), (8200, 2080)])
+def test_linear_two_tokens_gemv(dev, orc, N, K):
+    """M = 2 on raw weights with rows of 2048-4096 elements takes the FP32 GEMV
+    (automatic path; two rows per lane group from 8192 outputs; 8200 x 2080: a ragged
+    last row pair and 65 blocks per row): with bias, against the oracle, and bit-equal
+    to the forced GEMV launch with one and with two rows per group (the row count
+    does not change a row's sum)."""
+    M = 2
+    note(f"two-token GEMV {N}x{K}")
+    w, x = weight(82, N, K), acts(83, M, K)
+    bias = S.activations(84, (N,), tag=S.TAG_BIAS)
+    want = orc.linear(x, w, bias, M, N, K)
+    got = run_linear(dev, x, w, bias, M, N, K)
+    assert rel_l2(got, want) <= GEMV_TOL
+    for rw in (1, 2):
+        forced = run_linear(dev, x, w, bias, M, N, K, path=1, mt=2, lpr=32, rw=rw)
+        assert np.array_equal(bits(got), bits(forced)), rw
+
+
 # ----------------------------------------------------------------------------- linear MFMA decode
 
 DECODE_SHAPES = [(2, 16), (4, 16), (8, 16), (2, 32), (4, 32), (8, 32)]
