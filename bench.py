@@ -148,8 +148,10 @@ def rel_l2(a, ref):
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    # 20000 steps of the decode set: ~3.3 s of timed GPU work on tiled weights (and ~4.3 s
+    # on raw bytes), long enough for an outside clock or utilisation sampler to see it.
+    p.add_argument("--steps", type=int, default=20000)
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--launch-iters", type=int, default=120,
                    help="launches per shape and repetition for the per-launch timings")
     p.add_argument("--no-cpu-baseline", action="store_true")
