@@ -385,7 +385,7 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
   }
   for (int m0 = 0; m0 < M; m0 += 16) {
     const int mc = M - m0 < 16 ? M - m0 : 16;
-    const mle::DecodeMfmaConfig c = mle::decode_mfma_pick(mc, total_n, K, s.layout);
+    const mle::DecodeMfmaConfig c = mle::decode_mfma_pick_segs(mc, s, K);
     if (!mle::decode_mfma_fits(c, mc, 1, K))
       return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + ": K too large for the MFMA decode");
     mle::LinearSegs chunk = s;

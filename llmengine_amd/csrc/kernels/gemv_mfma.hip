@@ -662,9 +662,16 @@ struct RowsArgs {
   int count;
 };
 
-template <int MT, int NG, int NPH, int PHB, int NBUF, int RING, int WG>
+// MODE 1 (SwiGLU): groups [0, NG/2) of a workgroup hold rows of the gate weight
+// (seg[0]) and groups [NG/2, NG) the same rows of the up weight (seg[1]); the
+// first wave of each gate group writes silu(gate) * up to seg[0].y.  grp_end[0]
+// then counts the gate weight's groups.
+template <int MT, int NG, int NPH, int PHB, int NBUF, int RING, int WG, int MODE>
 __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
     const float* __restrict__ x, const RowsArgs args, int M, int K) {
+  constexpr bool kSwi = MODE == 1;
+  static_assert(!kSwi || NG % 2 == 0, "SwiGLU pairs gate and up groups");
+  constexpr int NGH = kSwi ? NG / 2 : NG;  // output groups per workgroup
   constexpr int W = WG * NG;
   constexpr int NT = 64 * W;
   constexpr int P = Cols<MT>::P;
@@ -692,11 +699,12 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
   const int KP = (KB + 1) >> 1;
   // This wave's group: global index -> segment (uniform selects: no indexing
   // into the argument) and its group within the segment's weight.
-  const unsigned grp = blockIdx.x * NG + lg;
-  const int si = (args.count > 1 && grp >= args.grp_end[0])
-                     ? ((args.count > 2 && grp >= args.grp_end[1]) ? 2 : 1)
-                     : 0;
-  const unsigned grp0 = si == 0 ? 0u : si == 1 ? args.grp_end[0] : args.grp_end[1];
+  const unsigned grp = blockIdx.x * NGH + (kSwi ? lg % NGH : lg);
+  const int si = kSwi ? (lg >= NGH ? 1 : 0)
+                      : (args.count > 1 && grp >= args.grp_end[0])
+                            ? ((args.count > 2 && grp >= args.grp_end[1]) ? 2 : 1)
+                            : 0;
+  const unsigned grp0 = kSwi || si == 0 ? 0u : si == 1 ? args.grp_end[0] : args.grp_end[1];
   const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
   const void* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
   const int bias_bf16 =
@@ -704,8 +712,9 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
   float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
   const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
   const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
-  const unsigned grp_total =
-      args.count == 1 ? args.grp_end[0] : args.count == 2 ? args.grp_end[1] : args.grp_end[2];
+  const unsigned grp_total = kSwi || args.count == 1 ? args.grp_end[0]
+                             : args.count == 2      ? args.grp_end[1]
+                                                    : args.grp_end[2];
   const bool live_g = grp < grp_total;
   const int64_t rg = live_g ? (int64_t)(grp - grp0) : 0;  // group within the segment's weight
   const int64_t rgc = rg;
@@ -877,24 +886,32 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
   red[wave][4 * g + 2][r16] = acc.z;
   red[wave][4 * g + 3][r16] = acc.w;
   __syncthreads();
-  if (qw != 0 || !live_g) return;
+  if (qw != 0 || !live_g || (kSwi && lg >= NGH)) return;
+  // The sum of group g's waves for (token m, row rr), in wave order.
+  auto group_sum = [&](int gl, int m, int rr) {
+    const int c0 = m, c1 = (MT + m) & 15, c2 = (2 * MT + m) & 15;
+    float t = 0.0f;
+#pragma unroll
+    for (int q4 = 0; q4 < WG; ++q4) {
+      const int wv = WG * gl + q4;
+      float s = red[wv][rr][c0];
+      if (c1 != c0) s += red[wv][rr][c1];
+      if (c2 != c0 && c2 != c1) s += red[wv][rr][c2];
+      t = q4 == 0 ? s : t + s;
+    }
+    return t;
+  };
 #pragma unroll
   for (int o = 0; o < OPL; ++o) {
     const int idx = lane + 64 * o;  // (token m, row rr), rows fastest
     const int m = idx >> 4, rr = idx & 15;
     const int64_t n = rg * 16 + rr;
     if (idx >= OUTS || m >= M || n >= N) continue;
-    const int c0 = m, c1 = (MT + m) & 15, c2 = (2 * MT + m) & 15;
-    float t = 0.0f;
-#pragma unroll
-    for (int q4 = 0; q4 < WG; ++q4) {
-      const int wv = WG * lg + q4;
-      float s = red[wv][rr][c0];
-      if (c1 != c0) s += red[wv][rr][c1];
-      if (c2 != c0 && c2 != c1) s += red[wv][rr][c2];
-      t = q4 == 0 ? s : t + s;
-    }
-    y[(int64_t)m * N + n] = t + (bias ? bias_at(bias, bias_bf16, n) : 0.0f);
+    const float t = group_sum(lg, m, rr);
+    if constexpr (kSwi)
+      y[(int64_t)m * N + n] = silu_mul(t, group_sum(lg + NGH, m, rr));
+    else
+      y[(int64_t)m * N + n] = t + (bias ? bias_at(bias, bias_bf16, n) : 0.0f);
   }
 }
 
@@ -906,14 +923,15 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
 //    buffers (2 x 50 KB; 0.95-0.97x the 64-block single buffer), 2 chunks in
 //    flight (0.98-0.99x one chunk on the Llama qkv / gate shapes; 3 or 4 chunks
 //    1.01-1.12x).
-template <int MT, int NG, int WG, int PHB, int NBUF, int RING>
+template <int MT, int NG, int WG, int PHB, int NBUF, int RING, int MODE = 0>
 hipError_t launch_rows_k(const float* x, const RowsArgs& a, int M, int K, hipStream_t stream) {
-  const unsigned groups = a.grp_end[a.count - 1];
-  const dim3 grid((groups + NG - 1) / NG), block(64 * WG * NG);
+  constexpr int NGH = MODE == 1 ? NG / 2 : NG;  // output groups per workgroup
+  const unsigned groups = MODE == 1 ? a.grp_end[0] : a.grp_end[a.count - 1];
+  const dim3 grid((groups + NGH - 1) / NGH), block(64 * WG * NG);
   const int nph = (K / kBlockElems + PHB - 1) / PHB;
-#define MLE_ROWS(NPH)                                                                        \
-  hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, NPH, PHB, NBUF, RING, WG>), grid, block, \
-                     0, stream, x, a, M, K)
+#define MLE_ROWS(NPH)                                                                         \
+  hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, NPH, PHB, NBUF, RING, WG, MODE>), grid,   \
+                     block, 0, stream, x, a, M, K)
   switch (nph) {
     case 1: MLE_ROWS(1); break;
     case 2: if constexpr (PHB < 128) MLE_ROWS(2); else return hipErrorInvalidValue; break;
@@ -925,16 +943,19 @@ hipError_t launch_rows_k(const float* x, const RowsArgs& a, int M, int K, hipStr
   return hipGetLastError();
 }
 
-// The 16-row groups of 1-3 output segments, numbered segment after segment.
+// The 16-row groups of 1-3 output segments, numbered segment after segment
+// (SwiGLU: the gate weight's groups; the up weight has the same rows).
 RowsArgs rows_args(const LinearSegs& s) {
   RowsArgs a{};
+  const bool swi = s.mode == Epilogue::kSwiGLU;
   unsigned end = 0;
   for (int i = 0; i < 3; ++i) {
     a.seg[i] = s.seg[i];
-    if (i < s.count) end += (unsigned)((s.seg[i].N + kTileRows - 1) / kTileRows);
+    if (i < (swi ? 1 : s.count)) end += (unsigned)((s.seg[i].N + kTileRows - 1) / kTileRows);
     a.grp_end[i] = end;
   }
-  a.count = s.count;
+  if (swi) a.seg[1].N = s.seg[0].N;
+  a.count = swi ? 1 : s.count;
   return a;
 }
 
@@ -942,6 +963,16 @@ template <int MT>
 hipError_t launch_rows(const float* x, const LinearSegs& s, int M, int K, hipStream_t stream) {
   const RowsArgs a = rows_args(s);
   const int64_t G = a.grp_end[a.count - 1];
+  if (s.mode == Epilogue::kSwiGLU) {
+    // Gate and up groups of the same rows side by side, two waves each: 2-4 pairs
+    // per workgroup (8-16 waves) for 512-1024 groups per weight on 256 CUs.
+    switch (rows_groups_per_workgroup(G)) {
+      case 2: return launch_rows_k<MT, 4, 2, MT == 4 ? 128 : 32, MT == 4 ? 1 : 2, 2, 1>(x, a, M, K, stream);
+      case 3: return launch_rows_k<MT, 6, 2, MT == 4 ? 128 : 32, MT == 4 ? 1 : 2, 2, 1>(x, a, M, K, stream);
+      case 4: return launch_rows_k<MT, 8, 2, MT == 4 ? 128 : 32, MT == 4 ? 1 : 2, 2, 1>(x, a, M, K, stream);
+    }
+    return hipErrorInvalidValue;
+  }
   if constexpr (MT == 4) {
     switch (rows_groups_per_workgroup(G)) {
       case 1: return launch_rows_k<4, 1, 16, 128, 1, 1>(x, a, M, K, stream);
@@ -1085,15 +1116,34 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
   return c;
 }
 
+DecodeMfmaConfig decode_mfma_pick_segs(int M, const LinearSegs& s, int K) {
+  int total_n = 0;
+  for (int i = 0; i < s.count; ++i) total_n += s.seg[i].N;
+  DecodeMfmaConfig c = decode_mfma_pick(M, total_n, K, s.layout);
+  if (s.mode == Epilogue::kSwiGLU && s.layout == WeightLayout::kTiled) {
+    // Measured on MI355X (Llama gate/up, 2 x 11008 x 4096, tiled weights): see
+    // the row-range launch shapes above.
+    const int64_t G = ((int64_t)s.seg[0].N + kTileRows - 1) / kTileRows;
+    const bool k_ok = K % 64 == 0 && K >= 2048 && K <= 4096;
+    c.rows = k_ok && (c.mt == 4 || c.mt == 8) && G >= 512 && G <= 1024 ? 1 : 0;
+  }
+  return c;
+}
+
 SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K) {
   return decode_mfma_workspace_segs(c, single(nullptr, nullptr, nullptr, N), K);
 }
 
 // The launches the row-range kernel takes: 1-3 plain outputs on tiled weights.
 static bool rows_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
-  if (c.rows != 1 || s.count < 1 || s.count > 3 || s.mode != Epilogue::kPlain ||
-      s.layout != WeightLayout::kTiled)
+  if (c.rows != 1 || s.count < 1 || s.count > 3 || s.layout != WeightLayout::kTiled)
     return false;
+  if (s.mode == Epilogue::kSwiGLU) {
+    // gate + up of 512-1024 row groups each, no bias (the SwiGLU launch has none)
+    const int64_t G = rows_args(s).grp_end[0];
+    return s.count == 2 && (c.mt == 4 || c.mt == 8) && G >= 512 && G <= 1024;
+  }
+  if (s.mode != Epilogue::kPlain) return false;
   // The launch shapes exist for these group counts (segments rounded up to whole
   // groups each, as the grid numbers them).
   const int64_t G = rows_args(s).grp_end[s.count - 1];

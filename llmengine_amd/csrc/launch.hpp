@@ -112,6 +112,10 @@ hipError_t launch_gemv_segs(const GemvConfig& cfg, const float* x, const LinearS
 
 DecodeMfmaConfig decode_mfma_pick(int M, int N, int K,
                                   WeightLayout layout = WeightLayout::kRaw);
+// The pick for a launch over segments: decode_mfma_pick on all output rows, and
+// for a gate/up SwiGLU pair on tiled weights the row-range kernel where it
+// applies (rows of 512-1024 groups per weight at 3-8 tokens, K 2048-4096).
+DecodeMfmaConfig decode_mfma_pick_segs(int M, const LinearSegs& s, int K);
 bool decode_mfma_config_valid(const DecodeMfmaConfig& c);
 SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K);
 // False when the shape's buffer offsets would not fit 32 bits (the caller then

@@ -57,6 +57,16 @@ def rows_decode(M, N, K):
     return ((four or 6 <= M <= 8) and 512 <= G <= 1024) or (four and 240 <= G <= 256)
 
 
+def rows_decode_swiglu(M, N, K):
+    """The C ABI's choice of the row-range MFMA decode for a tiled gate/up SwiGLU
+    launch (mle::decode_mfma_pick_segs): K 2048-4096 in steps of 64, 3-4 or 6-8
+    tokens, 512-1024 16-row groups per weight."""
+    G = (N + 15) // 16
+    if K % 64 != 0 or not 2048 <= K <= 4096:
+        return False
+    return (M in (3, 4) or 6 <= M <= 8) and 512 <= G <= 1024
+
+
 def rows_decode_multi(M, Ns, K):
     """rows_decode for a tiled multi-output Linear: the outputs' 16-row groups
     (each output rounded up to whole groups) counted together."""

@@ -18,6 +18,7 @@ import numpy as np
 import pytest
 
 from helpers import (assert_bitexact, empty_f32, note, rel_l2, rows_decode, rows_decode_multi,
+                     rows_decode_swiglu,
                      to_dev, to_host)
 from llmengine_amd import capi
 from llmengine_amd import synthetic as S
@@ -154,3 +155,45 @@ def test_rows_decode_multi_output(dev, orc, M, Ns, K):
         b = biases[i][rows] if biases[i] is not None else None
         assert rel_l2(got[:, rows], orc.linear(x, w_rows, b, M, rows.size, K)) <= DECODE_TOL, i
     assert capi.workspace_size(capi.OP_LINEAR_MULTI, M, list(Ns), K, True) == (0, 0)
+
+
+def silu_mul(g, u):
+    """silu(g) * u in the reference's operation order (cpu_kernels.cpp:848-858), fp32."""
+    g = np.asarray(g, np.float32)
+    return ((g / (np.float32(1.0) + np.exp(-g))) * u).astype(np.float32)
+
+
+# (M, N, K): gate/up pairs per workgroup 2 (G = 512), 3 (G = 513, 688) and 4
+# (G = 1024); MT 4 (K in one phase) and MT 8 (2-4 phases of 32 blocks).
+SWIGLU_CASES = [(4, 11008, 4096), (3, 8192, 2048), (4, 8200, 2112), (8, 11008, 4096),
+                (6, 16384, 3072), (7, 8200, 2112), (8, 8192, 2048)]
+
+
+@pytest.mark.parametrize("M,N,K", SWIGLU_CASES)
+def test_rows_decode_swiglu(dev, orc, M, N, K):
+    """The fused gate/up SwiGLU launch on the row-range decode (gate and up groups of
+    the same rows in one workgroup, silu(gate) * up in its epilogue): against the
+    oracle at the decode bar on sampled rows (each projection by the reference's
+    sgemm_nt, then its silu * up order), within 1e-6 of the raw SwiGLU launch, which
+    runs the split-K kernel, repeatable bit for bit, and with no workspace."""
+    import torch
+    assert rows_decode_swiglu(M, N, K)
+    note(f"rows decode swiglu M={M} N={N} K={K}")
+    wg, wu = weight(N + K + 1, N, K), weight(N + K + 2, N, K)
+    x = S.activations(K + 7 * M, (M, K))
+    dx, dwg, dwu = to_dev(x, dev), to_dev(wg, dev), to_dev(wu, dev)
+    tg, tu = tiled_dev(dwg, N, K, dev), tiled_dev(dwu, N, K, dev)
+    y_t, y_t2, y_raw = (empty_f32((M, N), dev) for _ in range(3))
+    capi.linear_swiglu_tiled(dx, tg, tu, y_t, M, N, K)
+    capi.linear_swiglu_tiled(dx, tg, tu, y_t2, M, N, K)
+    capi.linear_swiglu(dx, dwg, dwu, y_raw, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(y_t, y_t2)  # deterministic
+    got = to_host(y_t)
+    close_to_raw(got, to_host(y_raw), "swiglu rows vs split-K")
+    rows = np.array(sorted({0, 1, N // 2, N - 17, N - 1}))
+    pick = lambda w: np.ascontiguousarray(w.reshape(N, -1)[rows]).reshape(-1)
+    want = silu_mul(orc.linear(x, pick(wg), None, M, rows.size, K),
+                    orc.linear(x, pick(wu), None, M, rows.size, K))
+    assert rel_l2(got[:, rows], want) <= DECODE_TOL
+    assert capi.workspace_size(capi.OP_LINEAR_SWIGLU, M, [N, N], K, True) == (0, 0)

@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 
 from helpers import (assert_bitexact, empty_f32, note, rel_l2, rows_decode, rows_decode_multi,
+                     rows_decode_swiglu,
                      tile_ref, to_dev, to_host)
 from llmengine_amd import capi
 from llmengine_amd import synthetic as S
@@ -190,8 +191,9 @@ def test_swiglu_tiled(dev, orc, M, N, K):
     capi.linear_swiglu(dx, dwg, dwu, y_raw, M, N, K)
     capi.linear_swiglu_tiled(dx, tg, tu, y_t, M, N, K)
     got = to_host(y_t)
-    # raw SwiGLU runs its GEMV for M == 1 only; tiled, its GEMV as tiled_gemv says
-    exact = M > 1 and not tiled_gemv(M, N, K)
+    # raw SwiGLU runs its GEMV for M == 1 only; tiled, its GEMV as tiled_gemv says,
+    # and the row-range decode where rows_decode_swiglu says
+    exact = M > 1 and not tiled_gemv(M, N, K) and not rows_decode_swiglu(M, N, K)
     same_or_close(got, to_host(y_raw), exact, "swiglu tiled vs raw")
     rows = np.array(sorted({0, M // 2, M - 1}))
     want = silu_mul(orc.linear(x[rows], wg, None, rows.size, N, K),
@@ -241,7 +243,8 @@ def test_llama_decode_set_tiled(dev, M):
     """The four Llama-7B projection shapes of the decode benchmark, tiled against
     raw on the fused qkv, the fused gate/up and o_proj / down: bit for bit on the
     split-K MFMA decode (M = 4, 8), within 1e-6 on the tiled GEMV (M = 1, 2) and on
-    the row-range decode (o_proj at M = 4, the fused q/k/v at M = 4 and 8)."""
+    the row-range decode (o_proj at M = 4, the fused q/k/v and gate/up at M = 4 and
+    8)."""
     import torch
     K, H, F = 4096, 4096, 11008
     note(f"llama decode set tiled M={M}")
@@ -270,8 +273,10 @@ def test_llama_decode_set_tiled(dev, M):
     for a, b, what in [(ys_r[0], ys_t[0], "q"), (ys_r[1], ys_t[1], "k"),
                        (ys_r[2], ys_t[2], "v"), (g_r, g_t, "gate/up"), (o_r, o_t, "o"),
                        (d_r, d_t, "down")]:
-        # the row-range decode on tiled weights: o_proj at M = 4, q/k/v at M = 4 and 8
+        # the row-range decode on tiled weights: o_proj at M = 4, q/k/v and the
+        # gate/up SwiGLU at M = 4 and 8
         rows = (rows_decode(M, H, K) if what == "o" else
-                rows_decode_multi(M, (H, H, H), K) if what in "qkv" else False)
+                rows_decode_multi(M, (H, H, H), K) if what in "qkv" else
+                rows_decode_swiglu(M, F, K) if what == "gate/up" else False)
         exact = M > 2 and not rows
         same_or_close(to_host(b), to_host(a), exact, what)
