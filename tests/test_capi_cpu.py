@@ -112,6 +112,18 @@ def test_matmul_workspace_size():
     assert code == 1 and "count 1" in msg
 
 
+def test_swiglu_workspace_follows_the_decode_kernel():
+    """MLE_OP_LINEAR_SWIGLU: the tiled gate/up pair at 3-4 and 6-8 tokens on 512-1024
+    row groups per weight runs the row-range decode (no workspace); 5 tokens, raw
+    weights and 256-group weights run the split-K decode (partials and counters)."""
+    N, K = 11008, 4096
+    for M in (3, 4, 6, 8):
+        assert capi.workspace_size(capi.OP_LINEAR_SWIGLU, M, [N, N], K, True) == (0, 0), M
+    for M, n, tiled in ((5, N, True), (4, N, False), (8, N, False), (4, 4096, True)):
+        b, c = capi.workspace_size(capi.OP_LINEAR_SWIGLU, M, [n, n], K, tiled)
+        assert b > 0 and c > 0, (M, n, tiled)
+
+
 def test_probe_stream_read_validation_errors():
     st = capi.probe_stream_read_status
     code, msg = st(None, 64, FAKE, stream=0)
