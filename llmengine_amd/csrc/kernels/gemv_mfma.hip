@@ -666,10 +666,11 @@ struct RowsArgs {
 // (seg[0]) and groups [NG/2, NG) the same rows of the up weight (seg[1]); the
 // first wave of each gate group writes silu(gate) * up to seg[0].y.  grp_end[0]
 // then counts the gate weight's groups.
-template <int MT, int NG, int NPH, int PHB, int NBUF, int RING, int WG, int MODE>
+template <int MT, int NG, int NPH, int PHB, int NBUF, int RING, int WG, int MODE, int LAYOUT>
 __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
     const float* __restrict__ x, const RowsArgs args, int M, int K) {
   constexpr bool kSwi = MODE == 1;
+  constexpr bool kTiled = LAYOUT == int(WeightLayout::kTiled);
   static_assert(!kSwi || NG % 2 == 0, "SwiGLU pairs gate and up groups");
   constexpr int NGH = kSwi ? NG / 2 : NG;  // output groups per workgroup
   constexpr int W = WG * NG;
@@ -738,29 +739,63 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
     }
   };
 
-  // Quant slots (lane l: rows l % 16, quants 8 (l/16) .. +7 of both blocks of a
-  // pair) and scale dwords (lane l: pair l/16 of the chunk, row l % 16) of this
-  // wave's group; a group past N reads zeros (empty buffer).
+  // Tiled: quant slots (lane l: rows l % 16, quants 8 (l/16) .. +7 of both
+  // blocks of a pair) and scale dwords (lane l: pair l/16 of the chunk, row
+  // l % 16) of this wave's group; a group past N reads zeros (empty buffer).
+  // Raw (SwiGLU launches): a chunk's 8 blocks as two load sets of whole 34-byte
+  // blocks, lane (g, r16) taking block 4u + g of the chunk in row r16 of the
+  // group, as the split-K kernel's raw path (rows past N and blocks past K read
+  // as zeros).  A wave's chunks start 8-block (272-byte) steps apart, so each
+  // lane's 4-byte alignment phase is fixed.
   const uint8_t* qb = w + rgc * KP * kTilePieceBytes;
   const uint8_t* sb = w + G * KP * kTilePieceBytes + rgc * KP * kTileScaleBytes;
   const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qb, live_g ? (uint32_t)KP * kTilePieceBytes : 0u);
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, live_g ? (uint32_t)KP * kTileScaleBytes : 0u);
-  u32x4 tq[TC][4];
-  uint32_t ts[TC];
+  const uint32_t row_bytes = (uint32_t)KB * kBlockBytes;
+  const uint8_t* gbase = w + rgc * kTileRows * (int64_t)row_bytes;
+  const int64_t grows = live_g ? min((int64_t)kTileRows, (int64_t)N - rgc * kTileRows) : 0;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(gbase, (uint32_t)(grows * row_bytes));
+  const uint32_t lane_off = (uint32_t)r16 * row_bytes + (uint32_t)(2 * qw * WPP + g) * kBlockBytes;
+  const uint32_t mis = (uint32_t)(((uintptr_t)gbase + lane_off) & 2u);
+  const uint32_t voff = lane_off + mis;
+  const uint32_t uoff = lane_off + (mis ? 0u : 32u);
+  u32x4 tq[kTiled ? TC : 1][4];
+  uint32_t ts[kTiled ? TC : 1];
+  RawBlock wr[kTiled ? 1 : TC][2];
   auto load_chunk = [&](int cg) {  // chunk cg = ph * NCK + ck
     const int ph = cg / NCK, ck = cg % NCK;
     const int p0 = ph * PHP + qw * WPP + 4 * ck;
+    if constexpr (kTiled) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int pr = p0 + u;
-      uint32_t off = pr < KP ? (uint32_t)pr * kTilePieceBytes + (uint32_t)lane * 16 : 0x80000000u;
-      asm volatile("" : "+v"(off));
-      tq[cg][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, kNonTemporal);
+      for (int u = 0; u < 4; ++u) {
+        const int pr = p0 + u;
+        uint32_t off =
+            pr < KP ? (uint32_t)pr * kTilePieceBytes + (uint32_t)lane * 16 : 0x80000000u;
+        asm volatile("" : "+v"(off));
+        tq[cg][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, kNonTemporal);
+      }
+      const int ps = p0 + g;
+      uint32_t soff = ps < KP ? (uint32_t)ps * kTileScaleBytes + (uint32_t)r16 * 4 : 0x80000000u;
+      asm volatile("" : "+v"(soff));
+      ts[cg] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff, 0, 0);
+    } else {
+      // Blocks 2 p0 + 4u + g: the lane's own offset plus a wave-uniform 4-byte multiple.
+      const int bw = 2 * (p0 - qw * WPP);  // first block of the chunk past the wave's start
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bool live = 2 * p0 + 4 * u + g < KB;
+        const uint32_t soff = (uint32_t)(bw + 4 * u) * kBlockBytes;  // uniform
+        uint32_t v8 = live ? voff + soff : 0x80000000u;
+        uint32_t v2 = live ? uoff + soff : 0x80000000u;
+        asm volatile("" : "+v"(v8), "+v"(v2));
+        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, 0, 0);
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, 0, 0);
+        wr[cg][u].v0 = u32x4_a4{v0.x, v0.y, v0.z, v0.w};
+        wr[cg][u].v1 = u32x4_a4{v1.x, v1.y, v1.z, v1.w};
+        wr[cg][u].u = __builtin_amdgcn_raw_buffer_load_b16(wrs, v2, 0, 0);
+        wr[cg][u].mis = mis;
+      }
     }
-    const int ps = p0 + g;
-    uint32_t soff = ps < KP ? (uint32_t)ps * kTileScaleBytes + (uint32_t)r16 * 4 : 0x80000000u;
-    asm volatile("" : "+v"(soff));
-    ts[cg] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff, 0, 0);
   };
   load_x(0);  // first: the split waits only for these
   if constexpr (NBUF == 2) {
@@ -834,14 +869,36 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
 #pragma unroll
     for (int ck = 0; ck < NCK; ++ck) {
       const int cg = ph * NCK + ck;
-      scl[wave][2 * g][r16] = scale_to_f32_fast(ts[cg] & 0xffffu);
-      scl[wave][2 * g + 1][r16] = scale_to_f32_fast(ts[cg] >> 16);
       const int kb0 = 2 * (qw * WPP + 4 * ck);
+      if constexpr (kTiled) {
+        scl[wave][2 * g][r16] = scale_to_f32_fast(ts[cg] & 0xffffu);
+        scl[wave][2 * g + 1][r16] = scale_to_f32_fast(ts[cg] >> 16);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const u32x4 q = tq[cg][u];
-        block_mma(bb, 2 * u, kb0 + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
-        block_mma(bb, 2 * u + 1, kb0 + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
+        for (int u = 0; u < 4; ++u) {
+          const u32x4 q = tq[cg][u];
+          block_mma(bb, 2 * u, kb0 + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
+          block_mma(bb, 2 * u + 1, kb0 + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
+        }
+      } else {
+        // Realign, scales to (wave-private) LDS, in-register transpose into A
+        // fragments; blocks in K order into the even / odd accumulators, as above.
+        Block blk[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          blk[u] = finish_block(wr[cg][u]);
+          scl[wave][4 * u + g][r16] = scale_to_f32_fast(blk[u].scale_bits);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          uint32_t q[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) q[i] = blk[u].q[i];
+          transpose_chunks(q);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            block_mma(bb, 4 * u + j, kb0 + 4 * u + j, quants_to_bf16(q[2 * j], q[2 * j + 1]),
+                      accs[j & 1]);
+        }
       }
       if (cg + RING < TC) load_chunk(cg + RING);
     }
@@ -923,14 +980,15 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
 //    buffers (2 x 50 KB; 0.95-0.97x the 64-block single buffer), 2 chunks in
 //    flight (0.98-0.99x one chunk on the Llama qkv / gate shapes; 3 or 4 chunks
 //    1.01-1.12x).
-template <int MT, int NG, int WG, int PHB, int NBUF, int RING, int MODE = 0>
+template <int MT, int NG, int WG, int PHB, int NBUF, int RING, int MODE = 0,
+          int L = int(WeightLayout::kTiled)>
 hipError_t launch_rows_k(const float* x, const RowsArgs& a, int M, int K, hipStream_t stream) {
   constexpr int NGH = MODE == 1 ? NG / 2 : NG;  // output groups per workgroup
   const unsigned groups = MODE == 1 ? a.grp_end[0] : a.grp_end[a.count - 1];
   const dim3 grid((groups + NGH - 1) / NGH), block(64 * WG * NG);
   const int nph = (K / kBlockElems + PHB - 1) / PHB;
 #define MLE_ROWS(NPH)                                                                         \
-  hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, NPH, PHB, NBUF, RING, WG, MODE>), grid,   \
+  hipLaunchKernelGGL((gemv_mfma_rows_kernel<MT, NG, NPH, PHB, NBUF, RING, WG, MODE, L>), grid, \
                      block, 0, stream, x, a, M, K)
   switch (nph) {
     case 1: MLE_ROWS(1); break;
@@ -965,11 +1023,18 @@ hipError_t launch_rows(const float* x, const LinearSegs& s, int M, int K, hipStr
   const int64_t G = a.grp_end[a.count - 1];
   if (s.mode == Epilogue::kSwiGLU) {
     // Gate and up groups of the same rows side by side, two waves each: 2-4 pairs
-    // per workgroup (8-16 waves) for 512-1024 groups per weight on 256 CUs.
+    // per workgroup (8-16 waves) for 512-1024 groups per weight on 256 CUs; tiled
+    // or raw weights.
+    constexpr int PB = MT == 4 ? 128 : 32, NB = MT == 4 ? 1 : 2;
+    constexpr int T = int(WeightLayout::kTiled), R = int(WeightLayout::kRaw);
+    const bool tiled = s.layout == WeightLayout::kTiled;
     switch (rows_groups_per_workgroup(G)) {
-      case 2: return launch_rows_k<MT, 4, 2, MT == 4 ? 128 : 32, MT == 4 ? 1 : 2, 2, 1>(x, a, M, K, stream);
-      case 3: return launch_rows_k<MT, 6, 2, MT == 4 ? 128 : 32, MT == 4 ? 1 : 2, 2, 1>(x, a, M, K, stream);
-      case 4: return launch_rows_k<MT, 8, 2, MT == 4 ? 128 : 32, MT == 4 ? 1 : 2, 2, 1>(x, a, M, K, stream);
+      case 2: return tiled ? launch_rows_k<MT, 4, 2, PB, NB, 2, 1, T>(x, a, M, K, stream)
+                           : launch_rows_k<MT, 4, 2, PB, NB, 2, 1, R>(x, a, M, K, stream);
+      case 3: return tiled ? launch_rows_k<MT, 6, 2, PB, NB, 2, 1, T>(x, a, M, K, stream)
+                           : launch_rows_k<MT, 6, 2, PB, NB, 2, 1, R>(x, a, M, K, stream);
+      case 4: return tiled ? launch_rows_k<MT, 8, 2, PB, NB, 2, 1, T>(x, a, M, K, stream)
+                           : launch_rows_k<MT, 8, 2, PB, NB, 2, 1, R>(x, a, M, K, stream);
     }
     return hipErrorInvalidValue;
   }
@@ -1120,9 +1185,9 @@ DecodeMfmaConfig decode_mfma_pick_segs(int M, const LinearSegs& s, int K) {
   int total_n = 0;
   for (int i = 0; i < s.count; ++i) total_n += s.seg[i].N;
   DecodeMfmaConfig c = decode_mfma_pick(M, total_n, K, s.layout);
-  if (s.mode == Epilogue::kSwiGLU && s.layout == WeightLayout::kTiled) {
-    // Measured on MI355X (Llama gate/up, 2 x 11008 x 4096, tiled weights): see
-    // the row-range launch shapes above.
+  if (s.mode == Epilogue::kSwiGLU) {
+    // Measured on MI355X (Llama gate/up, 2 x 11008 x 4096, tiled and raw weights):
+    // see the row-range launch shapes above.
     const int64_t G = ((int64_t)s.seg[0].N + kTileRows - 1) / kTileRows;
     const bool k_ok = K % 64 == 0 && K >= 2048 && K <= 4096;
     c.rows = k_ok && (c.mt == 4 || c.mt == 8) && G >= 512 && G <= 1024 ? 1 : 0;
@@ -1136,14 +1201,13 @@ SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K) {
 
 // The launches the row-range kernel takes: 1-3 plain outputs on tiled weights.
 static bool rows_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
-  if (c.rows != 1 || s.count < 1 || s.count > 3 || s.layout != WeightLayout::kTiled)
-    return false;
-  if (s.mode == Epilogue::kSwiGLU) {
+  if (c.rows != 1 || s.count < 1 || s.count > 3) return false;
+  if (s.mode == Epilogue::kSwiGLU) {  // tiled or raw weights
     // gate + up of 512-1024 row groups each, no bias (the SwiGLU launch has none)
     const int64_t G = rows_args(s).grp_end[0];
     return s.count == 2 && (c.mt == 4 || c.mt == 8) && G >= 512 && G <= 1024;
   }
-  if (s.mode != Epilogue::kPlain) return false;
+  if (s.mode != Epilogue::kPlain || s.layout != WeightLayout::kTiled) return false;
   // The launch shapes exist for these group counts (segments rounded up to whole
   // groups each, as the grid numbers them).
   const int64_t G = rows_args(s).grp_end[s.count - 1];

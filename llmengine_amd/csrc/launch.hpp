@@ -113,7 +113,7 @@ hipError_t launch_gemv_segs(const GemvConfig& cfg, const float* x, const LinearS
 DecodeMfmaConfig decode_mfma_pick(int M, int N, int K,
                                   WeightLayout layout = WeightLayout::kRaw);
 // The pick for a launch over segments: decode_mfma_pick on all output rows, and
-// for a gate/up SwiGLU pair on tiled weights the row-range kernel where it
+// for a gate/up SwiGLU pair (tiled or raw weights) the row-range kernel where it
 // applies (rows of 512-1024 groups per weight at 3-8 tokens, K 2048-4096).
 DecodeMfmaConfig decode_mfma_pick_segs(int M, const LinearSegs& s, int K);
 bool decode_mfma_config_valid(const DecodeMfmaConfig& c);

@@ -113,13 +113,14 @@ def test_matmul_workspace_size():
 
 
 def test_swiglu_workspace_follows_the_decode_kernel():
-    """MLE_OP_LINEAR_SWIGLU: the tiled gate/up pair at 3-4 and 6-8 tokens on 512-1024
-    row groups per weight runs the row-range decode (no workspace); 5 tokens, raw
-    weights and 256-group weights run the split-K decode (partials and counters)."""
+    """MLE_OP_LINEAR_SWIGLU: the gate/up pair (tiled or raw) at 3-4 and 6-8 tokens on
+    512-1024 row groups per weight runs the row-range decode (no workspace); 5 tokens
+    and 256-group weights run the split-K decode (partials and counters)."""
     N, K = 11008, 4096
     for M in (3, 4, 6, 8):
-        assert capi.workspace_size(capi.OP_LINEAR_SWIGLU, M, [N, N], K, True) == (0, 0), M
-    for M, n, tiled in ((5, N, True), (4, N, False), (8, N, False), (4, 4096, True)):
+        for tiled in (True, False):
+            assert capi.workspace_size(capi.OP_LINEAR_SWIGLU, M, [N, N], K, tiled) == (0, 0), M
+    for M, n, tiled in ((5, N, True), (5, N, False), (4, 4096, True), (8, 4096, False)):
         b, c = capi.workspace_size(capi.OP_LINEAR_SWIGLU, M, [n, n], K, tiled)
         assert b > 0 and c > 0, (M, n, tiled)
 
@@ -358,8 +359,9 @@ def test_workspace_size_matches_launch_plan():
     b3, c3 = ws(capi.OP_LINEAR_MULTI, 8, [4096, 4096, 4096], 4096)
     b1, c1 = ws(capi.OP_LINEAR, 8, [12288], 4096)
     assert b3 > 0 and c3 > 0 and b1 > 0
-    bs, cs = ws(capi.OP_LINEAR_SWIGLU, 4, [11008, 11008], 4096)
+    bs, cs = ws(capi.OP_LINEAR_SWIGLU, 5, [11008, 11008], 4096)     # split-K SwiGLU
     assert bs > 0 and cs > 0
+    assert ws(capi.OP_LINEAR_SWIGLU, 4, [11008, 11008], 4096) == (0, 0)  # row-range SwiGLU
     # chunks of 16 tokens share one workspace: the need is the largest chunk's
     assert ws(capi.OP_LINEAR, 40, [4096], 11008) == ws(capi.OP_LINEAR, 16, [4096], 11008)
     code, msg, _, _ = capi.workspace_size_status(capi.OP_LINEAR, 1, [64], 48)

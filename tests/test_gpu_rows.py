@@ -172,10 +172,11 @@ SWIGLU_CASES = [(4, 11008, 4096), (3, 8192, 2048), (4, 8200, 2112), (8, 11008, 4
 @pytest.mark.parametrize("M,N,K", SWIGLU_CASES)
 def test_rows_decode_swiglu(dev, orc, M, N, K):
     """The fused gate/up SwiGLU launch on the row-range decode (gate and up groups of
-    the same rows in one workgroup, silu(gate) * up in its epilogue): against the
-    oracle at the decode bar on sampled rows (each projection by the reference's
-    sgemm_nt, then its silu * up order), within 1e-6 of the raw SwiGLU launch, which
-    runs the split-K kernel, repeatable bit for bit, and with no workspace."""
+    the same rows in one workgroup, silu(gate) * up in its epilogue), on tiled and on
+    raw weights: against the oracle at the decode bar on sampled rows (each projection
+    by the reference's sgemm_nt, then its silu * up order), raw equal to tiled bit for
+    bit (whole raw blocks per lane, transposed into the tiled layout's fragments, the
+    same K order), repeatable bit for bit, and with no workspace on either layout."""
     import torch
     assert rows_decode_swiglu(M, N, K)
     note(f"rows decode swiglu M={M} N={N} K={K}")
@@ -190,10 +191,11 @@ def test_rows_decode_swiglu(dev, orc, M, N, K):
     torch.cuda.synchronize()
     assert torch.equal(y_t, y_t2)  # deterministic
     got = to_host(y_t)
-    close_to_raw(got, to_host(y_raw), "swiglu rows vs split-K")
+    assert_bitexact(to_host(y_raw), got, "swiglu rows raw vs tiled")
     rows = np.array(sorted({0, 1, N // 2, N - 17, N - 1}))
     pick = lambda w: np.ascontiguousarray(w.reshape(N, -1)[rows]).reshape(-1)
     want = silu_mul(orc.linear(x, pick(wg), None, M, rows.size, K),
                     orc.linear(x, pick(wu), None, M, rows.size, K))
     assert rel_l2(got[:, rows], want) <= DECODE_TOL
-    assert capi.workspace_size(capi.OP_LINEAR_SWIGLU, M, [N, N], K, True) == (0, 0)
+    for tiled in (True, False):
+        assert capi.workspace_size(capi.OP_LINEAR_SWIGLU, M, [N, N], K, tiled) == (0, 0)
