@@ -9,11 +9,15 @@
  *     the raw GGUF block_q8_0 stream: per 34-byte block a little-endian binary16
  *     scale d followed by 32 int8 quants q; value = d * q.
  *   - Work is enqueued on `stream` (NULL = the default stream) and is
- *     asynchronous; the caller synchronises.  The Linear entry points keep one
- *     split-K workspace (partial sums + tile counters) per (device, stream).
- *     A caller that must not allocate on its hot path reserves it beforehand
- *     (mle_q8_0_workspace_size + mle_workspace_reserve); otherwise it is
- *     allocated with hipMalloc on first need.  It only grows: a buffer too
+ *     asynchronous; the caller synchronises.  The Linear entry points keep a
+ *     split-K workspace (partial sums + tile counters) per (device, stream),
+ *     and a second one per (device, stream) for calls made while the stream
+ *     is capturing a HIP graph, so a captured call never shares buffers with
+ *     eager calls (graphs captured on one stream share theirs: replays of two
+ *     such graphs must not overlap in time).  A caller that must not allocate
+ *     on its hot path reserves both beforehand (mle_q8_0_workspace_size +
+ *     mle_workspace_reserve), and capture requires it; otherwise the eager one
+ *     is allocated with hipMalloc on first need.  It only grows: a buffer too
  *     small for a call is replaced by one of max(need, 2 x capacity) bytes and
  *     the old one is kept (launches already enqueued, or captured in a HIP
  *     graph, still use it), so growth never synchronises; everything lives
@@ -283,11 +287,14 @@ int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const*
  *   nothing.  Errors: NULL outputs / N, M or K or an
  *   N <= 0, a bad count or op -> InvalidArgument; K % 32 != 0 (MatMul: or
  *   N % 32 != 0) -> Unsupported.
- * mle_workspace_reserve: grows the workspace of (current device, stream) to
- *   hold at least `bytes` and `counters` (a no-op when it already does); later
- *   calls within those sizes allocate and synchronise nothing.
- * mle_workspace_info: capacity of (current device, stream)'s workspace and the
- *   number of (re)allocations it has had (0 / 0 / 0 when it has none yet).
+ * mle_workspace_reserve: grows the eager and the graph workspace of (current
+ *   device, stream) to hold at least `bytes` and `counters` each (a no-op when
+ *   they already do); later calls within those sizes allocate and synchronise
+ *   nothing, eager or captured.  A call captured on a stream whose graph
+ *   workspace is too small returns RuntimeError ("reserve it before capture").
+ * mle_workspace_info: capacity of (current device, stream)'s eager workspace
+ *   and the number of (re)allocations it has had (0 / 0 / 0 when it has none
+ *   yet).
  * mle_workspace_plan_growth (test hook): the growth rule, applied to
  *   capacities and a need without allocating: returns 1 and the new capacities
  *   when the need does not fit (a buffer too small takes max(need,
@@ -318,7 +325,9 @@ int mle_workspace_plan_growth(size_t cap_bytes, size_t cap_counters, size_t need
  * any launch (every benchmark shape fits: prefill [512 x 4096 x 11008] takes
  * 28 MB).  All calls on one GPU share the array: calls that overlap in time on
  * one GPU (different streams, or threads without ordering) race and give wrong
- * results; calls ordered on one stream do not.
+ * results; calls ordered on one stream do not.  The first call on a GPU clears
+ * the array's counters with a kernel on `stream`; it returns RuntimeError if
+ * `stream` is capturing a graph (make one call outside capture first).
  */
 int mle_q8_0_linear_noalloc(const float* x, const uint8_t* w_q8_0, const float* bias,
                             float* y, int M, int N, int K, hipStream_t stream);

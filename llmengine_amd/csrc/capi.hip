@@ -15,6 +15,7 @@
 #include <vector>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <utility>
 
 #include "../../include/mle_q8_0.h"
@@ -89,17 +90,23 @@ int validate_linear(const float* x, const uint8_t* w, const void* bias, float* y
   return MLE_OK;
 }
 
-// Workspace of the MFMA paths, one per (device, stream): split-K partial sums
-// and tile counters, and the prefill GEMM's bf16 copy of X.  Calls on one
-// stream run in order, so the workspace is never used by two launches at once.
-// It is reserved ahead of the hot path (mle_workspace_reserve, which
-// minillm::HipExecutor calls from compile() and tile_weights() for its graph's
-// largest shapes), or allocated on the first call that needs it.  A buffer that
-// must grow is replaced by a new one of at least twice its capacity; the old
-// one is kept (launches already enqueued on the stream, or captured in a HIP
-// graph, may still use it), so growth never synchronises, and the kept buffers
-// add up to less than the live capacity.  Everything lives until the process
-// ends.
+// Workspace of the MFMA paths, two per (device, stream): split-K partial sums
+// and tile counters, and the prefill GEMM's bf16 copy of X.  Eager calls use
+// the stream's eager workspace; calls made while the stream is capturing a HIP
+// graph use its graph workspace, which no eager call touches, so a graph
+// replayed on any stream cannot race eager calls on the capturing stream.
+// Eager calls on one stream run in order, so the eager workspace is never used
+// by two launches at once; graphs captured on one stream share the graph
+// workspace, so their replays must not overlap each other.  Both are reserved
+// ahead of the hot path (mle_workspace_reserve, which minillm::HipExecutor
+// calls from compile() and tile_weights() for its graph's largest shapes); the
+// eager one is otherwise allocated on the first call that needs it, while the
+// graph one is never allocated during capture (a capture that needs more than
+// the reservation is refused).  A buffer that must grow is replaced by a new
+// one of at least twice its capacity; the old one is kept (launches already
+// enqueued on the stream, or captured in a HIP graph, may still use it), so
+// growth never synchronises, and the kept buffers add up to less than the live
+// capacity.  Everything lives until the process ends.
 struct StreamWorkspace {
   uint8_t* buf = nullptr;  // partial sums, then scratch
   size_t buf_cap = 0;      // bytes
@@ -109,7 +116,13 @@ struct StreamWorkspace {
   std::vector<void*> retired;  // replaced buffers, never freed (see above)
 };
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, StreamWorkspace> g_ws;
+// Key: (device, stream, graph workspace?).
+std::map<std::tuple<int, hipStream_t, bool>, StreamWorkspace> g_ws;
+
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone;
+}
 
 constexpr size_t kMinWorkspaceBytes = size_t(4) << 20;
 constexpr size_t kMinWorkspaceCounters = 4096;
@@ -134,15 +147,15 @@ size_t need_bytes(const mle::SplitKNeed& need) {
   return (need.partial_floats * sizeof(float) + 255) / 256 * 256 + need.scratch_bytes;
 }
 
-int ensure_workspace(size_t bytes, size_t counters, hipStream_t stream, StreamWorkspace** out) {
+int ensure_workspace(size_t bytes, size_t counters, hipStream_t stream, bool graph,
+                     StreamWorkspace** out) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return check_launch(err, "hip Q8_0 workspace");
-  StreamWorkspace& e = g_ws[{dev, stream}];
+  StreamWorkspace& e = g_ws[{dev, stream, graph}];
   size_t nb = 0, nc = 0;
   if (plan_growth(e.buf_cap, e.counter_cap, bytes, counters, &nb, &nc)) {
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+    if (stream_capturing(stream))
       return fail(MLE_RUNTIME_ERROR,
                   "hip Q8_0 workspace: this call needs " + std::to_string(bytes) + " bytes and " +
                       std::to_string(counters) +
@@ -186,7 +199,7 @@ int get_workspace(const mle::SplitKNeed& need, hipStream_t stream, mle::SplitKWo
   const size_t partial_bytes = (need.partial_floats * sizeof(float) + 255) / 256 * 256;
   std::unique_lock<std::mutex> lock(g_ws_mu);
   StreamWorkspace* e = nullptr;
-  MLE_TRY(ensure_workspace(bytes, need.counters, stream, &e));
+  MLE_TRY(ensure_workspace(bytes, need.counters, stream, stream_capturing(stream), &e));
   out->partials = reinterpret_cast<float*>(e->buf);
   out->counters = e->counters;
   out->scratch = need.scratch_bytes ? e->buf + partial_bytes : nullptr;
@@ -465,7 +478,10 @@ std::map<int, NoAllocScratch> g_noalloc;  // device -> its scratch
 
 // Device address of `scratch` on the current device; on the first call there,
 // its counters are cleared on `stream` (a fill kernel, enqueued before the
-// caller's launch).  Later launches leave the counters at zero.
+// caller's launch).  Later launches leave the counters at zero.  That first
+// call is refused while `stream` is capturing a graph: the clearing would
+// become a node of the graph and the eager calls after it would find the
+// counters uncleared.
 int noalloc_scratch(hipStream_t stream, uint8_t** base) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
@@ -473,6 +489,10 @@ int noalloc_scratch(hipStream_t stream, uint8_t** base) {
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   auto it = g_noalloc.find(dev);
   if (it == g_noalloc.end()) {
+    if (stream_capturing(stream))
+      return fail(MLE_RUNTIME_ERROR,
+                  "hip linear_noalloc: the first call on a device clears the scratch "
+                  "counters and must not be captured; make one call outside capture first");
     void* p = nullptr;
     err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (err != hipSuccess || p == nullptr)
@@ -709,7 +729,8 @@ int mle_workspace_reserve(size_t bytes, size_t counters, hipStream_t stream) {
   if (bytes == 0 && counters == 0) return ok();
   std::lock_guard<std::mutex> lock(g_ws_mu);
   StreamWorkspace* e = nullptr;
-  MLE_TRY(ensure_workspace(bytes, counters, stream, &e));
+  MLE_TRY(ensure_workspace(bytes, counters, stream, false, &e));
+  MLE_TRY(ensure_workspace(bytes, counters, stream, true, &e));
   return ok();
 }
 
@@ -721,7 +742,7 @@ int mle_workspace_info(hipStream_t stream, size_t* bytes, size_t* counters,
   const hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return check_launch(err, "hip workspace_info");
   std::lock_guard<std::mutex> lock(g_ws_mu);
-  auto it = g_ws.find({dev, stream});
+  auto it = g_ws.find({dev, stream, false});
   *bytes = it == g_ws.end() ? 0 : it->second.buf_cap;
   *counters = it == g_ws.end() ? 0 : it->second.counter_cap;
   *generation = it == g_ws.end() ? 0 : it->second.generation;

@@ -468,6 +468,13 @@ expected<RawBytes, Status> tensor_bytes(const std::string& path, const GGUFFile&
 Status load_tensor(const std::string& path, const GGUFFile& file, const GGUFTensorInfo& ti,
                    Tensor& tensor, const MappedFile* map) {
   if (!tensor.is_allocated()) return Status::runtime_error("tensor not allocated: " + tensor.name());
+  // Storage re-tiled in place (HipExecutor::tile_weights) holds 16-row tiles;
+  // raw GGUF bytes written into it would be read as tiles.  Refilling it needs
+  // a fresh allocation, which resets the layout to Raw.
+  if (tensor.storage_layout() != StorageLayout::Raw)
+    return Status::invalid_argument("tensor " + tensor.name() +
+                                    " holds Q8_0 16-row tiles; reallocate it before loading "
+                                    "raw GGUF bytes into it");
   auto raw = tensor_bytes(path, file, ti, map);
   if (!raw) return raw.error();
   auto numel = ti.num_elements();

@@ -596,6 +596,16 @@ static void test_gguf_model_end_to_end() {
       const auto after = download(ctx.get(vals[i]), cnt[i]);
       CHECK(std::memcmp(after.data(), before[i]->data(), cnt[i] * 4) == 0);
     }
+    // Raw GGUF bytes are not written into storage that now holds 16-row tiles
+    // (they would be read as tiles): InvalidArgument, and the tiles are kept.
+    const Status reload = loader.load_weights(*file, g, ctx);
+    CHECK(reload.code() == ErrorCode::InvalidArgument &&
+          reload.message().find("16-row tiles") != std::string::npos);
+    CHECK(store->get("layer_0.up_proj.weight")->storage_layout() == StorageLayout::Q8_0Tiled);
+    check_status(ex.run(ctx));
+    check_hip(hipDeviceSynchronize());
+    const auto again = download(ctx.get(*logits), cnt[3]);
+    CHECK(std::memcmp(again.data(), el.data(), cnt[3] * 4) == 0);
   }
   std::remove(path.c_str());
   std::printf("  PASS test_gguf_model_end_to_end\n");

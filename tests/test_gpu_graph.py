@@ -1,8 +1,10 @@
 """Linear launches captured in a HIP graph (torch.cuda.CUDAGraph) on a stream whose
 workspace was reserved beforehand (mle_q8_0_workspace_size + mle_workspace_reserve):
-capture allocates and synchronises nothing, and every replay -- with eager launches of
-other shapes on the same stream and host synchronisations between replays, and after a
-later call has outgrown the reservation -- gives the eager results bit for bit.  Shapes:
+capture allocates and synchronises nothing, and every replay -- on the capturing stream
+with eager launches of other shapes after it, on the default stream while eager launches
+of another shape run on the capturing stream at the same time (captured calls use the
+stream's graph workspace, which no eager call shares), and after a later eager call has
+outgrown the reservation -- gives the eager results bit for bit.  Shapes:
 the split-K MFMA decode (M = 8, 22 splits), the tiled FP32 GEMV (M = 1), the bf16 GEMM
 with its X pre-pass (M = 96) and the row-range MFMA decode (M = 4 on 512 tiled row
 groups, no workspace).  The kernels
@@ -38,8 +40,8 @@ def test_linear_graph_replays_match_eager(dev, orc):
         b, c = capi.workspace_size(capi.OP_LINEAR, M, [N], K, tiled)
         need_b, need_c = max(need_b, b), max(need_c, c)
         cases.append((M, N, K, tiled, dw, to_dev(x, dev), orc.sgemm_nt(x, w, M, N, K)))
-    # The eager launch made between replays must fit the reservation too: a growth
-    # would free the buffers the graph's kernels hold.
+    # The eager launch made between replays fits the reservation too, so the
+    # generation checks below see no growth.
     b, c = capi.workspace_size(capi.OP_LINEAR, 4, [2048], 4096)
     need_b, need_c = max(need_b, b), max(need_c, c)
     capi.workspace_reserve(need_b, need_c, stream=stream)
@@ -82,6 +84,29 @@ def test_linear_graph_replays_match_eager(dev, orc):
         for (M, N, *_r), a, b in zip(cases, eager, graph_out):
             assert torch.equal(a.view(torch.int32), b.view(torch.int32)), (rep, M, N)
     assert capi.workspace_info(stream)[2] == gen0
+
+    # Replays on the default stream, not ordered with eager split-K calls enqueued on the
+    # capturing stream right after them: the two may run at the same time, each on its
+    # own workspace.
+    note("replay on the default stream beside eager calls on the capturing stream")
+    xe = to_dev(S.activations(164, (8, 11008)), dev)
+    we = to_dev(S.q8_0_weight(165, 1024, 11008)[0], dev)
+    ye = [empty_f32((8, 1024), dev) for _ in range(3)]
+    want_e = empty_f32((8, 1024), dev)
+    capi.linear(xe, we, None, want_e, 8, 1024, 11008, stream=stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for y in graph_out:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()  # current stream: the default stream
+        for y in ye:
+            capi.linear(xe, we, None, y, 8, 1024, 11008, stream=stream)
+        torch.cuda.synchronize()
+        for (M, N, *_r), a, b in zip(cases, eager, graph_out):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32)), ("default", rep, M, N)
+        for y in ye:
+            assert torch.equal(y.view(torch.int32), want_e.view(torch.int32)), ("eager", rep)
 
     # A call that outgrows the reservation replaces the workspace buffers but keeps
     # the old ones, which the graph's kernels still point to: replays stay exact.

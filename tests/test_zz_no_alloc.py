@@ -5,8 +5,16 @@ library's static device array instead of the per-stream workspace.  Bar: the sam
 kernels run on the same operands, so outputs are bit-identical to mle_q8_0_linear (the
 Linear paths themselves are held to the oracle by the other GPU tests).  Each pair of
 calls runs twice in a row on the shared array, the second call with a smaller input, so
-stale partials or counters left by the first call would show.
+stale partials or counters left by the first call would show; a chain of split-K calls of
+different shapes is also enqueued back to back with a single synchronisation at the end
+(calls ordered on one stream share the array safely).  A child process checks the
+array's first use under graph capture (refused) and a captured split-K call replayed
+between eager calls.
 """
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 
@@ -27,7 +35,7 @@ def _operands(dev, seed, M, N, K, bias):
 @pytest.mark.parametrize("first,second", [
     ((8, 4096, 11008, False), (4, 1024, 4096, True)),      # split-K decode: 22 then 8 splits
     ((512, 4096, 11008, False), (96, 512, 2048, True)),    # prefill GEMM: 28 MB of scratch
-    ((16, 2048, 8192, True), (1, 4096, 4096, False)),      # decode, then the FP32 GEMV
+    ((16, 2048, 8192, True), (5, 1024, 4096, False)),      # split-K decode, other tile/splits
 ])
 def test_noalloc_matches_linear_two_calls(dev, first, second):
     import torch
@@ -60,3 +68,45 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(dev):
     torch.cuda.synchronize()
     assert code == 4 and "no-allocation" in msg and str(b) in msg
     assert bool((y == 7.0).all())     # nothing was launched
+
+
+def test_noalloc_back_to_back_split_k(dev):
+    """Three split-K decode calls of different shapes (22, 8 and 16 splits; different tile
+    counts) enqueued on one stream with no synchronisation between them: each resets
+    the counters it used before the next starts, and each matches mle_q8_0_linear."""
+    import torch
+    shapes = [(8, 4096, 11008, False), (4, 1024, 4096, True), (16, 2048, 8192, False)]
+    stream = torch.cuda.Stream()
+    ops, outs = [], []
+    for i, (M, N, K, bias) in enumerate(shapes):
+        ops.append(_operands(dev, 300 + 10 * i, M, N, K, bias))
+        outs.append(empty_f32((M, N), dev))
+    torch.cuda.synchronize()
+    note("linear_noalloc: three split-K calls back to back on one stream")
+    with torch.cuda.stream(stream):
+        for (M, N, K, _b), (dx, dw, db), y in zip(shapes, ops, outs):
+            capi.linear_noalloc(dx, dw, db, y, M, N, K, stream=stream)
+    stream.synchronize()
+    for (M, N, K, _b), (dx, dw, db), y in zip(shapes, ops, outs):
+        want = empty_f32((M, N), dev)
+        capi.linear(dx, dw, db, want, M, N, K)
+        torch.cuda.synchronize()
+        assert torch.isfinite(y).all()
+        assert torch.equal(y, want), (M, N, K)
+
+
+def test_noalloc_under_graph_capture_fresh_process():
+    """In a fresh process (the library's per-device scratch not yet set up): the first
+    no-allocation call, made under graph capture, is refused; after one eager call a
+    captured split-K call replays bit-identical to the eager result, with eager
+    no-allocation calls of another shape on the same stream between the replays."""
+    child = os.path.join(os.path.dirname(__file__), "noalloc_capture_child.py")
+    note("linear_noalloc under graph capture (child process)")
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join(
+        [os.path.dirname(os.path.dirname(os.path.abspath(__file__))), env.get("PYTHONPATH", "")])
+    p = subprocess.run([sys.executable, "-u", child], capture_output=True, text=True,
+                       timeout=240, env=env)
+    print(p.stdout[-3000:], p.stderr[-3000:])
+    assert p.returncode == 0, p.stderr[-2000:]
+    assert "noalloc capture child: OK" in p.stdout
