@@ -525,6 +525,35 @@ def main():
                                 f"bf16 (no Q8_0 decode); {Rb} rotated W copies"})
             del wbs, xb
         extras["prefill"] = pre
+        # ---- MatMul from 64 rows of A (B[K, N] blocks along N) on the same bf16 MFMA
+        # GEMM, beside the Linear of the same shape (raw bytes both; no BASELINE config
+        # names a MatMul, so this is a side row)
+        M, N, K = 512, 4096, 4096
+        bh = qweight(41, K, N)
+        R = rotation(bh.size)
+        bs = [torch.from_numpy(bh).to(dev)] + [None] * (R - 1)
+        for j in range(1, R):
+            bs[j] = bs[0].clone()
+        ah = S.activations(42, (M, K))
+        a = torch.from_numpy(ah).to(dev)
+        c = torch.empty((M, N), dtype=torch.float32, device=dev)
+        med_mm, lo_mm, hi_mm = timer(lambda j: capi.matmul(a, bs[j % R], c, M, N, K,
+                                                           stream=stream), 40)
+        rows = sample_rows(M, 43)
+        gate(f"matmul M={M} [{K}x{N}]", c.cpu().numpy()[rows],
+             orc.sgemm(np.ascontiguousarray(ah[rows]), bh, len(rows), N, K), GEMM_BAR)
+        yl = torch.empty((M, N), dtype=torch.float32, device=dev)
+        med_l, _, _ = timer(lambda j: capi.linear(a, bs[j % R], None, yl, M, N, K,
+                                                  stream=stream), 40)
+        extras["matmul"] = {"M": M, "N": N, "K": K, "us": round(med_mm, 2),
+                            "us_min": round(lo_mm, 2), "us_max": round(hi_mm, 2),
+                            "TFLOPs": round(2.0 * M * N * K / med_mm / 1e6, 1),
+                            "us_linear_same_shape": round(med_l, 2),
+                            "ratio_to_linear": round(med_mm / med_l, 3),
+                            "rotated_copies": R,
+                            "note": "MatMul (B [K, N], blocks along N) on the bf16 MFMA "
+                                    "GEMM vs the Linear GEMM of the same shape, raw bytes"}
+        del bs
         # ---- embedding gather, configs[4] (parity: the whole output, bit for bit)
         V, H, T = 151936, 896, 8 * 512
         tbl_h = qweight(5, V, H)

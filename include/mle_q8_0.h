@@ -135,12 +135,18 @@ int mle_q8_0_linear_multi(const float* x, int count, const uint8_t* const* w,
  * Replaces minillm::cuda::sgemm(const float* A, const uint8_t* B_q8_0, float* C,
  * int M, int N, int K)  (reference cuda_kernels.h:13, cuda_kernels.cu:852-868).
  * Elements as the reference CPU kernel cpu::sgemm(q8_0) forms them
- * (src/runtime/kernels/cpu_kernels.cpp:116-130), v = d*q in fp32; the K sum is
- * split into fixed pieces added in a fixed order (as the reference's device
- * kernel splits K over warps), so results are deterministic and within fp32
- * rounding of the CPU kernel (relative L2 <= 1e-5; small exact cases match it
- * bit for bit).  Uses the per-(device, stream) workspace of the Linear calls
- * when K is spread over several workgroups per output tile.
+ * (src/runtime/kernels/cpu_kernels.cpp:116-130), v = d*q in fp32.
+ *   M < 64 (or A not 16-byte aligned): FP32 FMAs; the K sum is split into
+ *   fixed pieces added in a fixed order (as the reference's device kernel
+ *   splits K over warps), so results are deterministic and within fp32
+ *   rounding of the CPU kernel (relative L2 <= 1e-5; small exact cases match it
+ *   bit for bit).
+ *   M >= 64: the bf16 MFMA GEMM of the Linear prefill, B dequantised
+ *   transposed into its W tile: A and d*q rounded once to bf16, fp32
+ *   accumulation, deterministic; relative L2 <= 1e-2 (about 2e-3 on N(0,1)
+ *   data), as the Linear GEMM.
+ * Uses the per-(device, stream) workspace of the Linear calls (split-K
+ * partials, the GEMM's bf16 copy of A).
  * Errors: NULL pointers, non-positive sizes -> InvalidArgument;
  * K % 32 != 0 or N % 32 != 0, or more than 524280 rows -> Unsupported.
  */

@@ -507,6 +507,19 @@ int noalloc_scratch(hipStream_t stream, uint8_t** base) {
   return MLE_OK;
 }
 
+// MatMul from 64 rows of A on the bf16 MFMA GEMM (B[K, N] dequantised
+// transposed into its W tile); below that, and where B's offsets would not fit
+// 32 bits, the FP32 kernel of matmul.hip.  Fills the GEMM's tile choice and
+// segment (B and C are set by the caller).
+bool matmul_on_gemm(int M, int N, int K, mle::GemmConfig* c, mle::LinearSegs* s) {
+  if (M < 64) return false;
+  *s = mle::LinearSegs{};
+  s->seg[0].N = N;
+  s->layout = mle::WeightLayout::kKN;
+  *c = mle::gemm_mfma_pick_kn(M, N, K);
+  return mle::gemm_mfma_fits(*c, M, N, K) && mle::gemm_mfma_kn_fits(*s, K);
+}
+
 }  // namespace
 
 extern "C" {
@@ -717,6 +730,14 @@ int mle_q8_0_workspace_size(int op, int M, int count, const int* N, int K, int t
     MLE_TRY(check_positive(ctx, N[0], "N"));
     if (N[0] % 32 != 0)
       return fail(MLE_UNSUPPORTED, std::string("hip ") + ctx + " requires a MatMul's N to be a multiple of 32");
+    mle::GemmConfig gc;
+    mle::LinearSegs gs;
+    if (matmul_on_gemm(M, N[0], K, &gc, &gs)) {
+      const mle::SplitKNeed need = mle::gemm_mfma_workspace_segs(gc, M, gs, K);
+      *bytes = need_bytes(need);
+      *counters = need.counters;
+      return ok();
+    }
     mle::SplitKNeed need;
     need.partial_floats = mle::matmul_workspace_floats(M, N[0], K);
     *bytes = need_bytes(need);
@@ -847,6 +868,18 @@ int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M, int 
   MLE_TRY(check_align(ctx, c, 16, "C"));
   if ((M + 7) / 8 > 65535)
     return fail(MLE_UNSUPPORTED, "hip sgemm Q8_0: at most 524280 rows of A per call");
+  mle::GemmConfig gc;
+  mle::LinearSegs gs;
+  // The GEMM's X pre-pass reads A in 16-byte pieces (any hipMalloc'd A qualifies).
+  if (((uintptr_t)a & 15u) == 0 && matmul_on_gemm(M, N, K, &gc, &gs)) {
+    gs.seg[0].w = b_q8_0;
+    gs.seg[0].y = c;
+    mle::SplitKWorkspace ws;
+    std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
+    MLE_TRY(get_workspace(mle::gemm_mfma_workspace_segs(gc, M, gs, K), stream, &ws, &hold));
+    return check_launch(mle::launch_gemm_mfma_segs(gc, a, gs, M, K, ws, stream),
+                        "hip sgemm Q8_0 launch failed");
+  }
   mle::SplitKNeed need;
   need.partial_floats = mle::matmul_workspace_floats(M, N, K);
   mle::SplitKWorkspace ws;

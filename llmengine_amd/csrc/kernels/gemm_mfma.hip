@@ -57,6 +57,14 @@
 // Every load is unconditional: rows past M or N and blocks past K read as zero
 // through the buffer range check, and steps past the end re-read the last step.
 //
+// MatMul (LAYOUT kKN): the same GEMM with B[K, N] in Q8_0 blocks along N
+// (cpu::sgemm, src/runtime/kernels/cpu_kernels.cpp:116-130).  A 34-byte block
+// then holds 32 consecutive columns of one K row, so producer item (k pair kp,
+// block column c) loads the blocks of rows 2 kp and 2 kp + 1 of the step in
+// column block c and writes their 32 columns transposed into the W tile, one
+// dword (the bf16 values of both rows) per column.  The consumers, the K order
+// and the epilogue are the Linear's.
+//
 // Split K (gridDim.z > 1, for shapes with too few tiles to fill the GPU): each
 // workgroup stores its BM x BN fp32 partial tile with device-scope (sc1)
 // stores, waits for their completion and bumps a per-tile counter; the last
@@ -414,13 +422,26 @@ __global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
     const bool up_rows = kSwi && pwave >= 2;
     const int item = kSwi ? (pwave & 1) * 64 + lane : pt;
     const int prow = item >> 1, wn_h = item & 1;  // row within its weight, block of the step
-    const bool w_thread = kSwi ? prow < BNO : (NBLK == 256 || pt < NBLK);
+    constexpr bool kKN = LAYOUT == int(WeightLayout::kKN);
+    // MatMul items: 32 k pairs x NJ column blocks.
+    const int kn_c = pt >> 5, kn_kp = pt & 31;
+    const bool w_thread = kKN ? pt < 32 * NJ : kSwi ? prow < BNO : (NBLK == 256 || pt < NBLK);
     const int wn_row = (up_rows ? BNO : 0) + prow;  // tile row
     const uint8_t* wsrc = up_rows ? args.seg[1].w : w;
     const int64_t wrows = min((int64_t)BNO, (int64_t)N - n0);
     const uint8_t* wtile = wsrc + n0 * row_bytes;
     const __amdgpu_buffer_rsrc_t wrs = rsrc(wtile, (uint32_t)(wrows * row_bytes));
     const uint32_t boff = (uint32_t)prow * row_bytes + (uint32_t)wn_h * kBlockBytes;
+    // MatMul: B row k holds NB = N / 32 blocks; the item's blocks are column
+    // block n0 / 32 + kn_c of rows 64 s + 2 kn_kp and + 1.  Rows past K read as
+    // zero through the range check, column blocks past N are masked.
+    const int NBK = N / kBlockElems;
+    const uint32_t kn_row = (uint32_t)NBK * kBlockBytes;
+    const __amdgpu_buffer_rsrc_t knrs = rsrc(wsrc, (uint32_t)((int64_t)K * kn_row));
+    const bool kn_live = n0 / kBlockElems + kn_c < NBK;
+    const uint32_t kn_off = (uint32_t)(2 * kn_kp) * kn_row + (uint32_t)(n0 / kBlockElems + kn_c) * kBlockBytes;
+    const uint32_t kn_mis0 = (uint32_t)(((uintptr_t)wsrc + kn_off) & 2u);
+    const uint32_t kn_mis1 = (uint32_t)(((uintptr_t)wsrc + kn_off + kn_row) & 2u);
     const uint32_t wmis = (uint32_t)(((uintptr_t)wtile + boff) & 2u);
     const uint32_t wv8 = boff + wmis;
     const uint32_t wv2 = boff + (wmis ? 0u : 32u);
@@ -445,16 +466,35 @@ __global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
     // Steps s with block 2 s + h < KB (none for threads without a W block,
     // whose loads are then all masked); tiled: every pair (the block past an
     // odd K/32 is zero in the tiled tensor).
-    const int w_steps = w_thread ? (kTiled ? KP : (KB - wn_h + 1) >> 1) : 0;
+    const int w_steps = w_thread ? (kKN ? (kn_live ? n_steps : 0)
+                                         : kTiled ? KP : (KB - wn_h + 1) >> 1)
+                                 : 0;
     struct TiledW {
       u32x4 a, b;  // quant slots 32 j + r, 32 j + 16 + r
       uint32_t sc;  // scales of both blocks
     };
-    using WItem = std::conditional_t<kTiled, TiledW, RawBlock>;
+    struct KNPair {
+      RawBlock r0, r1;  // rows 2 kp and 2 kp + 1 of the step, one column block
+    };
+    using WItem = std::conditional_t<kTiled, TiledW, std::conditional_t<kKN, KNPair, RawBlock>>;
+    auto load_kn = [&](uint32_t off, uint32_t mis, uint32_t so, bool live, RawBlock& r) {
+      const uint32_t v8 = live ? off + mis : 0x80000000u;
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(knrs, v8, so, 0);
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(knrs, v8 + 16, so, 0);
+      r.v0 = u32x4_a4{a.x, a.y, a.z, a.w};
+      r.v1 = u32x4_a4{b.x, b.y, b.z, b.w};
+      r.u = __builtin_amdgcn_raw_buffer_load_b16(
+          knrs, live ? off + (mis ? 0u : 32u) : 0x80000000u, so, 0);
+      r.mis = mis;
+    };
     auto load_w = [&](int s, WItem& r) {
       s = min(s, s_last);
       const bool live = s < w_steps;
-      if constexpr (kTiled) {
+      if constexpr (kKN) {
+        const uint32_t so = (uint32_t)s * (uint32_t)BK * kn_row;  // 64 rows of B per step
+        load_kn(kn_off, kn_mis0, so, live, r.r0);
+        load_kn(kn_off + kn_row, kn_mis1, so, live, r.r1);
+      } else if constexpr (kTiled) {
         const uint32_t sq = (uint32_t)s * kTilePieceBytes;
         r.a = __builtin_amdgcn_raw_buffer_load_b128(tqrs, live ? tqv : 0x80000000u, sq, 0);
         r.b = __builtin_amdgcn_raw_buffer_load_b128(tqrs, live ? tqv + 256 : 0x80000000u, sq, 0);
@@ -479,7 +519,16 @@ __global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
     };
     auto dequant = [&](const WItem& r, uint16_t* bs) {
       if (!w_thread) return;
-      if constexpr (kTiled) {
+      if constexpr (kKN) {
+        // Column 32 kn_c + i of the tile, K values 2 kp and 2 kp + 1: one dword.
+        const Block b0 = finish_block(r.r0), b1 = finish_block(r.r1);
+        const float d0 = scale_to_f32_fast(b0.scale_bits), d1 = scale_to_f32_fast(b1.scale_bits);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(bs + 32 * kn_c * LDS_STRIDE + 2 * kn_kp);
+#pragma unroll
+        for (int i = 0; i < kBlockElems; ++i)
+          dst[i * (LDS_STRIDE / 2)] =
+              cvt_bf16x2(d0 * q_at(b0.q[i >> 2], i & 3), d1 * q_at(b1.q[i >> 2], i & 3));
+      } else if constexpr (kTiled) {
         // Quants 16 j .. 16 j + 15 of block h go to elements 32 h + 16 j ..
         const float d0 = scale_to_f32_fast(r.sc & 0xffffu);
         const float d1 = scale_to_f32_fast(r.sc >> 16);
@@ -501,7 +550,7 @@ __global__ __launch_bounds__(Roles<MI>::kThreads, 1) void gemm_q8_0_mfma_kernel(
     // The first two steps are requested alone and dequantised before the rest of
     // the ring goes out, so the first barrier does not wait behind six more loads
     // (0.97-0.99x the time of issuing all eight first, bit-identical results).
-    constexpr int RING = 8;
+    constexpr int RING = kKN ? 4 : 8;
     WItem r[RING];
     load_w(s_begin, r[0]);
     load_w(s_begin + 1, r[1]);
@@ -572,7 +621,12 @@ template <int MI, int NJ, int L>
 void launch_tile_l(const GemmGrid& g, Epilogue mode, const u32x4* xf, uint32_t xf_bytes, int M,
                    int K, const SplitKWorkspace& ws, hipStream_t stream) {
   const dim3 grid(g.tn, g.tm, g.splits);
-  if (mode == Epilogue::kSwiGLU) {
+  if constexpr (L == int(WeightLayout::kKN)) {  // MatMul: plain epilogue only
+    (void)mode;
+    hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 0, L>), grid, dim3(Roles<MI>::kThreads), 0,
+                       stream, xf, xf_bytes, g.args, M, K, g.steps_per_split, ws.partials,
+                       ws.counters);
+  } else if (mode == Epilogue::kSwiGLU) {
     hipLaunchKernelGGL((gemm_q8_0_mfma_kernel<MI, NJ, 1, L>), grid, dim3(Roles<MI>::kThreads), 0,
                        stream, xf, xf_bytes, g.args, M, K, g.steps_per_split, ws.partials,
                        ws.counters);
@@ -589,7 +643,13 @@ void launch_tile(const GemmGrid& g, Epilogue mode, WeightLayout layout, const u3
                  hipStream_t stream) {
   if (layout == WeightLayout::kTiled)
     launch_tile_l<MI, NJ, int(WeightLayout::kTiled)>(g, mode, xf, xf_bytes, M, K, ws, stream);
-  else
+  else if (layout == WeightLayout::kKN) {
+    // MatMul tiles are 128 rows high: its producer ring (two raw blocks per
+    // item and step) does not fit the register budget of the 12-wave 256-row
+    // tiles without spilling.
+    if constexpr (MI == 1)
+      launch_tile_l<MI, NJ, int(WeightLayout::kKN)>(g, mode, xf, xf_bytes, M, K, ws, stream);
+  } else
     launch_tile_l<MI, NJ, int(WeightLayout::kRaw)>(g, mode, xf, xf_bytes, M, K, ws, stream);
 }
 
@@ -626,7 +686,7 @@ GemmConfig gemm_mfma_pick_segs(int M, const LinearSegs& s, int K) {
   GemmConfig best{128, 64, 1};
   double best_us = 1e300;
   for (const Shape& sh : shapes) {
-    if (sh.bm == 256 && M <= 128) continue;
+    if (sh.bm == 256 && (M <= 128 || s.layout == WeightLayout::kKN)) continue;
     const int cols = swi ? sh.bn / 2 : sh.bn;
     int64_t col_tiles = 0, out_cols = 0;
     for (int i = 0; i < count; ++i) {
@@ -678,6 +738,19 @@ bool gemm_mfma_fits(const GemmConfig& c, int M, int N, int K) {
          (int64_t)c.bn * row_bytes < (int64_t(1) << 31) && (M + 31) / 32 <= 65535;
 }
 
+bool gemm_mfma_kn_fits(const LinearSegs& s, int K) {
+  // One plain output; N a whole number of blocks; 32-bit offsets within B.
+  const int N = s.seg[0].N;
+  return s.count == 1 && s.mode == Epilogue::kPlain && N % kBlockElems == 0 &&
+         (int64_t)K * (N / kBlockElems) * kBlockBytes < (int64_t(1) << 31);
+}
+
+GemmConfig gemm_mfma_pick_kn(int M, int N, int K) {
+  LinearSegs s = single_seg(nullptr, nullptr, nullptr, N);
+  s.layout = WeightLayout::kKN;
+  return gemm_mfma_pick_segs(M, s, K);
+}
+
 hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const LinearSegs& s,
                                  int M, int K, const SplitKWorkspace& ws, hipStream_t stream) {
   const bool swi = s.mode == Epilogue::kSwiGLU;
@@ -687,6 +760,8 @@ hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const Line
     return hipErrorInvalidValue;
   for (int i = 0; i < s.count; ++i)
     if (s.seg[i].N <= 0 || s.seg[i].w == nullptr) return hipErrorInvalidValue;
+  if (s.layout == WeightLayout::kKN && (c.bm != 128 || !gemm_mfma_kn_fits(s, K)))
+    return hipErrorInvalidValue;
   const GemmGrid g = gemm_grid(c, M, s, K);
   if (g.splits > 1 && (ws.partials == nullptr || ws.counters == nullptr))
     return hipErrorInvalidValue;

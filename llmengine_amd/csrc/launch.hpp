@@ -72,7 +72,9 @@ enum class Epilogue { kPlain = 0, kSwiGLU = 1 };
 //     2p+1: the bf16 MFMA A-fragment order, so one 16-byte load per lane feeds
 //     two 16x16x32 MFMAs.  Dword r of scale piece (g, p) holds the binary16
 //     scale of block 2p (low half) and 2p+1 (high half) of row 16g + r.
-enum class WeightLayout { kRaw = 0, kTiled = 1 };
+//   kKN (prefill GEMM only, the MatMul's B operand): B[K, N] raw Q8_0 with
+//     blocks along N, element (k, n) at flat index k*N + n.
+enum class WeightLayout { kRaw = 0, kTiled = 1, kKN = 2 };
 constexpr int kTileRows = 16;
 constexpr int kTilePieceBytes = 1024;
 constexpr int kTileScaleBytes = 64;
@@ -151,6 +153,11 @@ GemmConfig gemm_mfma_pick_segs(int M, const LinearSegs& s, int K);
 SplitKNeed gemm_mfma_workspace_segs(const GemmConfig& c, int M, const LinearSegs& s, int K);
 hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const LinearSegs& s,
                                  int M, int K, const SplitKWorkspace& ws, hipStream_t stream);
+// Whether a MatMul (layout kKN: one plain segment, seg[0].w = B[K, N]) fits the
+// GEMM's 32-bit offsets within B.
+bool gemm_mfma_kn_fits(const LinearSegs& s, int K);
+// Tile choice of a MatMul on the GEMM (128-row tiles only).
+GemmConfig gemm_mfma_pick_kn(int M, int N, int K);
 
 // MatMul C[M,N] = A[M,K] . B[K,N] with B in Q8_0 blocks along N.  When the
 // launch spreads K over several workgroups per tile it needs

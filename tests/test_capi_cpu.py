@@ -101,11 +101,17 @@ def test_swiglu_validation_errors():
 
 def test_matmul_workspace_size():
     """MLE_OP_MATMUL: decode-size MatMuls spread K over workgroups and need
-    workspace ([S][M][N] partial floats); large M or wide N need none."""
+    workspace ([S][M][N] partial floats); wide N at small M needs none; from 64 rows
+    of A the MatMul runs the bf16 MFMA GEMM, which needs its bf16 copy of A (rows
+    rounded up to 32, K to 64) plus any split-K partials and counters."""
     b, c = capi.workspace_size(capi.OP_MATMUL, 1, [4096], 4096)
     assert b >= 16 * 4096 * 4 and c == 0
-    assert capi.workspace_size(capi.OP_MATMUL, 512, [4096], 4096) == (0, 0)
+    assert capi.workspace_size(capi.OP_MATMUL, 63, [512], 256) == (0, 0)
     assert capi.workspace_size(capi.OP_MATMUL, 1, [151936], 896) == (0, 0)
+    b, c = capi.workspace_size(capi.OP_MATMUL, 512, [4096], 4096)
+    assert b >= 512 * 4096 * 2
+    b, c = capi.workspace_size(capi.OP_MATMUL, 77, [1056], 1312)
+    assert b >= 96 * 1344 * 2
     code, msg, _, _ = capi.workspace_size_status(capi.OP_MATMUL, 1, [48], 64)
     assert code == 4 and "multiple of 32" in msg
     code, msg, _, _ = capi.workspace_size_status(capi.OP_MATMUL, 1, [64, 64], 64)

@@ -616,12 +616,12 @@ def test_matmul_known_answers(dev, golden):
         assert sha(to_host(out)) == c["sha256"]
 
 
-# (M, N, K): 1, 2, 4 and 8 token rows per tile (a partial last tile at M = 3, 5, 33,
-# 70); N past a 256-column tile (ragged tiles); K past a 256-row slice; shapes whose
-# K is spread over several workgroups (the workspace path: 1 x 4096 x 4096,
-# 2 x 512 x 11008) and shapes whose column tiles alone fill the GPU.
+# (M, N, K) of the FP32 MatMul (M < 64): 1, 2, 4 and 8 token rows per tile (a partial
+# last tile at M = 3, 5, 33, 63); N past a 256-column tile (ragged tiles); K past a
+# 256-row slice; shapes whose K is spread over several workgroups (the workspace path:
+# 1 x 4096 x 4096, 2 x 512 x 11008) and shapes whose column tiles alone fill the GPU.
 MATMUL_CASES = [(2, 32, 32), (3, 64, 160), (5, 256, 512), (1, 32, 4096), (8, 1024, 96),
-                (33, 96, 64), (4, 32, 32), (70, 512, 256), (1, 4096, 4096),
+                (33, 96, 64), (4, 32, 32), (63, 512, 256), (1, 4096, 4096),
                 (2, 512, 11008), (9, 800, 288), (1, 151936, 64)]
 
 
@@ -642,6 +642,42 @@ def test_matmul_matches_oracle(dev, orc, M, N, K):
     got, want = to_host(out), orc.sgemm(a, b, M, N, K)
     assert rel_l2(got, want) <= 1e-5, (M, N, K)
     assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-6
+
+
+# (M, N, K) of the MatMul on the bf16 MFMA GEMM (M >= 64): the configs[2]-sized square
+# shape, ragged M / N tiles with an odd number of K blocks (the last K step half empty),
+# the smallest GEMM shape, and a long K with split-K partials.
+MATMUL_GEMM_CASES = [(512, 4096, 4096), (77, 1056, 1312), (64, 32, 32), (130, 384, 11008)]
+
+
+@pytest.mark.parametrize("M,N,K", MATMUL_GEMM_CASES)
+def test_matmul_gemm_path(dev, orc, M, N, K):
+    """MatMul from 64 rows of A runs the bf16 MFMA GEMM with B[K, N] dequantised
+    transposed into its W tile.  Bar 1e-2 relative L2 (the prefill GEMM's): against the
+    oracle's cpu::sgemm restatement (cpu_kernels.cpp:116-130) on sampled rows, and on the
+    whole output against the FP32 MatMul run on 32-row chunks (the M < 64 path, held to
+    1e-5 by test_matmul_matches_oracle); repeatable bit for bit."""
+    import torch
+    note(f"matmul GEMM M={M} N={N} K={K}")
+    b, a = weight(300 + N, K, N), acts(301 + K, M, K)
+    out, out2 = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    da, db = to_dev(a, dev), to_dev(b, dev)
+    capi.matmul(da, db, out, M, N, K)
+    capi.matmul(da, db, out2, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    got = to_host(out)
+    assert np.isfinite(got).all()
+    rows = np.unique(np.r_[0, M - 1, np.linspace(0, M - 1, 30).astype(int)])
+    want = orc.sgemm(np.ascontiguousarray(a[rows]), b, rows.size, N, K)
+    assert rel_l2(got[rows], want) <= 1e-2, (M, N, K)
+    ref = empty_f32((M, N), dev)
+    for m0 in range(0, M, 32):
+        mc = min(32, M - m0)
+        capi.matmul(da[m0:m0 + mc], db, ref[m0:m0 + mc], mc, N, K)
+    fp32 = to_host(ref)
+    assert rel_l2(fp32[rows], want) <= 1e-5
+    assert rel_l2(got, fp32) <= 1e-2, (M, N, K)
 
 
 # ----------------------------------------------------------------------------- errors
