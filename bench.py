@@ -647,10 +647,17 @@ def main():
             ts = timer(lambda j: (capi.linear(x, gw[j % R], None, y, M, N, K, stream=stream),
                                   capi.linear(x, uw[j % R], None, g2, M, N, K,
                                               stream=stream)), iters)
+            # the unfused sequence the executor would run otherwise: two Linears, then
+            # the SwiGLU kernel over their outputs
+            y3 = torch.empty_like(y)
+            tu = timer(lambda j: (capi.linear(x, gw[j % R], None, y, M, N, K, stream=stream),
+                                  capi.linear(x, uw[j % R], None, g2, M, N, K, stream=stream),
+                                  capi.swiglu(y, g2, y3, M * N, stream=stream)), iters)
             nb = 2 * gemv_bytes(M, N, K) - 4 * M * K - 4 * M * N
             fused.append({"op": "gate+up -> SwiGLU [2 x 11008x4096]", "M": M,
                           "us_fused": round(tf[0], 2), "us_fused_spread": [round(v, 2) for v in tf[1:]],
                           "us_two_linears": round(ts[0], 2),
+                          "us_unfused_with_swiglu_kernel": round(tu[0], 2),
                           "GBps_fused": round(nb / tf[0] / 1e3, 1),
                           "us_fused_tiled": round(tft[0], 2),
                           "us_fused_tiled_spread": [round(v, 2) for v in tft[1:]],
