@@ -296,8 +296,11 @@ int mle_q8_0_linear_multi_tiled(const float* x, int count, const uint8_t* const*
  * mle_workspace_reserve: grows the eager and the graph workspace of (current
  *   device, stream) to hold at least `bytes` and `counters` each (a no-op when
  *   they already do); later calls within those sizes allocate and synchronise
- *   nothing, eager or captured.  A call captured on a stream whose graph
- *   workspace is too small returns RuntimeError ("reserve it before capture").
+ *   nothing, eager or captured.  When the graph workspace grows, the call
+ *   synchronises `stream` once (its counters are cleared by a kernel there, and
+ *   a graph captured later may be replayed on any stream).  A call captured on
+ *   a stream whose graph workspace is too small returns RuntimeError ("reserve
+ *   it before capture").
  * mle_workspace_info: capacity of (current device, stream)'s eager workspace
  *   and the number of (re)allocations it has had (0 / 0 / 0 when it has none
  *   yet).

@@ -113,6 +113,7 @@ struct StreamWorkspace {
   uint32_t* counters = nullptr;
   size_t counter_cap = 0;  // uint32 entries
   uint64_t generation = 0;  // (re)allocations so far
+  uint64_t synced_generation = 0;  // graph workspace: the generation last waited for
   std::vector<void*> retired;  // replaced buffers, never freed (see above)
 };
 std::mutex g_ws_mu;
@@ -752,6 +753,15 @@ int mle_workspace_reserve(size_t bytes, size_t counters, hipStream_t stream) {
   StreamWorkspace* e = nullptr;
   MLE_TRY(ensure_workspace(bytes, counters, stream, false, &e));
   MLE_TRY(ensure_workspace(bytes, counters, stream, true, &e));
+  // A graph workspace that grew had its counters cleared by a kernel on
+  // `stream`; a graph captured later may be replayed on another stream, which is
+  // not ordered after that kernel, so wait for it here.
+  const uint64_t gen = e->generation;
+  if (gen != e->synced_generation) {
+    const hipError_t err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) return check_launch(err, "hip workspace_reserve: synchronise");
+    e->synced_generation = gen;
+  }
   return ok();
 }
 
