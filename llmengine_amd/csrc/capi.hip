@@ -739,9 +739,12 @@ int mle_q8_0_workspace_size(int op, int M, int count, const int* N, int K, int t
       *counters = need.counters;
       return ok();
     }
+    const mle::MatmulNeed mm = mle::matmul_workspace(M, N[0], K);
     mle::SplitKNeed need;
-    need.partial_floats = mle::matmul_workspace_floats(M, N[0], K);
+    need.partial_floats = mm.partial_floats;
+    need.counters = mm.counters;
     *bytes = need_bytes(need);
+    *counters = need.counters;
     return ok();
   }
   return fail(MLE_INVALID_ARGUMENT, std::string("hip ") + ctx + ": unknown op " + std::to_string(op));
@@ -890,13 +893,16 @@ int mle_q8_0_matmul(const float* a, const uint8_t* b_q8_0, float* c, int M, int 
     return check_launch(mle::launch_gemm_mfma_segs(gc, a, gs, M, K, ws, stream),
                         "hip sgemm Q8_0 launch failed");
   }
+  const mle::MatmulNeed mm = mle::matmul_workspace(M, N, K);
   mle::SplitKNeed need;
-  need.partial_floats = mle::matmul_workspace_floats(M, N, K);
+  need.partial_floats = mm.partial_floats;
+  need.counters = mm.counters;
   mle::SplitKWorkspace ws;
   std::unique_lock<std::mutex> hold;  // released after the launch is enqueued
   MLE_TRY(get_workspace(need, stream, &ws, &hold));
-  return check_launch(mle::launch_matmul(a, b_q8_0, c, M, N, K, ws.partials, stream),
-                      "hip sgemm Q8_0 launch failed");
+  return check_launch(
+      mle::launch_matmul(a, b_q8_0, c, M, N, K, ws.partials, ws.counters, stream),
+      "hip sgemm Q8_0 launch failed");
 }
 
 int mle_q8_0_embedding(const uint8_t* table_q8_0, const int32_t* ids, float* out,

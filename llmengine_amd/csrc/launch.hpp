@@ -160,11 +160,16 @@ bool gemm_mfma_kn_fits(const LinearSegs& s, int K);
 GemmConfig gemm_mfma_pick_kn(int M, int N, int K);
 
 // MatMul C[M,N] = A[M,K] . B[K,N] with B in Q8_0 blocks along N.  When the
-// launch spreads K over several workgroups per tile it needs
-// matmul_workspace_floats(M, N, K) floats of workspace in `partials` (0: none).
-size_t matmul_workspace_floats(int M, int N, int K);
+// launch spreads K over several workgroups per tile it needs the workspace
+// matmul_workspace(M, N, K) names: `partials` floats and, for M <= 8, tile
+// counters (zero between launches; the kernel resets them).
+struct MatmulNeed {
+  size_t partial_floats = 0;
+  size_t counters = 0;
+};
+MatmulNeed matmul_workspace(int M, int N, int K);
 hipError_t launch_matmul(const float* a, const uint8_t* b, float* c, int M, int N, int K,
-                         float* partials, hipStream_t stream);
+                         float* partials, uint32_t* counters, hipStream_t stream);
 
 // Greedy argmax of `rows` rows of n fp32 logits: idx (and val, if non-null) per
 // row; `keys` is a workspace of rows * argmax_chunks(n) 64-bit entries.

@@ -101,10 +101,14 @@ def test_swiglu_validation_errors():
 
 def test_matmul_workspace_size():
     """MLE_OP_MATMUL: decode-size MatMuls spread K over workgroups and need
-    workspace ([S][M][N] partial floats); wide N at small M needs none; from 64 rows
+    workspace: up to 8 rows of A, a partial tile of 256 columns x the token tile per
+    workgroup plus a counter per tile (16 tiles x 16 splits at 1 x 4096 x 4096);
+    9-63 rows, [S][M][N] partial floats; wide N at small M needs none; from 64 rows
     of A the MatMul runs the bf16 MFMA GEMM, which needs its bf16 copy of A (rows
     rounded up to 32, K to 64) plus any split-K partials and counters."""
     b, c = capi.workspace_size(capi.OP_MATMUL, 1, [4096], 4096)
+    assert b >= 16 * 16 * 256 * 4 and c >= 16
+    b, c = capi.workspace_size(capi.OP_MATMUL, 16, [4096], 4096)
     assert b >= 16 * 4096 * 4 and c == 0
     assert capi.workspace_size(capi.OP_MATMUL, 63, [512], 256) == (0, 0)
     assert capi.workspace_size(capi.OP_MATMUL, 1, [151936], 896) == (0, 0)

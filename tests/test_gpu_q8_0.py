@@ -617,12 +617,16 @@ def test_matmul_known_answers(dev, golden):
 
 
 # (M, N, K) of the FP32 MatMul (M < 64): 1, 2, 4 and 8 token rows per tile (a partial
-# last tile at M = 3, 5, 33, 63); N past a 256-column tile (ragged tiles); K past a
+# last tile at M = 3, 5, 33, 63); N past a 256-column tile (ragged tiles) and an odd
+# number of blocks per B row (rows alternate 4-byte phase: N = 32, 96); K past a
 # 256-row slice; shapes whose K is spread over several workgroups (the workspace path:
-# 1 x 4096 x 4096, 2 x 512 x 11008) and shapes whose column tiles alone fill the GPU.
+# 1 x 4096 x 4096 and 4 x 11008 x 4096 with the last-arriving workgroup adding the
+# partials, 2 x 512 x 11008 with 43 of them) and shapes whose column tiles alone fill
+# the GPU.
 MATMUL_CASES = [(2, 32, 32), (3, 64, 160), (5, 256, 512), (1, 32, 4096), (8, 1024, 96),
                 (33, 96, 64), (4, 32, 32), (63, 512, 256), (1, 4096, 4096),
-                (2, 512, 11008), (9, 800, 288), (1, 151936, 64)]
+                (2, 512, 11008), (9, 800, 288), (1, 151936, 64), (3, 96, 1024),
+                (8, 4096, 4096), (4, 11008, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", MATMUL_CASES)
@@ -642,6 +646,25 @@ def test_matmul_matches_oracle(dev, orc, M, N, K):
     got, want = to_host(out), orc.sgemm(a, b, M, N, K)
     assert rel_l2(got, want) <= 1e-5, (M, N, K)
     assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-6
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 96, 256), (4, 4096, 512), (8, 512, 1024), (2, 32, 64)])
+def test_matmul_b_at_two_byte_offset(dev, M, N, K):
+    """B may start 2 bytes past a 4-byte boundary (Q8_0 blocks are 34 bytes): every
+    block then sits at the other 4-byte phase, so the up-to-8-row kernel takes its
+    other load pattern; the result is the aligned copy's bit for bit."""
+    import torch
+    b, a = weight(400 + N, K, N), acts(401 + K, M, K)
+    da, db = to_dev(a, dev), to_dev(b, dev)
+    buf = torch.zeros(db.numel() + 2, dtype=torch.uint8, device=dev)
+    buf[2:] = db
+    shifted = buf[2:]
+    assert shifted.data_ptr() % 4 == 2
+    out, out2 = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    capi.matmul(da, db, out, M, N, K)
+    capi.matmul(da, shifted, out2, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int32), out2.view(torch.int32)), (M, N, K)
 
 
 # (M, N, K) of the MatMul on the bf16 MFMA GEMM (M >= 64): the configs[2]-sized square
