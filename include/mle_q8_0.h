@@ -373,13 +373,20 @@ size_t mle_q8_0_bytes(int64_t numel);
  *             t3 = 0 (a 0 among t0..t2 keeps that field automatic);
  *     path 3: t0 = token tile in {1,2,4,5,8,16} >= min(M,16), t1 = waves per
  *             workgroup in {2,4,8} (16 rows each), t2 = K blocks per
- *             workgroup in {16, 32} (32 only for a token tile <= 8), t3 = 0.
+ *             workgroup in {16, 32} (32 only for a token tile <= 8), t3 = 0,
+ *             or t3 in 1..4 = a launch shape of the hybrid kernel (row groups x
+ *             a short K split; tiled weights, token tile 4 or 8, t1 and t2
+ *             then unused but valid).
+ * mle_q8_0_linear_tiled_ex: the same hook on kTiled weights (path 0 or 3).
  */
 int mle_q8_0_f16_decode(const uint16_t* bits, float* out, int64_t n,
                         hipStream_t stream);
 int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
                        float* y, int M, int N, int K, int path, int t0, int t1,
                        int t2, int t3, hipStream_t stream);
+int mle_q8_0_linear_tiled_ex(const float* x, const uint8_t* w_tiled, const float* bias,
+                             float* y, int M, int N, int K, int path, int t0, int t1,
+                             int t2, int t3, hipStream_t stream);
 
 /*
  * Streaming-read probe, a measurement aid with no counterpart in the reference:

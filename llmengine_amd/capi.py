@@ -21,6 +21,7 @@ ERROR_NAMES = {0: "Ok", 1: "InvalidArgument", 2: "OutOfRange", 3: "ShapeMismatch
                4: "Unsupported", 5: "NotImplemented", 6: "RuntimeError"}
 
 EXPORTED = ("mle_q8_0_abi_version", "mle_q8_0_linear", "mle_q8_0_linear_ex",
+            "mle_q8_0_linear_tiled_ex",
             "mle_q8_0_linear_swiglu", "mle_q8_0_linear_multi", "mle_q8_0_matmul",
             "mle_q8_0_embedding", "mle_q8_0_embedding_tiled", "mle_argmax_f32", "mle_top_tokens_f32", "mle_swiglu_f32",
             "mle_last_error", "mle_q8_0_bytes", "mle_q8_0_f16_decode", "mle_q8_0_tiled_bytes",
@@ -62,6 +63,8 @@ def load() -> ctypes.CDLL:
     lib.mle_q8_0_linear_ex.restype = _i
     lib.mle_q8_0_linear_ex.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
                                        _vp]
+    lib.mle_q8_0_linear_tiled_ex.restype = _i
+    lib.mle_q8_0_linear_tiled_ex.argtypes = lib.mle_q8_0_linear_ex.argtypes
     lib.mle_q8_0_linear_swiglu.restype = _i
     lib.mle_q8_0_linear_swiglu.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mle_q8_0_linear_multi.restype = _i
@@ -170,19 +173,20 @@ def linear_noalloc(x, w, bias, y, M, N, K, stream=None) -> None:
 
 
 def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice=0,
-              splits=0, bm=0, bn=0, stream=None) -> None:
+              splits=0, bm=0, bn=0, hyb=0, stream=None, tiled=False) -> None:
     """Linear with a forced path and launch shape (test / tuning hook).
 
     path 1 (FP32 GEMV) takes mt, lpr, rw; path 2 (MFMA GEMM) takes splits, bm, bn;
-    path 3 (MFMA decode) takes mt, waves, kslice; zero = automatic."""
+    path 3 (MFMA decode) takes mt, waves, kslice and hyb (a hybrid-kernel launch
+    shape, tiled weights); zero = automatic.  tiled: W in 16-row tiles (path 0 or 3)."""
     if path == 3:
-        t = (mt, waves, kslice, 0)
+        t = (mt, waves or (4 if hyb else 0), kslice or (16 if hyb else 0), hyb)
     elif path == 2:
         t = (splits, bm, bn, 0)
     else:
         t = (mt, lpr, rw, 0)
-    rc = load().mle_q8_0_linear_ex(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K,
-                                   path, *t, _stream(stream))
+    fn = load().mle_q8_0_linear_tiled_ex if tiled else load().mle_q8_0_linear_ex
+    rc = fn(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K, path, *t, _stream(stream))
     _raise(rc)
 
 

@@ -297,7 +297,7 @@ int run_linear(const float* x, const uint8_t* w, const void* bias, float* y, int
   one.seg[0] = mle::LinearSeg{w, bias, y, N};
   one.seg[0].bias_bf16 = bias_bf16 ? 1 : 0;
   one.layout = layout;
-  if (tiled && path == 3 && M <= 4 && mle::gemv_tiled_wins(M, N, K)) {
+  if (tiled && path == 3 && tune.dec.mt == 0 && M <= 4 && mle::gemv_tiled_wins(M, N, K)) {
     const mle::TiledGemvConfig c = mle::gemv_tiled_pick(M, N, K, false);
     return check_launch((ex.planning() ? hipSuccess : mle::launch_gemv_tiled_segs(c, x, one, M, K, ex.stream)),
                         "hip sgemm_nt Q8_0 launch failed");
@@ -542,10 +542,11 @@ int mle_q8_0_linear(const float* x, const uint8_t* w_q8_0, const float* bias, fl
   return run_linear(x, w_q8_0, bias, y, M, N, K, 0, Tune{}, Exec{stream});
 }
 
-int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
-                       float* y, int M, int N, int K, int path, int t0, int t1, int t2,
-                       int t3, hipStream_t stream) {
-  MLE_TRY(validate_linear(x, w_q8_0, bias, y, M, N, K));
+namespace {
+
+int linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias, float* y, int M, int N,
+              int K, int path, int t0, int t1, int t2, int t3, hipStream_t stream,
+              mle::WeightLayout layout) {
   if (path < 0 || path > 3)
     return fail(MLE_INVALID_ARGUMENT,
                 "hip sgemm_nt_q8_0_weight: path must be 0, 1, 2 or 3");
@@ -561,7 +562,12 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
                         std::to_string(t2) + ")");
     } else if (path == 3) {
       tune.dec = mle::DecodeMfmaConfig{t0, t1, t2};
-      if (t3 != 0 || !mle::decode_mfma_config_valid(tune.dec))
+      tune.dec.hyb = t3;
+      if (t3 != 0 && (layout != mle::WeightLayout::kTiled || (t0 != 4 && t0 != 8)))
+        return fail(MLE_INVALID_ARGUMENT,
+                    "hip sgemm_nt_q8_0_weight: a hybrid MFMA decode shape needs tiled weights "
+                    "and a token tile of 4 or 8");
+      if (t3 < 0 || t3 > 4 || !mle::decode_mfma_config_valid(tune.dec))
         return fail(MLE_INVALID_ARGUMENT,
                     "hip sgemm_nt_q8_0_weight: invalid MFMA decode shape (mt " +
                         std::to_string(t0) + ", waves " + std::to_string(t1) + ", kslice " +
@@ -579,7 +585,29 @@ int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
                   "hip sgemm_nt_q8_0_weight: a launch shape needs path 1, 2 or 3");
     }
   }
-  return run_linear(x, w_q8_0, bias, y, M, N, K, path, tune, Exec{stream});
+  return run_linear(x, w_q8_0, bias, y, M, N, K, path, tune, Exec{stream}, layout);
+}
+
+}  // namespace
+
+int mle_q8_0_linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias,
+                       float* y, int M, int N, int K, int path, int t0, int t1, int t2,
+                       int t3, hipStream_t stream) {
+  MLE_TRY(validate_linear(x, w_q8_0, bias, y, M, N, K));
+  return linear_ex(x, w_q8_0, bias, y, M, N, K, path, t0, t1, t2, t3, stream,
+                   mle::WeightLayout::kRaw);
+}
+
+int mle_q8_0_linear_tiled_ex(const float* x, const uint8_t* w_tiled, const float* bias,
+                             float* y, int M, int N, int K, int path, int t0, int t1, int t2,
+                             int t3, hipStream_t stream) {
+  MLE_TRY(validate_linear(x, w_tiled, bias, y, M, N, K));
+  MLE_TRY(check_align("sgemm_nt_q8_0_tiled", w_tiled, 16, "B"));
+  if (path == 1 || path == 2)
+    return fail(MLE_INVALID_ARGUMENT,
+                "hip sgemm_nt_q8_0_tiled: a forced path on tiled weights is 0 or 3");
+  return linear_ex(x, w_tiled, bias, y, M, N, K, path, t0, t1, t2, t3, stream,
+                   mle::WeightLayout::kTiled);
 }
 
 

@@ -241,7 +241,10 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(const float* __restrict_
   }
 }
 
-constexpr int kXLdsBudget = 48 * 1024;  // bytes of staged activations per workgroup
+// Bytes of staged activations per workgroup: all of K in one chunk up to 384
+// blocks at one token (the Llama down projection, K = 11008, in one pass: a
+// second chunk drains the load ring behind two barriers mid-row).
+constexpr int kXLdsBudget = 54 * 1024;
 
 template <int MT, int LPR, int RW>
 hipError_t launch_one(const float* x, const LinearSegs& s, int M, int K, hipStream_t stream) {

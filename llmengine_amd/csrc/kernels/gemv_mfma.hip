@@ -31,10 +31,11 @@
 // l % 16, blocks 4u + l / 16 of the chunk (u = 0 .. KS/4-1).  A 4 x 4 transpose
 // of 8-byte quant chunks across the four 16-lane rows (v_permlane32_swap then
 // v_permlane16_swap, 8 instructions per 4 blocks) turns those registers straight
-// into MFMA A fragments, with no LDS round trip.  Software pipeline: the weight
-// loads of chunks c+1 and c+2 and the activation loads of chunk c+1 are in
-// flight while chunk c is multiplied; the activation split of chunk c+1 goes to
-// the other half of a double-buffered LDS B-fragment area; one barrier per chunk.
+// into MFMA A fragments, with no LDS round trip.  Order of work: the slice's
+// activation loads, the first chunk's weight loads (raw weights: every chunk's),
+// the activation split into LDS B fragments (shared by the waves), one barrier,
+// the other chunks' weight loads, then the multiplies chunk by chunk as the
+// loads land.
 //
 // Split K.  When there are too few row tiles to fill the GPU, the K chunks are
 // split over gridDim.y workgroups.  Each stores its 16 W x MT partial sums to its
@@ -240,10 +241,12 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   static_assert(KSL % KS == 0, "K slice = whole chunks");
   __shared__ __attribute__((aligned(16))) uint8_t bfr[S::BBUF];
   __shared__ __attribute__((aligned(16))) float scl[W][KS][16];
-  __shared__ float red[W][16][17];
   __shared__ __attribute__((aligned(16))) uint8_t xdummy[16];
   __shared__ float gate_out[kSwi ? RW : 1][kSwi ? S::OPL * 64 : 1];
-  __shared__ uint32_t arrived;
+  // The split-K arrival count, in the last dword of the B area (free by then;
+  // the reductions below use its start): 8-token fragments of a 16-block slice
+  // then take 26880 bytes of LDS in all, six 4-wave workgroups per CU.
+  uint32_t& arrived = *reinterpret_cast<uint32_t*>(bfr + S::BBUF - 4);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -303,17 +306,20 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
     xv[i][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16, 0, 0));
   }
 
-  // 1. Every weight load of this wave's 16 rows x KSL blocks, issued up front.
-  //    Blocks past the slice's end read as zeros: their per-lane offset is put
+  // 1. The weight loads of this wave's 16 rows x KSL blocks, in chunks of KS
+  //    blocks (tiled: the first chunk before the activation split, the others
+  //    right after it; raw: all up front).  Blocks past the slice's end read as
+  //    zeros: their per-lane offset is put
   //    past the buffer (the range check applies to the per-lane offset), so no
   //    lane ever addresses a byte outside its slice of the weight tensor.
   constexpr bool kTiled = LAYOUT == int(WeightLayout::kTiled);
   RawBlock wr[kTiled ? 1 : NCH][NL];
   u32x4 tq[kTiled ? NCH : 1][4];  // tiled: the chunk's 4 block pairs
   uint32_t ts[kTiled ? NCH : 1];  // tiled: one scale dword per chunk
+  // Chunk c's loads (raw: NL load sets of whole blocks; tiled: 4 quant pieces
+  // and a scale dword).
+  auto issue_chunk = [&](int c) {
   if constexpr (!kTiled) {
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
 #pragma unroll
       for (int u = 0; u < NL; ++u) {
         const int b = KS * c + 4 * u;  // first block of the load set (lane adds g)
@@ -344,8 +350,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
     const __amdgpu_buffer_rsrc_t srs =
         make_rsrc(sb, rg < G ? (uint32_t)KP * kTileScaleBytes : 0u);
     const int p0 = kb0 >> 1;  // KSL is even
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
+    {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int pr = (KS / 2) * c + u;  // pair within the slice
@@ -361,6 +366,13 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
           0, 0);
     }
   }
+  };
+  // Tiled weights: the first chunk before the split, the others right after it.
+  // Raw weights: every chunk up front (issuing the later ones after the split
+  // measured 1.04-1.15x slower on the Llama shapes at 4 and 8 tokens).
+  constexpr int kPre = kTiled ? 1 : NCH;
+#pragma unroll
+  for (int c = 0; c < kPre; ++c) issue_chunk(c);
 
   // 2. B fragments of the whole K slice (activations split into bf16 parts),
   //    shared by the workgroup's waves.  B fragment (block kb, MFMA p): lane l
@@ -408,6 +420,12 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
     }
   }
   __syncthreads();
+  // Tiled weights: the other chunks' loads go out once the split is done, so a
+  // wave that waits on full request queues while issuing them has only
+  // multiplies and the hand-off left after that wait (MI355X: o_proj 4096 x 4096
+  // at 8 tokens 0.96x against issuing every chunk first).
+#pragma unroll
+  for (int c = kPre; c < NCH; ++c) issue_chunk(c);
 
   // 3. Each wave multiplies its rows chunk by chunk as the loads land: realign,
   //    scales to (wave-private) LDS, in-register transpose into A fragments,
@@ -468,7 +486,13 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   }
   const f32x4 acc = accs[0] + accs[1];
 
-  // Sum the part columns of each token (within the wave).
+  // Sum the part columns of each token (within the wave), in a wave-private
+  // slice of the B-fragment area once every wave is done with the fragments:
+  // no LDS of its own, which lets a sixth 4-wave workgroup of 8-token fragments
+  // onto a CU.
+  static_assert(W * 16 * 17 * 4 <= S::BBUF - 4, "the part sums fit the B area");
+  __syncthreads();
+  float (*red)[16][17] = reinterpret_cast<float (*)[16][17]>(bfr);
   red[wave][4 * g + 0][r16] = acc.x;
   red[wave][4 * g + 1][r16] = acc.y;
   red[wave][4 * g + 2][r16] = acc.z;
@@ -585,7 +609,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
   constexpr int CHUNKS = REGION / 4;
   constexpr int TPC = S::NT / CHUNKS;  // 16 / MT threads per piece, rounded down
   static_assert(TPC >= 1, "one thread per piece at least");
-  static_assert((4 * S::NT + REGION) * 4 <= S::BBUF, "reduction scratch fits the B area");
+  static_assert((4 * S::NT + REGION) * 4 <= S::BBUF - 4, "reduction scratch fits the B area");
   float* const sums = reinterpret_cast<float*>(bfr);  // [TPC][CHUNKS] x 4
   float* const tot = sums + 4 * S::NT;                // [REGION]
   {
@@ -1055,6 +1079,350 @@ hipError_t launch_rows(const float* x, const LinearSegs& s, int M, int K, hipStr
   return hipErrorInvalidValue;
 }
 
+// Row groups with a short K split ("hybrid" decode, tiled weights, 4 or 8
+// tokens, plain outputs).  The split-K kernel above gives a workgroup 16 W rows
+// x 16 blocks, so every output row's activations are read and split once per
+// row tile (64 times for down's 4096 rows) and 22 partial sums meet per output;
+// the row-range kernel reads and splits all of K once per workgroup.  Here a
+// workgroup owns NG 16-row groups x one split of SPB blocks (NG = 8, SPB = 44 on
+// down 4096 x 11008: 32 x 8 = 256 workgroups, one per CU): its split's
+// activations are loaded and split once into LDS B fragments (the layout and
+// arithmetic of the kernels above) and shared by all NG groups, every weight
+// load of the workgroup (RING chunks of 4 block pairs per wave, all of them when
+// RING covers the wave's share) is issued before the split, and the splits of a
+// row tile meet in one hand-off (partials, completion wait, counter, read-back
+// by the last workgroup in split order: deterministic).  Wave (group lg, index
+// qw) multiplies pairs [qw WPP, (qw + 1) WPP) of the split for its group; the
+// WG waves of a group add their sums in LDS in wave order.
+template <int MT, int NG, int WG, int SPB, int RING>
+__global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_hyb_kernel(
+    const float* __restrict__ x, const RowsArgs args, int M, int K,
+    float* __restrict__ partials, uint32_t* __restrict__ counters) {
+  constexpr int W = WG * NG;
+  constexpr int NT = 64 * W;
+  constexpr int P = Cols<MT>::P;
+  using C = Cols<MT, 4>;                  // half-size last fragment when it fits
+  static_assert(SPB % 2 == 0, "whole block pairs per split");
+  constexpr int SPP = SPB / 2;            // pairs per split
+  constexpr int WPP = (SPP + WG - 1) / WG;  // pairs per wave
+  constexpr int NCK = (WPP + 3) / 4;      // 4-pair chunks per wave
+  constexpr int PADB = 8 * NCK * WG;      // blocks of the B area (>= SPB)
+  constexpr int BBUF = PADB * C::FB;
+  constexpr int XITEMS = MT * PADB * 4;   // (token, k quarter, block)
+  constexpr int XPT = (XITEMS + NT - 1) / NT;
+  constexpr int OUTS = 16 * MT;           // outputs per group
+  constexpr int OPL = (OUTS + 63) / 64;
+  constexpr int REGION = NG * OUTS;       // partial floats per workgroup
+  constexpr int RPT = (REGION + NT - 1) / NT;
+  constexpr int RG = RING < NCK ? RING : NCK;
+  static_assert(W * 16 * 17 * 4 <= BBUF, "the group reduction fits the B area");
+  __shared__ __attribute__((aligned(16))) uint8_t bfr[BBUF];
+  __shared__ __attribute__((aligned(16))) float scl[W][8][16];
+  __shared__ uint32_t arrived;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r16 = lane & 15;
+  const int lg = wave / WG, qw = wave % WG;
+  const int KB = K / kBlockElems;
+  const int KP = (KB + 1) >> 1;
+  const int kb0 = blockIdx.y * SPB;       // first block of this split
+  const int pp0 = kb0 >> 1;               // first pair of this split
+
+  const unsigned grp_total = args.count == 1 ? args.grp_end[0]
+                             : args.count == 2 ? args.grp_end[1]
+                                               : args.grp_end[2];
+  // Segment of a group (uniform selects: no indexing into the argument).
+  auto seg_of = [&](unsigned gr) {
+    return (args.count > 1 && gr >= args.grp_end[0])
+               ? ((args.count > 2 && gr >= args.grp_end[1]) ? 2 : 1)
+               : 0;
+  };
+  const unsigned grp = blockIdx.x * NG + lg;
+  const int si = seg_of(grp);
+  const unsigned grp0 = si == 0 ? 0u : si == 1 ? args.grp_end[0] : args.grp_end[1];
+  const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
+  const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
+  const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
+  const bool live_g = grp < grp_total;
+  const int64_t rg = live_g ? (int64_t)(grp - grp0) : 0;
+
+  // 0. This split's activations first: item (token m fastest, k quarter, block
+  //    of the B area); items past M, past the split or past K read zeros.
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)((int64_t)M * K * 4));
+  f32x4 xv[XPT][2];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int it = tid + NT * i;
+    const int m = it % MT, q = it / MT;
+    const int kb = q >> 2;
+    uint32_t off = it < XITEMS && kb < SPB && kb0 + kb < KB && m < M
+                       ? (uint32_t)((m * K + (kb0 + kb) * kBlockElems + 8 * (q & 3)) * 4)
+                       : 0x80000000u;
+    asm volatile("" : "+v"(off));  // the load stays where it is written
+    xv[i][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+    xv[i][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16, 0, 0));
+  }
+
+  // 1. Weights: quant slots (lane l: rows l % 16, quants 8 (l/16) .. +7 of both
+  //    blocks of a pair) and scale dwords (lane l: pair l/16 of the chunk, row
+  //    l % 16) of this wave's group; pairs past the wave's share, the split or K,
+  //    and groups past N, read zeros.
+  const uint8_t* qb = w + rg * KP * kTilePieceBytes;
+  const uint8_t* sb = w + G * KP * kTilePieceBytes + rg * KP * kTileScaleBytes;
+  const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qb, live_g ? (uint32_t)KP * kTilePieceBytes : 0u);
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, live_g ? (uint32_t)KP * kTileScaleBytes : 0u);
+  u32x4 tq[NCK][4];
+  uint32_t ts[NCK];
+  auto pair_live = [&](int j) {  // pair j of this wave's share
+    return j < WPP && qw * WPP + j < SPP && pp0 + qw * WPP + j < KP;
+  };
+  auto load_chunk = [&](int ck) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = 4 * ck + u;
+      uint32_t off = pair_live(j)
+                         ? (uint32_t)(pp0 + qw * WPP + j) * kTilePieceBytes + (uint32_t)lane * 16
+                         : 0x80000000u;
+      asm volatile("" : "+v"(off));
+      tq[ck][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, kNonTemporal);
+    }
+    const int j = 4 * ck + g;
+    uint32_t soff = pair_live(j)
+                        ? (uint32_t)(pp0 + qw * WPP + j) * kTileScaleBytes + (uint32_t)r16 * 4
+                        : 0x80000000u;
+    asm volatile("" : "+v"(soff));
+    ts[ck] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff, 0, 0);
+  };
+#pragma unroll
+  for (int ck = 0; ck < RG; ++ck) load_chunk(ck);
+
+  // 2. B fragments of the split (stored columns past 3 MT zeroed once).
+  if constexpr (C::HALF) {
+    for (int kb = tid; kb < PADB; kb += NT)
+      *reinterpret_cast<u32x4*>(bfr + kb * C::FB + (P - 1) * 1024 + 512) = u32x4{0u, 0u, 0u, 0u};
+  }
+  if constexpr (C::PADC > 0) {
+    constexpr int PADC = C::PADC;
+    for (int it = tid; it < PADB * 4 * PADC; it += NT) {
+      const int kb = it / (4 * PADC), q = it % (4 * PADC);
+      const int c = q / PADC, vc = 3 * MT + q % PADC;
+      *reinterpret_cast<u32x4*>(bfr + bslot<MT, 4, P>(kb, vc >> 4, c, vc & 15)) =
+          u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int it = tid + NT * i;
+    if (XITEMS % NT != 0 && it >= XITEMS) continue;
+    const int m = it % MT, q = it / MT;
+    const int kb = q >> 2, c = q & 3;
+    const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                        xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) finite &= !__builtin_amdgcn_class(v[j], 0x207);  // NaN, +-Inf
+    uint32_t parts[3][4];
+    if (__builtin_expect(finite, 1))
+      split3_finite(v, parts[0], parts[1], parts[2]);
+    else
+      split3_any(v, parts[0], parts[1], parts[2]);
+#pragma unroll
+    for (int part = 0; part < 3; ++part) {
+      const int vc = part * MT + m;
+      *reinterpret_cast<u32x4*>(bfr + bslot<MT, 4, P>(kb, vc >> 4, c, vc & 15)) =
+          u32x4{parts[part][0], parts[part][1], parts[part][2], parts[part][3]};
+    }
+  }
+  __syncthreads();
+
+  // 3. Chunks in order as their loads land: P chained MFMAs per block, fp32
+  //    scale FMA into the even / odd accumulators (the kernels' arithmetic).
+  f32x4 accs[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  auto block_mma = [&](int kc, int kb, const bf16x8_t a, f32x4& a4) {
+    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, 4, P>(kb, 0, g, r16)),
+        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+    for (int p = 1; p < P; ++p)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          a, *reinterpret_cast<const bf16x8_t*>(bfr + bslot_rd<MT, 4, P>(kb, p, g, r16)), d, 0,
+          0, 0);
+    const f32x4 sc = *reinterpret_cast<const f32x4*>(&scl[wave][kc][4 * g]);
+    a4.x = __builtin_fmaf(sc.x, d.x, a4.x);
+    a4.y = __builtin_fmaf(sc.y, d.y, a4.y);
+    a4.z = __builtin_fmaf(sc.z, d.z, a4.z);
+    a4.w = __builtin_fmaf(sc.w, d.w, a4.w);
+  };
+#pragma unroll
+  for (int ck = 0; ck < NCK; ++ck) {
+    const int kbw = 2 * (qw * WPP + 4 * ck);  // first B-area block of the chunk
+    scl[wave][2 * g][r16] = scale_to_f32_fast(ts[ck] & 0xffffu);
+    scl[wave][2 * g + 1][r16] = scale_to_f32_fast(ts[ck] >> 16);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (4 * ck + u >= WPP) break;  // past the wave's share: nothing to add
+      const u32x4 q = tq[ck][u];
+      block_mma(2 * u, kbw + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
+      block_mma(2 * u + 1, kbw + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
+    }
+    if (ck + RG < NCK) load_chunk(ck + RG);
+  }
+  const f32x4 acc = accs[0] + accs[1];
+
+  // 4. The WG waves of a group add their sums in LDS (the B area is free after
+  //    the barrier); group sums of (token, row) in wave order.
+  __syncthreads();
+  float (*red)[16][17] = reinterpret_cast<float (*)[16][17]>(bfr);
+  red[wave][4 * g + 0][r16] = acc.x;
+  red[wave][4 * g + 1][r16] = acc.y;
+  red[wave][4 * g + 2][r16] = acc.z;
+  red[wave][4 * g + 3][r16] = acc.w;
+  __syncthreads();
+  auto group_sum = [&](int gl, int idx) {
+    const int m = idx >> 4, rr = idx & 15;
+    const int c0 = m, c1 = (MT + m) & 15, c2 = (2 * MT + m) & 15;
+    float t = 0.0f;
+#pragma unroll
+    for (int q4 = 0; q4 < WG; ++q4) {
+      const int wv = WG * gl + q4;
+      float s = red[wv][rr][c0];
+      if (c1 != c0) s += red[wv][rr][c1];
+      if (c2 != c0 && c2 != c1) s += red[wv][rr][c2];
+      t = q4 == 0 ? s : t + s;
+    }
+    return t;
+  };
+  // Output (group-local index idx = token m x 16 + row) of group gl -> y.
+  auto write_y = [&](int gl, int idx, float t) {
+    const unsigned gr = blockIdx.x * NG + gl;
+    if (gr >= grp_total) return;
+    const int s2 = seg_of(gr);
+    const unsigned g0 = s2 == 0 ? 0u : s2 == 1 ? args.grp_end[0] : args.grp_end[1];
+    float* y = s2 == 0 ? args.seg[0].y : s2 == 1 ? args.seg[1].y : args.seg[2].y;
+    const int n2 = s2 == 0 ? args.seg[0].N : s2 == 1 ? args.seg[1].N : args.seg[2].N;
+    const void* bias = s2 == 0 ? args.seg[0].bias : s2 == 1 ? args.seg[1].bias : args.seg[2].bias;
+    const int bias_bf16 =
+        s2 == 0 ? args.seg[0].bias_bf16 : s2 == 1 ? args.seg[1].bias_bf16 : args.seg[2].bias_bf16;
+    const int m = idx >> 4;
+    const int64_t n = (int64_t)(gr - g0) * 16 + (idx & 15);
+    if (m >= M || n >= n2) return;
+    y[(int64_t)m * n2 + n] = t + (bias ? bias_at(bias, bias_bf16, n) : 0.0f);
+  };
+
+  if (gridDim.y == 1) {
+    if (qw != 0) return;
+#pragma unroll
+    for (int o = 0; o < OPL; ++o) {
+      const int idx = lane + 64 * o;
+      if (idx < OUTS) write_y(lg, idx, group_sum(lg, idx));
+    }
+    return;
+  }
+
+  // 5. Split K: partials [tile][split][REGION] by device-scope stores, their
+  //    completion, the tile's counter; the last workgroup resets the counter and
+  //    adds the splits of every output in split order.
+  constexpr int SC1 = 16;  // cache-policy bit: device scope
+  const unsigned nspl = gridDim.y;
+  const __amdgpu_buffer_rsrc_t prs =
+      make_rsrc(partials + (int64_t)blockIdx.x * nspl * REGION, (uint32_t)(nspl * REGION * 4));
+  if (qw == 0) {
+#pragma unroll
+    for (int o = 0; o < OPL; ++o) {
+      const int idx = lane + 64 * o;
+      if (idx < OUTS)
+        __builtin_amdgcn_raw_buffer_store_b32(
+            __builtin_bit_cast(uint32_t, group_sum(lg, idx)), prs,
+            (uint32_t)((blockIdx.y * REGION + lg * OUTS + idx) * 4), 0, SC1);
+    }
+  }
+  uint32_t* const counter = counters + (size_t)blockIdx.x * kCounterStride;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // every partial has reached the coherence point
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid == 0)
+    arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  if (arrived != nspl - 1) return;
+  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int o = 0; o < RPT; ++o) {
+    const int r = tid + NT * o;
+    if (REGION % NT != 0 && r >= REGION) break;
+    float s = 0.0f;
+    for (unsigned sp = 0; sp < nspl; sp += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(
+                       prs, sp + j < nspl ? (uint32_t)(((sp + j) * REGION + r) * 4) : 0x80000000u,
+                       0, SC1));
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (sp + j < nspl) s += v[j];
+    }
+    write_y(r / OUTS, r % OUTS, s);
+  }
+}
+
+// Launch shapes of the hybrid decode (index = DecodeMfmaConfig::hyb): row
+// groups per workgroup, waves per group, blocks per split, 4-pair load chunks in
+// flight per wave.  Measured on MI355X (tiled weights, rotated copies), against
+// the split-K kernel's 13.0-13.5 / 14.5-15.5 us on down 4096 x 11008 at 4 / 8
+// tokens:
+//   1: 4 groups x 2 waves, 44-block splits, 2 chunks in flight: 64 x 8 = 512
+//      workgroups, two per CU: 11.98-12.21 / 13.68-13.81 us (picked);
+//      the same with 1 chunk in flight 15.3 / 17.2, all 3 up front 12.6 / 15.1;
+//   2: 8 groups x 1 wave, 44-block splits, 3 of 6 chunks in flight (256
+//      workgroups): 12.1-12.3 / 14.2-14.8 (all 6 up front: 14.5 / 16.1);
+//   3: 16 groups x 1 wave, 22-block splits, 2 of 3 chunks in flight: 13.4 / 16.6;
+//   4: 4 groups x 4 waves, 32-block splits, 1 chunk: 64 x 11 workgroups.
+// Other measured shapes (kept out): 9-10 splits (288-320 workgroups, more than
+// fit at once) 15.8-16.7 / 20-20.7; 2 groups per workgroup (1024 workgroups)
+// 14.4 / 18.7; 16 waves over 4 groups 12.5 / 17.0.  On K = 4096 (o_proj, gate,
+// qkv) every shape tried was slower than the kernels above.
+struct HybShape {
+  int ng, wg, spb, ring;
+};
+constexpr HybShape kHybShapes[] = {
+    {0, 0, 0, 0},
+    {4, 2, 44, 2},
+    {8, 1, 44, 3},
+    {16, 1, 22, 2},
+    {4, 4, 32, 1},
+};
+constexpr int kHybCount = sizeof(kHybShapes) / sizeof(kHybShapes[0]);
+
+template <int MT, int NG, int WG, int SPB, int RING>
+hipError_t launch_hyb_k(const float* x, const RowsArgs& a, int M, int K,
+                        const SplitKWorkspace& ws, hipStream_t stream) {
+  const unsigned groups = a.grp_end[a.count - 1];
+  const int KB = K / kBlockElems;
+  const dim3 grid((groups + NG - 1) / NG, (unsigned)((KB + SPB - 1) / SPB)), block(64 * WG * NG);
+  if (grid.y > 1 && (ws.partials == nullptr || ws.counters == nullptr))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemv_mfma_hyb_kernel<MT, NG, WG, SPB, RING>), grid, block, 0, stream, x, a,
+                     M, K, ws.partials, ws.counters);
+  return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_hyb(int hyb, const float* x, const LinearSegs& s, int M, int K,
+                      const SplitKWorkspace& ws, hipStream_t stream) {
+  const RowsArgs a = rows_args(s);
+  switch (hyb) {
+    case 1: return launch_hyb_k<MT, 4, 2, 44, 2>(x, a, M, K, ws, stream);
+    case 2: return launch_hyb_k<MT, 8, 1, 44, 3>(x, a, M, K, ws, stream);
+    case 3: return launch_hyb_k<MT, 16, 1, 22, 2>(x, a, M, K, ws, stream);
+    case 4: return launch_hyb_k<MT, 4, 4, 32, 1>(x, a, M, K, ws, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
 struct Grid {
   unsigned tiles, splits;
   DecodeArgs args;
@@ -1175,6 +1543,10 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
     const bool k_ok = K % 64 == 0 && K >= 2048 && K <= 4096;
     if (k_ok && (c.mt == 4 || c.mt == 8) && G >= 512 && G <= 1024) c.rows = 1;
     if (k_ok && c.mt == 4 && G >= 240 && G <= 256) c.rows = 1;
+    // Long rows over few row groups (down 4096 x 11008): the hybrid kernel, 4
+    // groups x 44-block splits per workgroup (at most 8 splits, so the 512
+    // workgroups of a 256-group weight are resident at once).
+    if ((c.mt == 4 || c.mt == 8) && K >= 8192 && KB <= 8 * 44 && G <= 256) c.hyb = 1;
     return c;
   }
   c.waves = (c.mt >= 4 && N >= 8192) ? 8 : 4;
@@ -1214,7 +1586,27 @@ static bool rows_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
   return (G >= 512 && G <= 1024) || (c.mt == 4 && G >= 240 && G <= 256);
 }
 
+// The launches the hybrid kernel takes: 1-3 plain outputs on tiled weights, 4 or
+// 8 tokens.
+static bool hyb_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
+  return c.hyb > 0 && c.hyb < kHybCount && (c.mt == 4 || c.mt == 8) && s.count >= 1 &&
+         s.count <= 3 && s.mode == Epilogue::kPlain && s.layout == WeightLayout::kTiled;
+}
+
 SplitKNeed decode_mfma_workspace_segs(const DecodeMfmaConfig& c, const LinearSegs& s, int K) {
+  if (hyb_takes(c, s)) {
+    const HybShape h = kHybShapes[c.hyb];
+    const RowsArgs a = rows_args(s);
+    const size_t tiles = (a.grp_end[a.count - 1] + h.ng - 1) / h.ng;
+    const int splits = (K / kBlockElems + h.spb - 1) / h.spb;
+    SplitKNeed need;
+    need.splits = splits;
+    if (splits > 1) {
+      need.partial_floats = tiles * splits * (size_t)h.ng * 16 * c.mt;
+      need.counters = tiles * kCounterStride;
+    }
+    return need;
+  }
   if (rows_takes(c, s)) return SplitKNeed{};  // no split K, no workspace
   const Grid gr = grid_of(c, s, K);
   SplitKNeed need;
@@ -1248,6 +1640,11 @@ hipError_t launch_gemv_mfma_segs(const DecodeMfmaConfig& c, const float* x,
     return hipErrorInvalidValue;
   for (int i = 0; i < s.count; ++i)
     if (!decode_mfma_fits(c, M, s.seg[i].N, K) || s.seg[i].N <= 0) return hipErrorInvalidValue;
+  if (hyb_takes(c, s)) {
+    if (M > c.mt) return hipErrorInvalidValue;
+    if (c.mt == 4) return launch_hyb<4>(c.hyb, x, s, M, K, ws, stream);
+    return launch_hyb<8>(c.hyb, x, s, M, K, ws, stream);
+  }
   if (rows_takes(c, s)) {
     if (M > c.mt || K % 64 != 0) return hipErrorInvalidValue;
     if (c.mt == 4) return launch_rows<4>(x, s, M, K, stream);

@@ -32,6 +32,8 @@ struct DecodeMfmaConfig {
   int rows = 0;  // 1: row-range kernel, no split K (tiled Linears with 1-3 plain
                  // outputs, mt 4 or 8, see decode_mfma_pick); the fields above then
                  // serve launches it does not take (SwiGLU, other group counts)
+  int hyb = 0;   // > 0: launch shape of the hybrid kernel (row groups x a short K
+                 // split; tiled Linears with 1-3 plain outputs, mt 4 or 8)
 };
 struct SplitKNeed {
   int splits = 1;             // workgroups along K

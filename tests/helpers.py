@@ -57,6 +57,14 @@ def rows_decode(M, N, K):
     return ((four or 6 <= M <= 8) and 512 <= G <= 1024) or (four and 240 <= G <= 256)
 
 
+def hybrid_decode(M, N, K):
+    """The C ABI's choice of the hybrid MFMA decode (row groups x a short K split)
+    for a tiled plain Linear (mle::decode_mfma_pick): 3-4 or 6-8 tokens, rows of
+    8192+ elements in at most 8 splits of 44 blocks, at most 256 16-row groups."""
+    G = (N + 15) // 16
+    return (M in (3, 4) or 6 <= M <= 8) and K >= 8192 and K // 32 <= 8 * 44 and G <= 256
+
+
 def rows_decode_swiglu(M, N, K):
     """The C ABI's choice of the row-range MFMA decode for a tiled gate/up SwiGLU
     launch (mle::decode_mfma_pick_segs): K 2048-4096 in steps of 64, 3-4 or 6-8

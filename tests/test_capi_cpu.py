@@ -197,10 +197,21 @@ def test_linear_ex_rejects_bad_launch_shape():
     assert rc == 1 and "launch shape" in capi.last_error()
     rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 5, 0, 0, 0, 0, None)
     assert rc == 1 and "path" in capi.last_error()
-    # MFMA decode: token tile 3 does not exist, 6 waves is not a shape, 65 splits too many
-    for t in [(3, 4, 16, 0), (4, 6, 16, 0), (4, 4, 16, 1), (4, 4, 8, 0), (16, 4, 32, 0)]:
+    # MFMA decode: token tile 3 does not exist, 6 waves is not a shape, 8-block slices
+    # and 16-token 32-block slices do not exist
+    for t in [(3, 4, 16, 0), (4, 6, 16, 0), (4, 4, 8, 0), (16, 4, 32, 0)]:
         rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 3, *t, None)
         assert rc == 1 and "MFMA decode shape" in capi.last_error(), t
+    # hybrid MFMA decode shapes (t3 = 1..4): tiled weights and a 4- or 8-token tile only
+    for t in [(4, 4, 16, 1), (8, 4, 16, 4)]:
+        rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 3, *t, None)
+        assert rc == 1 and "hybrid MFMA decode shape" in capi.last_error(), t
+    fake16 = FAKE + 64 - FAKE % 64  # 16-byte aligned, never dereferenced
+    for t in [(2, 4, 16, 1), (4, 4, 16, 5), (8, 4, 16, -1)]:
+        rc = lib.mle_q8_0_linear_tiled_ex(FAKE, fake16, None, FAKE, 1, 64, 64, 3, *t, None)
+        assert rc == 1 and "MFMA decode shape" in capi.last_error(), t
+    rc = lib.mle_q8_0_linear_tiled_ex(FAKE, fake16, None, FAKE, 1, 64, 64, 2, 0, 0, 0, 0, None)
+    assert rc == 1 and "path on tiled weights" in capi.last_error()
     # MFMA GEMM: t3 unused, 65 splits too many, 1 / 192 tile rows, 80 tile columns,
     # 256 x 128 tiles
     for t in [(0, 0, 0, 1), (65, 0, 0, 0), (2, 1, 0, 0), (0, 192, 0, 0), (1, 128, 80, 0),
@@ -358,10 +369,13 @@ def test_workspace_size_matches_launch_plan():
     assert ws(capi.OP_LINEAR, 1, [4096], 4096, tiled=True) == (0, 0)  # tiled GEMV
     b, c = ws(capi.OP_LINEAR, 8, [4096], 11008)                       # MFMA decode, 22 splits
     # every row x 22 K slices x 8 tokens of partial floats; 32 counters per row tile
-    # (4-wave tiles of 64 rows, raw and tiled: rows this long take 4-wave tiles when
-    # tiled too; o_proj's 4096-element rows take 8-wave tiles of 128 rows when tiled)
+    # (4-wave tiles of 64 rows; o_proj's 4096-element rows take 8-wave tiles of 128
+    # rows when tiled)
     assert b == 4096 * 22 * 8 * 4 and c == (4096 // 64) * 32
-    assert ws(capi.OP_LINEAR, 8, [4096], 11008, tiled=True) == (b, (4096 // 64) * 32)
+    # tiled, the hybrid decode: every row x 8 splits of 44 blocks x 8 tokens, one
+    # counter line per 4-group (64-row) workgroup column
+    assert ws(capi.OP_LINEAR, 8, [4096], 11008, tiled=True) == (4096 * 8 * 8 * 4,
+                                                                (4096 // 64) * 32)
     bo, co = ws(capi.OP_LINEAR, 8, [4096], 4096, tiled=True)         # o_proj: 8 splits
     assert bo == 4096 * 8 * 8 * 4 and co == (4096 // 128) * 32
     bg, cg = ws(capi.OP_LINEAR, 512, [11008], 4096)                   # prefill GEMM

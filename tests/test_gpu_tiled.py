@@ -7,9 +7,10 @@
   against the raw entry points wherever both run the MFMA decode or the bf16
   MFMA GEMM (same arithmetic, same accumulation order); where the tiled entry
   point runs its FP32 GEMV (one token, two below vocabulary-sized outputs, up to
-  four on short rows: ``tiled_gemv`` below mirrors the C ABI's choice) or its
-  row-range MFMA decode (``helpers.rows_decode``) within relative L2 1e-6 of the
-  raw entry point; and always against the CPU oracle
+  four on short rows: ``tiled_gemv`` below mirrors the C ABI's choice), its
+  row-range MFMA decode (``helpers.rows_decode``) or its hybrid MFMA decode
+  (``helpers.hybrid_decode``) within relative L2 1e-6 of the raw entry point; and
+  always against the CPU oracle
   (reference cpu_kernels.cpp:208-218) at the Linear bars: relative L2 <= 1e-5
   for M < 64 (FP32 GEMV, FP32-exact MFMA decode), <= 1e-2 for M >= 64 (bf16
   GEMM).
@@ -19,7 +20,8 @@ import functools
 import numpy as np
 import pytest
 
-from helpers import (assert_bitexact, empty_f32, note, rel_l2, rows_decode, rows_decode_multi,
+from helpers import (assert_bitexact, empty_f32, hybrid_decode, note, rel_l2, rows_decode,
+                     rows_decode_multi,
                      rows_decode_swiglu,
                      tile_ref, to_dev, to_host)
 from llmengine_amd import capi
@@ -104,8 +106,9 @@ def test_linear_tiled_matches_raw_and_oracle(dev, orc, M, N, K, has_bias):
     capi.linear(dx, dw, db, y_raw, M, N, K)
     capi.linear_tiled(dx, dt, db, y_t, M, N, K)
     got = to_host(y_t)
-    # bit for bit where both run the split-K MFMA decode or the GEMM
-    exact = not tiled_gemv(M, N, K) and not rows_decode(M, N, K)
+    # bit for bit where both run the split-K MFMA decode or the GEMM (the tiled GEMV,
+    # the row-range and the hybrid decode group the K sum differently)
+    exact = not tiled_gemv(M, N, K) and not rows_decode(M, N, K) and not hybrid_decode(M, N, K)
     same_or_close(got, to_host(y_raw), exact, "tiled vs raw")
     if M * N * K <= 64 * 1024 * 1024:
         assert rel_l2(got, orc.linear(x, raw, bias, M, N, K)) <= tol(M)
@@ -274,9 +277,10 @@ def test_llama_decode_set_tiled(dev, M):
                        (ys_r[2], ys_t[2], "v"), (g_r, g_t, "gate/up"), (o_r, o_t, "o"),
                        (d_r, d_t, "down")]:
         # the row-range decode on tiled weights: o_proj at M = 4, q/k/v and the
-        # gate/up SwiGLU at M = 4 and 8
-        rows = (rows_decode(M, H, K) if what == "o" else
-                rows_decode_multi(M, (H, H, H), K) if what in "qkv" else
-                rows_decode_swiglu(M, F, K) if what == "gate/up" else False)
-        exact = M > 2 and not rows
+        # gate/up SwiGLU at M = 4 and 8; the hybrid decode: down at M = 4 and 8
+        other = (rows_decode(M, H, K) if what == "o" else
+                 rows_decode_multi(M, (H, H, H), K) if what in "qkv" else
+                 rows_decode_swiglu(M, F, K) if what == "gate/up" else
+                 hybrid_decode(M, H, F))
+        exact = M > 2 and not other
         same_or_close(to_host(b), to_host(a), exact, what)
