@@ -66,7 +66,8 @@ PARITY_ROWS = 64                 # output rows (n) sampled per shape for the par
 # `bench.py --profile-kernel M,N,K[,tiled]` (FETCH_SIZE scaled by a device copy's
 # read/write ratio), keyed by (layout, M, N, K); the summaries are in profiles/.
 MEASURED_TRAFFIC = {("raw", 8, 4096, 11008): 57.242e6, ("raw", 8, 12288, 4096): 61.358e6,
-                    ("tiled", 8, 4096, 11008): 56.787e6, ("tiled", 8, 12288, 4096): 55.104e6,
+                    ("tiled", 8, 4096, 11008): 53.098e6, ("tiled", 4, 4096, 11008): 50.564e6,
+                    ("tiled", 8, 12288, 4096): 55.104e6,
                     ("tiled", 4, 11008, 4096): 48.734e6, ("tiled", 1, 4096, 11008): 48.306e6,
                     ("raw", 512, 11008, 4096): 152.297e6, ("tiled", 512, 11008, 4096): 152.287e6}
 
@@ -101,6 +102,14 @@ def rows_decode_wins(M, N, K):
     return ((four or 6 <= M <= 8) and 512 <= G <= 1024) or (four and 240 <= G <= 256)
 
 
+def hybrid_decode_wins(M, N, K):
+    """mle_q8_0_linear_tiled's choice of its hybrid MFMA decode (mle::decode_mfma_pick):
+    3-4 or 6-8 tokens, rows of 8192+ elements in at most 8 splits of 44 blocks, at most
+    256 16-row groups."""
+    G = (N + 15) // 16
+    return (M in (3, 4) or 6 <= M <= 8) and K >= 8192 and K // 32 <= 8 * 44 and G <= 256
+
+
 def decode_kernel_name(M, layout="raw", N=4096, K=4096):
     """Kernel the C ABI runs for an M-token Linear (mle_q8_0_linear[_tiled] path choice)."""
     if M == 1 and layout == "raw":
@@ -110,6 +119,9 @@ def decode_kernel_name(M, layout="raw", N=4096, K=4096):
     if layout == "tiled" and rows_decode_wins(M, N, K):
         return ("gemv_mfma_rows_kernel (MFMA decode without split K, exact bf16 activation "
                 "split, tiled weights)")
+    if layout == "tiled" and hybrid_decode_wins(M, N, K):
+        return ("gemv_mfma_hyb_kernel (hybrid MFMA decode: 4 row groups x 44-block K splits "
+                "per workgroup, exact bf16 activation split, tiled weights)")
     if M < 64:
         return ("gemv_q8_0_mfma_kernel (MFMA decode, exact bf16 activation split"
                 + (", tiled weights)" if layout == "tiled" else ")"))
