@@ -6,15 +6,16 @@ of another shape run on the capturing stream at the same time (captured calls us
 stream's graph workspace, which no eager call shares), and after a later eager call has
 outgrown the reservation -- gives the eager results bit for bit.  Shapes:
 the split-K MFMA decode (M = 8, 22 splits), the tiled FP32 GEMV (M = 1), the bf16 GEMM
-with its X pre-pass (M = 96) and the row-range MFMA decode (M = 4 on 512 tiled row
-groups, no workspace).  The kernels
+with its X pre-pass (M = 96), the row-range MFMA decode (M = 4 on 512 tiled row
+groups, no workspace) and the hybrid MFMA decode (M = 8 on tiled rows of 11008
+elements, 8 splits through the workspace).  The kernels
 reset their split-K counters themselves and the workspace counters were cleared by a
 fill kernel at allocation, so no memset node enters the graph.
 """
 import numpy as np
 import pytest
 
-from helpers import empty_f32, note, rel_l2, rows_decode, to_dev, to_host
+from helpers import empty_f32, hybrid_decode, note, rel_l2, rows_decode, to_dev, to_host
 from llmengine_amd import capi
 from llmengine_amd import synthetic as S
 
@@ -24,8 +25,9 @@ pytestmark = pytest.mark.gpu
 def test_linear_graph_replays_match_eager(dev, orc):
     import torch
     shapes = [(8, 1024, 11008, False), (1, 512, 4096, True), (96, 384, 1024, False),
-              (4, 8192, 4096, True)]
-    assert rows_decode(4, 8192, 4096)  # the last shape takes the row-range kernel
+              (4, 8192, 4096, True), (8, 1024, 11008, True)]
+    assert rows_decode(4, 8192, 4096)  # the fourth shape takes the row-range kernel
+    assert hybrid_decode(8, 1024, 11008)  # the last one the hybrid kernel
     stream = torch.cuda.Stream()
     need_b = need_c = 0
     cases = []
