@@ -367,7 +367,9 @@ size_t mle_q8_0_bytes(int64_t numel);
  *   FP32-exact activations for any M, 0 = automatic) and an optional launch
  *   shape t0..t3 (all four 0 = automatic):
  *     path 1: t0 = token tile mt in {1,2,4,8} >= min(M,8), t1 = lanes per row
- *             in {16,32,64}, t2 = rows per lane group in {1,2,4,8}, t3 = 0;
+ *             in {16,32,64}, t2 = rows per lane group in {1,2,4,8}, t3 = 0,
+ *             or t0 = 1 and t3 = 4: the row-span kernel on raw weights (one
+ *             token, 4 rows per workgroup, lanes along K; t1, t2 unused);
  *     path 2: t0 = K splits in [1, 64], t1 = tile rows in {128, 256},
  *             t2 = tile columns in {64, 96, 128} (at most 96 for 256 rows),
  *             t3 = 0 (a 0 among t0..t2 keeps that field automatic);

@@ -173,10 +173,11 @@ def linear_noalloc(x, w, bias, y, M, N, K, stream=None) -> None:
 
 
 def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice=0,
-              splits=0, bm=0, bn=0, hyb=0, stream=None, tiled=False) -> None:
+              splits=0, bm=0, bn=0, hyb=0, rpw=0, stream=None, tiled=False) -> None:
     """Linear with a forced path and launch shape (test / tuning hook).
 
-    path 1 (FP32 GEMV) takes mt, lpr, rw; path 2 (MFMA GEMM) takes splits, bm, bn;
+    path 1 (FP32 GEMV) takes mt, lpr, rw, or mt and rpw (the row-span kernel on
+    raw weights, rpw rows per workgroup); path 2 (MFMA GEMM) takes splits, bm, bn;
     path 3 (MFMA decode) takes mt, waves, kslice and hyb (a hybrid-kernel launch
     shape, tiled weights); zero = automatic.  tiled: W in 16-row tiles (path 0 or 3)."""
     if path == 3:
@@ -184,7 +185,7 @@ def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice
     elif path == 2:
         t = (splits, bm, bn, 0)
     else:
-        t = (mt, lpr, rw, 0)
+        t = (mt, lpr or (64 if rpw else 0), rw or (1 if rpw else 0), rpw)
     fn = load().mle_q8_0_linear_tiled_ex if tiled else load().mle_q8_0_linear_ex
     rc = fn(_addr(x), _addr(w), _addr(bias), _addr(y), M, N, K, path, *t, _stream(stream))
     _raise(rc)

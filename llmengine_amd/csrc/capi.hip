@@ -393,7 +393,8 @@ int run_segs(const char* ctx, const float* x, const mle::LinearSegs& s, int M, i
                         "hip Q8_0 fused Linear launch failed");
   }
   if (!tiled && (swi ? M == 1 : pick_path(M, total_n, K) == 1)) {
-    const mle::GemvConfig c = mle::gemv_pick_config(M, total_n, K);
+    mle::GemvConfig c = mle::gemv_pick_config(M, total_n, K);
+    if (swi) c.rpw = 0;  // the row-span kernel has no SwiGLU epilogue
     return check_launch((ex.planning() ? hipSuccess : mle::launch_gemv_segs(c, x, s, M, K, ex.stream)),
                         "hip Q8_0 fused Linear launch failed");
   }
@@ -554,12 +555,12 @@ int linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias, float* y
   const bool all_zero = t0 == 0 && t1 == 0 && t2 == 0 && t3 == 0;
   if (!all_zero) {
     if (path == 1) {
-      tune.gemv = mle::GemvConfig{t0, t1, t2};
-      if (t3 != 0 || !mle::gemv_config_valid(tune.gemv))
+      tune.gemv = mle::GemvConfig{t0, t1, t2, t3};
+      if (!mle::gemv_config_valid(tune.gemv))
         return fail(MLE_INVALID_ARGUMENT,
                     "hip sgemm_nt_q8_0_weight: invalid GEMV launch shape (mt " +
                         std::to_string(t0) + ", lpr " + std::to_string(t1) + ", rw " +
-                        std::to_string(t2) + ")");
+                        std::to_string(t2) + ", rpw " + std::to_string(t3) + ")");
     } else if (path == 3) {
       tune.dec = mle::DecodeMfmaConfig{t0, t1, t2};
       tune.dec.hyb = t3;

@@ -241,6 +241,161 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(const float* __restrict_
   }
 }
 
+// Row-span GEMV on raw weights, one token, lanes along K.  A workgroup owns
+// RPW = 4 consecutive rows of a weight and all of K; wave w (of up to 8) takes
+// the 64-block chunks c = w, w + waves, .. and lane l block 64 c + l of every
+// row.  So a wave's load instruction reads 64 consecutive blocks of one row
+// (2176 contiguous bytes), and the lane loads the 32 activations of its block
+// once, straight into registers, for all RPW rows: no LDS staging, no barrier
+// before the first multiply.  Per row the lane realigns its block, forms
+// s = sum_j x_j q_j over the 32 quants in fp32 FMAs and adds d * s; the loads of
+// all RPW rows are in flight before the first multiply.  Lanes past K read zeros
+// (buffer range check).  The 64 lanes' sums are added by a transposing butterfly
+// (each exchange halves the values a lane holds), the waves' totals in LDS in
+// wave order: deterministic.
+//
+// Measured on MI355X against the LDS-staged kernel above (one token, rotated
+// weight copies): 0.93x on [4096, 11008], 0.94x on [4096, 4096], 0.78x on the
+// [896, 4864] Qwen down projection; 1.05x on [12288, 4096] and equal on
+// [11008, 4096], so it takes outputs up to 4096 only.  Eight or 16 rows per
+// workgroup cut the activation reads (every workgroup reads all of x) but were
+// slower: 1.1-1.3x with four rows in flight per lane, 1.7-1.9x with eight
+// (each lane's whole share requested up front).
+constexpr int kRawkRows = 4;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemv_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// Sums each of the V per-lane values v[0..V) over the wave's 64 lanes (V a power
+// of two, <= 64).  On return v[0] of lane l holds the total of value l >> (6 - log2 V).
+template <int V>
+__device__ __forceinline__ void wave_sum_transpose(float (&v)[V], int lane) {
+  int n = V;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    if (n > 1) {
+      const int h = n / 2;
+      const bool up = (lane & o) != 0;
+#pragma unroll
+      for (int i = 0; i < V / 2; ++i) {
+        if (i >= h) break;
+        const float keep = up ? v[i + h] : v[i];
+        const float give = up ? v[i] : v[i + h];
+        v[i] = keep + __shfl_xor(give, o);
+      }
+      n = h;
+    } else {
+      v[0] += __shfl_xor(v[0], o);
+    }
+  }
+}
+
+template <int RPW>
+__global__ __launch_bounds__(512) void gemv_rawk_kernel(const float* __restrict__ x,
+                                                         const GemvArgs args, int K) {
+  static_assert(RPW == 4 || RPW == 8 || RPW == 16, "the row sums fit one butterfly");
+  constexpr int SHIFT = RPW == 16 ? 2 : RPW == 8 ? 3 : 4;
+  __shared__ float red[8][RPW];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const unsigned wg = blockIdx.x;
+  const int si = (args.count > 1 && wg >= args.wg_end[0])
+                     ? ((args.count > 2 && wg >= args.wg_end[1]) ? 2 : 1)
+                     : 0;
+  const unsigned wg0 = si == 0 ? 0u : si == 1 ? args.wg_end[0] : args.wg_end[1];
+  const uint8_t* w = si == 0 ? args.seg[0].w : si == 1 ? args.seg[1].w : args.seg[2].w;
+  const void* bias = si == 0 ? args.seg[0].bias : si == 1 ? args.seg[1].bias : args.seg[2].bias;
+  const int bias_bf16 =
+      si == 0 ? args.seg[0].bias_bf16 : si == 1 ? args.seg[1].bias_bf16 : args.seg[2].bias_bf16;
+  float* y = si == 0 ? args.seg[0].y : si == 1 ? args.seg[1].y : args.seg[2].y;
+  const int N = si == 0 ? args.seg[0].N : si == 1 ? args.seg[1].N : args.seg[2].N;
+  const int64_t row0 = (int64_t)(wg - wg0) * RPW;
+  const int KB = K / kBlockElems;
+  const uint32_t row_bytes = (uint32_t)KB * kBlockBytes;
+  // Buffer over this workgroup's rows (rows past N read as zero); a block's
+  // offset is relative to the first row, so its byte phase is the base's plus
+  // the offset's.
+  const int64_t live_rows = N - row0 < RPW ? N - row0 : RPW;
+  const uint8_t* base = w + row0 * row_bytes;
+  const __amdgpu_buffer_rsrc_t wrs = gemv_rsrc(base, (uint32_t)(live_rows * row_bytes));
+  const uint32_t phase = (uint32_t)((uintptr_t)base & 2u);
+  const __amdgpu_buffer_rsrc_t xrs = gemv_rsrc(x, (uint32_t)K * 4u);
+
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+  for (int c = wave; c * 64 < KB; c += nw) {
+    const int b = c * 64 + lane;
+    const bool live = b < KB;
+    f32x4 xv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t off = live ? (uint32_t)((b * kBlockElems + 4 * j) * 4) : 0x80000000u;
+      xv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+    }
+    // Block b of row r: two 16-byte loads from the 4-aligned address at or after
+    // the block and the remaining u16 (load_block_raw's cases A and B).
+    RawBlock rb[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const uint32_t off = (uint32_t)r * row_bytes + (uint32_t)b * kBlockBytes;
+      const uint32_t mis = (phase + off) & 2u;
+      uint32_t v8 = live ? off + mis : 0x80000000u;
+      uint32_t v2 = live ? off + (mis ? 0u : 32u) : 0x80000000u;
+      asm volatile("" : "+v"(v8), "+v"(v2));  // the loads stay where they are written
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, 0, 0);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, 0, 0);
+      rb[r].v0 = u32x4_a4{v0.x, v0.y, v0.z, v0.w};
+      rb[r].v1 = u32x4_a4{v1.x, v1.y, v1.z, v1.w};
+      rb[r].u = __builtin_amdgcn_raw_buffer_load_b16(wrs, v2, 0, 0);
+      rb[r].mis = mis;
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const Block blk = finish_block(rb[r]);
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t q = blk.q[j];
+        s = __builtin_fmaf(xv[j].x, q_at(q, 0), s);
+        s = __builtin_fmaf(xv[j].y, q_at(q, 1), s);
+        s = __builtin_fmaf(xv[j].z, q_at(q, 2), s);
+        s = __builtin_fmaf(xv[j].w, q_at(q, 3), s);
+      }
+      acc[r] = __builtin_fmaf(scale_to_f32_fast(blk.scale_bits), s, acc[r]);
+    }
+  }
+  wave_sum_transpose<RPW>(acc, lane);
+  if ((lane & ((1 << SHIFT) - 1)) == 0) red[wave][lane >> SHIFT] = acc[0];
+  __syncthreads();
+  if (wave != 0 || lane >= RPW) return;
+  const int64_t n = row0 + lane;
+  if (n >= N) return;
+  float sum = 0.0f;
+  for (int wi = 0; wi < nw; ++wi) sum += red[wi][lane];
+  y[n] = sum + (bias ? bias_at(bias, bias_bf16, n) : 0.0f);
+}
+
+hipError_t launch_rawk(const float* x, const LinearSegs& s, int M, int K, hipStream_t stream) {
+  if (M != 1 || s.mode != Epilogue::kPlain) return hipErrorInvalidValue;
+  GemvArgs args{};
+  int64_t grid = 0;
+  for (int i = 0; i < 3; ++i) {
+    args.seg[i] = s.seg[i];
+    if (i < s.count) grid += ((int64_t)s.seg[i].N + kRawkRows - 1) / kRawkRows;
+    args.wg_end[i] = (unsigned)grid;
+  }
+  args.count = s.count;
+  const int chunks = (K / kBlockElems + 63) / 64;
+  const unsigned threads = 64u * (unsigned)(chunks < 8 ? chunks : 8);
+  hipLaunchKernelGGL((gemv_rawk_kernel<kRawkRows>), dim3((unsigned)grid), dim3(threads), 0,
+                     stream, x, args, K);
+  return hipGetLastError();
+}
+
 // Bytes of staged activations per workgroup: all of K in one chunk up to 384
 // blocks at one token (the Llama down projection, K = 11008, in one pass: a
 // second chunk drains the load ring behind two barriers mid-row).
@@ -309,6 +464,7 @@ hipError_t dispatch_lpr(int lpr, int rw, const float* x, const LinearSegs& s, in
 }  // namespace
 
 bool gemv_config_valid(const GemvConfig& c) {
+  if (c.rpw != 0) return c.mt == 1 && c.rpw == kRawkRows;
   const bool mt = c.mt == 1 || c.mt == 2 || c.mt == 4 || c.mt == 8;
   const bool lpr = c.lpr == 16 || c.lpr == 32 || c.lpr == 64;
   const bool rw = c.rw == 1 || c.rw == 2 || c.rw == 4 || c.rw == 8;
@@ -330,6 +486,9 @@ GemvConfig gemv_pick_config(int M, int N, int K) {
   const bool two = c.mt == 8 || (c.lpr == 64 && c.mt == 1 && N > 2048) ||
                    (c.lpr == 32 && c.mt >= 4) || (c.lpr == 32 && c.mt == 2 && N >= 8192);
   c.rw = two ? 2 : 1;
+  // One token on rows of 2048+ elements and at most 4096 outputs: the row-span
+  // kernel (measured figures at gemv_rawk_kernel).
+  if (M == 1 && K >= 2048 && N <= 4096) c.rpw = kRawkRows;
   return c;
 }
 
@@ -337,6 +496,10 @@ hipError_t launch_gemv_segs(const GemvConfig& cfg, const float* x, const LinearS
                             int K, hipStream_t stream) {
   if (s.count < 1 || s.count > 3 || (s.mode == Epilogue::kSwiGLU && s.count != 2))
     return hipErrorInvalidValue;
+  if (cfg.rpw != 0) {
+    if (!gemv_config_valid(cfg)) return hipErrorInvalidValue;
+    return launch_rawk(x, s, M, K, stream);
+  }
   switch (cfg.mt) {
     case 1: return dispatch_lpr<1>(cfg.lpr, cfg.rw, x, s, M, K, stream);
     case 2: return dispatch_lpr<2>(cfg.lpr, cfg.rw, x, s, M, K, stream);

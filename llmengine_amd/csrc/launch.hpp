@@ -14,6 +14,9 @@ struct GemvConfig {
   int mt;   // token tile: 1, 2, 4 or 8 (>= M)
   int lpr;  // lanes cooperating on one output row: 16, 32 or 64
   int rw;   // output rows per lane group: 1, 2, 4 or 8
+  // Nonzero: the row-span kernel on raw weights instead (one token, lanes along
+  // K, rpw = 4 rows per workgroup; lpr and rw unused).
+  int rpw = 0;
 };
 GemvConfig gemv_pick_config(int M, int N, int K);
 bool gemv_config_valid(const GemvConfig& c);

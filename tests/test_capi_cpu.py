@@ -197,6 +197,10 @@ def test_linear_ex_rejects_bad_launch_shape():
     assert rc == 1 and "launch shape" in capi.last_error()
     rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 5, 0, 0, 0, 0, None)
     assert rc == 1 and "path" in capi.last_error()
+    # row-span GEMV (t3 = rows per workgroup): 4 rows and a one-token tile only
+    for t in [(1, 64, 1, 8), (2, 64, 1, 4), (1, 64, 1, 16), (1, 64, 1, -4)]:
+        rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 1, *t, None)
+        assert rc == 1 and "GEMV launch shape" in capi.last_error(), t
     # MFMA decode: token tile 3 does not exist, 6 waves is not a shape, 8-block slices
     # and 16-token 32-block slices do not exist
     for t in [(3, 4, 16, 0), (4, 6, 16, 0), (4, 4, 8, 0), (16, 4, 32, 0)]:

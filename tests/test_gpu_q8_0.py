@@ -341,6 +341,75 @@ def test_linear_two_tokens_gemv(dev, orc, N, K):
         assert np.array_equal(bits(got), bits(forced)), rw
 
 
+# (N, K, byte shift of W): Llama o_proj / down, a ragged row count with 65 blocks per
+# row (the second 64-block chunk holds one live lane), the Qwen down projection (152
+# blocks: a partial last chunk), 10 chunks of 64 blocks over 8 waves (the chunk loop),
+# and W 2 bytes past a 4-byte boundary (every block at its other 4-byte phase).
+RAWK_CASES = [(4096, 4096, 0), (4096, 11008, 0), (515, 2080, 2), (896, 4864, 0),
+              (7, 20480, 2), (4096, 11008, 2)]
+
+
+@pytest.mark.parametrize("N,K,shift", RAWK_CASES)
+def test_linear_one_token_row_span(dev, orc, N, K, shift):
+    """One token on raw weights with rows of 2048+ elements and at most 4096 outputs
+    takes the row-span kernel (automatic path): with bias, against the oracle; within
+    1e-6 of the LDS-staged GEMV (forced launch shape); bitwise repeatable; a BFloat16
+    bias gives the widened fp32 bias's bits."""
+    import torch
+    M = 1
+    note(f"row-span GEMV {N}x{K} shift={shift}")
+    w, x = weight(90 + N, N, K), acts(91 + K, M, K)
+    b32 = S.activations(92, (N,), tag=S.TAG_BIAS)
+    b16 = (b32.view(np.uint32) >> 16).astype(np.uint16)
+    widened = (b16.astype(np.uint32) << 16).view(np.float32)
+    dx, dw = to_dev(x, dev), to_dev(w, dev)
+    if shift:
+        buf = torch.zeros(dw.numel() + shift, dtype=torch.uint8, device=dev)
+        buf[shift:] = dw
+        dw = buf[shift:]
+        assert dw.data_ptr() % 4 == shift
+    db = to_dev(widened, dev)
+    y, y2, y16, yold = (empty_f32((M, N), dev) for _ in range(4))
+    capi.linear(dx, dw, db, y, M, N, K)
+    capi.linear(dx, dw, db, y2, M, N, K)
+    capi.linear_bias_bf16(dx, dw, to_dev(b16, dev), y16, M, N, K)
+    capi.linear_ex(dx, dw, db, yold, M, N, K, path=1, mt=1, lpr=64, rw=1)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    assert torch.equal(y, y16)
+    got = to_host(y)
+    assert rel_l2(got, orc.linear(x, w, widened, M, N, K)) <= GEMV_TOL
+    assert rel_l2(got, to_host(yold)) <= 1e-6
+    forced = empty_f32((M, N), dev)
+    capi.linear_ex(dx, dw, db, forced, M, N, K, path=1, mt=1, rpw=4)
+    torch.cuda.synchronize()
+    assert torch.equal(y, forced)
+
+
+def test_linear_multi_one_token_row_span(dev, orc):
+    """A one-token multi-output Linear of at most 4096 outputs in all (q / k / v of a
+    small model) runs the row-span kernel over its three segments: each output
+    against the oracle and bit-equal to its single Linear (the same kernel)."""
+    import torch
+    M, K, Ns = 1, 2048, (1000, 24, 3000)
+    note(f"row-span multi {Ns} K={K}")
+    x = acts(93, M, K)
+    ws = [weight(94 + i, n, K) for i, n in enumerate(Ns)]
+    bs = [S.activations(97 + i, (n,), tag=S.TAG_BIAS) for i, n in enumerate(Ns)]
+    dx = to_dev(x, dev)
+    dws = [to_dev(w, dev) for w in ws]
+    dbs = [to_dev(b, dev) for b in bs]
+    ys = [empty_f32((M, n), dev) for n in Ns]
+    singles = [empty_f32((M, n), dev) for n in Ns]
+    capi.linear_multi(dx, dws, dbs, ys, list(Ns), M, K)
+    for dw, db, yy, n in zip(dws, dbs, singles, Ns):
+        capi.linear(dx, dw, db, yy, M, n, K)
+    torch.cuda.synchronize()
+    for i, n in enumerate(Ns):
+        assert torch.equal(ys[i], singles[i]), i
+        assert rel_l2(to_host(ys[i]), orc.linear(x, ws[i], bs[i], M, n, K)) <= GEMV_TOL, i
+
+
 # ----------------------------------------------------------------------------- linear MFMA decode
 
 DECODE_SHAPES = [(2, 16), (4, 16), (8, 16), (2, 32), (4, 32), (8, 32)]
