@@ -351,8 +351,8 @@ RAWK_CASES = [(4096, 4096, 0), (4096, 11008, 0), (515, 2080, 2), (896, 4864, 0),
 
 @pytest.mark.parametrize("N,K,shift", RAWK_CASES)
 def test_linear_one_token_row_span(dev, orc, N, K, shift):
-    """One token on raw weights with rows of 2048+ elements and at most 4096 outputs
-    takes the row-span kernel (automatic path): with bias, against the oracle; within
+    """One token on raw weights with rows of 2048+ elements takes the row-span kernel
+    (automatic path): with bias, against the oracle; within
     1e-6 of the LDS-staged GEMV (forced launch shape); bitwise repeatable; a BFloat16
     bias gives the widened fp32 bias's bits."""
     import torch
@@ -387,9 +387,9 @@ def test_linear_one_token_row_span(dev, orc, N, K, shift):
 
 
 def test_linear_multi_one_token_row_span(dev, orc):
-    """A one-token multi-output Linear of at most 4096 outputs in all (q / k / v of a
-    small model) runs the row-span kernel over its three segments: each output
-    against the oracle and bit-equal to its single Linear (the same kernel)."""
+    """A one-token multi-output Linear on rows of 2048+ elements runs the row-span
+    kernel over its three segments: each output against the oracle and bit-equal to
+    its single Linear (the same kernel)."""
     import torch
     M, K, Ns = 1, 2048, (1000, 24, 3000)
     note(f"row-span multi {Ns} K={K}")
