@@ -113,6 +113,8 @@ def hybrid_decode_wins(M, N, K):
 def decode_kernel_name(M, layout="raw", N=4096, K=4096):
     """Kernel the C ABI runs for an M-token Linear (mle_q8_0_linear[_tiled] path choice)."""
     if M == 1 and layout == "raw":
+        if K >= 2048:
+            return "gemv_rawk_kernel (FP32 GEMV, 4 rows per workgroup, lanes along K)"
         return "gemv_q8_0_kernel (FP32 GEMV)"
     if layout == "tiled" and tiled_gemv_wins(M, N, K):
         return "gemv_tiled_kernel (FP32 GEMV, tiled weights)"
@@ -475,6 +477,23 @@ def main():
                                     M, len(rows), K)
                 got = outs[layout][(M, name)][:, rows]
                 gate(f"decode {layout} M={M} {name} [{N}x{K}]", got, want, GEMV_BAR)
+    # Both paths against an FP64 evaluation of the same sampled rows (the configs[0]
+    # shape, 4096 x 4096, at every M): the GPU's rounding next to the reference CPU
+    # path's own (its sequential fp32 FMA chain over K).
+    fp64 = []
+    name, N, K = "o_proj", 4096, 4096
+    for M in MS:
+        rows = sample_rows(N, 100 * M + SEED_W[name])
+        wr = rows_of(weights_host[name], N, K, rows)
+        exact = xs_host[(M, K)].astype(np.float64) @ S.dequantize(wr, len(rows) * K).reshape(
+            len(rows), K).T
+        cpu_err = rel_l2(orc.sgemm_nt(xs_host[(M, K)], wr, M, len(rows), K), exact)
+        entry = {"M": M, "shape": f"[{N}x{K}]", "cpu_rel_l2_vs_fp64": float(f"{cpu_err:.3g}")}
+        for layout in ("tiled", "raw"):
+            gpu_err = rel_l2(outs[layout][(M, name)][:, rows], exact)
+            entry[f"gpu_{layout}_rel_l2_vs_fp64"] = float(f"{gpu_err:.3g}")
+        fp64.append(entry)
+    parity["fp64_error"] = fp64
     elapsed, value = timing["tiled"]
     raw_elapsed, raw_value = timing["raw"]
 
