@@ -221,12 +221,10 @@ bool gemv_tiled_config_valid(const TiledGemvConfig& c, bool swiglu) {
 
 TiledGemvConfig gemv_tiled_pick(int M, int rows, int K, bool swiglu) {
   // Measured on MI355X (Llama-7B and Qwen2.5-0.5B projections, Qwen lm_head,
-  // M = 1..4): chunks of 4 block pairs win everywhere; about 2-4 thousand
-  // waves in flight do, so waves per 16-row group = 65536 / rows rounded down
+  // M = 1..4): chunks of 4 block pairs win everywhere; about 2-3 thousand
+  // waves in flight do, so waves per 16-row group = 49152 / rows rounded down
   // to a power of two, at least 4 (a vocabulary-sized weight still gains from
   // 4), at most 16 (8 per weight for SwiGLU) and at most the chunks of a row.
-  // (16 rather than 8 waves on 4096-row weights: down [4096, 11008] 0.97x at one
-  // token, 0.93x at two; o_proj [4096, 4096] unchanged.)
   // `rows`: output rows of the launch (all segments; SwiGLU: one weight's).
   TiledGemvConfig c;
   c.mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
@@ -234,7 +232,7 @@ TiledGemvConfig gemv_tiled_pick(int M, int rows, int K, bool swiglu) {
   const int KP = (K / kBlockElems + 1) / 2;
   const int chunks = (KP + c.ppw - 1) / c.ppw;
   int w = 4;
-  while (w < 16 && (int64_t)(2 * w) * rows <= 65536) w *= 2;
+  while (w < 16 && (int64_t)(2 * w) * rows <= 49152) w *= 2;
   if (swiglu && w > 8) w = 8;
   c.wpg = w < chunks ? w : chunks;
   while (!gemv_tiled_config_valid(c, swiglu) && c.wpg > 1) --c.wpg;
