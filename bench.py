@@ -113,7 +113,7 @@ def hybrid_decode_wins(M, N, K):
 def decode_kernel_name(M, layout="raw", N=4096, K=4096):
     """Kernel the C ABI runs for an M-token Linear (mle_q8_0_linear[_tiled] path choice)."""
     if M == 1 and layout == "raw":
-        if K >= 2048:
+        if K > 4096:
             return "gemv_rawk_kernel (FP32 GEMV, 4 rows per workgroup, lanes along K)"
         return "gemv_q8_0_kernel (FP32 GEMV)"
     if layout == "tiled" and tiled_gemv_wins(M, N, K):

@@ -255,12 +255,13 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(const float* __restrict_
 // wave order: deterministic.
 //
 // Measured on MI355X against the LDS-staged kernel above (one token, rotated
-// weight copies): 0.93x on [4096, 11008], 0.94x on [4096, 4096], 0.78x on the
-// [896, 4864] Qwen down projection; 1.05x on [12288, 4096] and 0.98x on
-// [11008, 4096].  It takes every one-token launch on rows of 2048+ elements,
-// whatever the output count, so that a fused q / k / v launch and its single
-// Linears run the same kernel and agree bit for bit (a row's sum depends only on
-// K's split over lanes and waves).  Eight or 16 rows per
+// weight copies, three interleaved runs per build): 0.92x on [4096, 11008],
+// 0.82x on the [896, 4864] Qwen down projection; on rows of 4096 elements 0.95x
+// on [4096, 4096] but 1.03x on [12288, 4096] and [11008, 4096].  It takes the
+// one-token launches on rows of more than 4096 elements, whatever the output
+// count, so that a fused q / k / v launch and its single Linears run the same
+// kernel and agree bit for bit (a row's sum depends only on K's split over lanes
+// and waves).  Eight or 16 rows per
 // workgroup cut the activation reads (every workgroup reads all of x) but were
 // slower: 1.1-1.3x with four rows in flight per lane, 1.7-1.9x with eight
 // (each lane's whole share requested up front).
@@ -489,10 +490,11 @@ GemvConfig gemv_pick_config(int M, int N, int K) {
   const bool two = c.mt == 8 || (c.lpr == 64 && c.mt == 1 && N > 2048) ||
                    (c.lpr == 32 && c.mt >= 4) || (c.lpr == 32 && c.mt == 2 && N >= 8192);
   c.rw = two ? 2 : 1;
-  // One token on rows of 2048+ elements: the row-span kernel (measured figures
-  // at gemv_rawk_kernel; the rule ignores N, so fused and single launches agree).
+  // One token on rows of more than 4096 elements: the row-span kernel (measured
+  // figures at gemv_rawk_kernel; the rule ignores N, so fused and single
+  // launches agree).
   (void)N;
-  if (M == 1 && K >= 2048) c.rpw = kRawkRows;
+  if (M == 1 && K > 4096) c.rpw = kRawkRows;
   return c;
 }
 

@@ -37,7 +37,8 @@ def test_measured_traffic_table():
 
 
 def test_kernel_names_follow_the_path_choice():
-    assert "gemv_rawk_kernel" in bench.decode_kernel_name(1, "raw")
+    assert "gemv_rawk_kernel" in bench.decode_kernel_name(1, "raw", 4096, 11008)
+    assert "gemv_q8_0_kernel" in bench.decode_kernel_name(1, "raw")
     assert "gemv_q8_0_kernel" in bench.decode_kernel_name(1, "raw", 151936, 896)
     assert "gemv_tiled_kernel" in bench.decode_kernel_name(1, "tiled", 4096, 11008)
     assert "gemv_tiled_kernel" in bench.decode_kernel_name(2, "tiled", 4096, 4096)

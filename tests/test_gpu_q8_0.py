@@ -351,10 +351,10 @@ RAWK_CASES = [(4096, 4096, 0), (4096, 11008, 0), (515, 2080, 2), (896, 4864, 0),
 
 @pytest.mark.parametrize("N,K,shift", RAWK_CASES)
 def test_linear_one_token_row_span(dev, orc, N, K, shift):
-    """One token on raw weights with rows of 2048+ elements takes the row-span kernel
-    (automatic path): with bias, against the oracle; within
-    1e-6 of the LDS-staged GEMV (forced launch shape); bitwise repeatable; a BFloat16
-    bias gives the widened fp32 bias's bits."""
+    """The row-span kernel (forced launch shape; the automatic path for one token on
+    rows of more than 4096 elements): with bias, against the oracle; within 1e-6 of the
+    LDS-staged GEMV; bitwise repeatable; a BFloat16 bias gives the widened fp32 bias's
+    bits; bit-equal to the automatic path where that takes it."""
     import torch
     M = 1
     note(f"row-span GEMV {N}x{K} shift={shift}")
@@ -369,29 +369,28 @@ def test_linear_one_token_row_span(dev, orc, N, K, shift):
         dw = buf[shift:]
         assert dw.data_ptr() % 4 == shift
     db = to_dev(widened, dev)
-    y, y2, y16, yold = (empty_f32((M, N), dev) for _ in range(4))
-    capi.linear(dx, dw, db, y, M, N, K)
-    capi.linear(dx, dw, db, y2, M, N, K)
+    y, y2, y16, yold, auto = (empty_f32((M, N), dev) for _ in range(5))
+    for out in (y, y2):
+        capi.linear_ex(dx, dw, db, out, M, N, K, path=1, mt=1, rpw=4)
     capi.linear_bias_bf16(dx, dw, to_dev(b16, dev), y16, M, N, K)
     capi.linear_ex(dx, dw, db, yold, M, N, K, path=1, mt=1, lpr=64, rw=1)
+    capi.linear(dx, dw, db, auto, M, N, K)
     torch.cuda.synchronize()
     assert torch.equal(y, y2)
-    assert torch.equal(y, y16)
+    assert torch.equal(auto, y16)
     got = to_host(y)
     assert rel_l2(got, orc.linear(x, w, widened, M, N, K)) <= GEMV_TOL
     assert rel_l2(got, to_host(yold)) <= 1e-6
-    forced = empty_f32((M, N), dev)
-    capi.linear_ex(dx, dw, db, forced, M, N, K, path=1, mt=1, rpw=4)
-    torch.cuda.synchronize()
-    assert torch.equal(y, forced)
+    if K > 4096:
+        assert torch.equal(y, auto)
 
 
 def test_linear_multi_one_token_row_span(dev, orc):
-    """A one-token multi-output Linear on rows of 2048+ elements runs the row-span
-    kernel over its three segments: each output against the oracle and bit-equal to
-    its single Linear (the same kernel)."""
+    """A one-token multi-output Linear on rows of more than 4096 elements runs the
+    row-span kernel over its three segments: each output against the oracle and
+    bit-equal to its single Linear (the same kernel)."""
     import torch
-    M, K, Ns = 1, 2048, (1000, 24, 3000)
+    M, K, Ns = 1, 4864, (1000, 24, 3000)
     note(f"row-span multi {Ns} K={K}")
     x = acts(93, M, K)
     ws = [weight(94 + i, n, K) for i, n in enumerate(Ns)]
