@@ -1063,6 +1063,15 @@ hipError_t launch_rows(const float* x, const LinearSegs& s, int M, int K, hipStr
     return hipErrorInvalidValue;
   }
   if constexpr (MT == 4) {
+    constexpr int R = int(WeightLayout::kRaw);
+    if (s.layout == WeightLayout::kRaw) {
+      switch (rows_groups_per_workgroup(G)) {
+        case 2: return launch_rows_k<4, 2, 4, 128, 1, 2, 0, R>(x, a, M, K, stream);
+        case 3: return launch_rows_k<4, 3, 4, 128, 1, 2, 0, R>(x, a, M, K, stream);
+        case 4: return launch_rows_k<4, 4, 4, 128, 1, 2, 0, R>(x, a, M, K, stream);
+      }
+      return hipErrorInvalidValue;
+    }
     switch (rows_groups_per_workgroup(G)) {
       case 1: return launch_rows_k<4, 1, 16, 128, 1, 1>(x, a, M, K, stream);
       case 2: return launch_rows_k<4, 2, 4, 128, 1, 2>(x, a, M, K, stream);
@@ -1550,6 +1559,12 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
     return c;
   }
   c.waves = (c.mt >= 4 && N >= 8192) ? 8 : 4;
+  // Raw weights: the row-range kernel at 4 tokens on 512-1024 row groups of rows of
+  // 2048-4096 elements (Llama qkv / gate / up; whole 34-byte blocks per lane,
+  // transposed into the A fragments in registers): 0.89x the split-K launch.  Not
+  // at 8 tokens (1.00-1.01x) or on 256 groups (o_proj at 4 tokens: 1.01x).
+  const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
+  if (K % 64 == 0 && K >= 2048 && K <= 4096 && c.mt == 4 && G >= 512 && G <= 1024) c.rows = 1;
   return c;
 }
 
@@ -1579,10 +1594,12 @@ static bool rows_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
     const int64_t G = rows_args(s).grp_end[0];
     return s.count == 2 && (c.mt == 4 || c.mt == 8) && G >= 512 && G <= 1024;
   }
-  if (s.mode != Epilogue::kPlain || s.layout != WeightLayout::kTiled) return false;
+  if (s.mode != Epilogue::kPlain) return false;
   // The launch shapes exist for these group counts (segments rounded up to whole
-  // groups each, as the grid numbers them).
+  // groups each, as the grid numbers them); raw weights: 4 tokens on 512-1024.
   const int64_t G = rows_args(s).grp_end[s.count - 1];
+  if (s.layout != WeightLayout::kTiled)
+    return s.layout == WeightLayout::kRaw && c.mt == 4 && G >= 512 && G <= 1024;
   return (G >= 512 && G <= 1024) || (c.mt == 4 && G >= 240 && G <= 256);
 }
 

@@ -57,6 +57,14 @@ def rows_decode(M, N, K):
     return ((four or 6 <= M <= 8) and 512 <= G <= 1024) or (four and 240 <= G <= 256)
 
 
+def rows_decode_raw(M, N, K):
+    """The C ABI's choice of the row-range MFMA decode for a raw single- or
+    multi-output Linear (N = all outputs' rows): 3-4 tokens on 512-1024 16-row
+    groups, K 2048-4096 in steps of 64."""
+    G = (N + 15) // 16
+    return M in (3, 4) and 512 <= G <= 1024 and K % 64 == 0 and 2048 <= K <= 4096
+
+
 def hybrid_decode(M, N, K):
     """The C ABI's choice of the hybrid MFMA decode (row groups x a short K split)
     for a tiled plain Linear (mle::decode_mfma_pick): 3-4 or 6-8 tokens, rows of

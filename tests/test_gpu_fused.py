@@ -111,8 +111,10 @@ def test_multi_output_matches_oracle_and_single(dev, orc, M):
 def test_multi_output_llama_qkv(dev, orc, M, Ns):
     """q/k/v of a grouped-query ([4096, 4096], [1024, 4096] x 2) and a multi-head
     ([4096, 4096] x 3) layer: one launch equals three single Linears bit for bit
-    (at M=4 and 8 the fused multi-head launch uses 8-wave workgroups, the single
-    ones 4-wave) and each output is within 1e-5 relative L2 of the oracle."""
+    (at M=8 the fused multi-head launch uses 8-wave workgroups, the single ones
+    4-wave), except where the fused launch alone takes the row-range decode (4 tokens
+    on 512-1024 row groups: the multi-head layer's 768), within 1e-6 there; each
+    output is within 1e-5 relative L2 of the oracle."""
     import torch
     K = 4096
     hws = [weight(90 + i, n, K) for i, n in enumerate(Ns)]
@@ -127,11 +129,16 @@ def test_multi_output_llama_qkv(dev, orc, M, Ns):
             first = [y.clone() for y in ys]
         else:
             assert all(torch.equal(a, b) for a, b in zip(first, ys))
+    G = sum((n + 15) // 16 for n in Ns)
+    fused_rows = M in (3, 4) and 512 <= G <= 1024
     for i, n in enumerate(Ns):
         single = empty_f32((M, n), dev)
         capi.linear(dx, dws[i], None, single, M, n, K)
         torch.cuda.synchronize()
-        assert torch.equal(single, ys[i]), i
+        if fused_rows:
+            assert rel_l2(to_host(ys[i]), to_host(single)) <= 1e-6, i
+        else:
+            assert torch.equal(single, ys[i]), i
         assert rel_l2(to_host(ys[i]), orc.sgemm_nt(hx, hws[i], M, n, K)) <= 1e-5, i
 
 

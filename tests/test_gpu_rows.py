@@ -4,9 +4,12 @@ launches for which mle::decode_mfma_pick sets DecodeMfmaConfig::rows).  Each wor
 16-row groups and all of K, so there is no split-K hand-off and no workspace.
 
 Checked against the CPU oracle (reference cpu_kernels.cpp:208-218) at the decode
-bar, relative L2 <= 1e-5; against the raw entry point, which runs the split-K
-MFMA decode, within relative L2 1e-6 with equal non-finite entries (both sum the
-same exact block products, grouped differently over K); repeatable bit for bit;
+bar, relative L2 <= 1e-5; against the split-K MFMA decode on raw weights within
+relative L2 1e-6 with equal non-finite entries (both sum the same exact block
+products, grouped differently over K); against the raw entry point bit for bit where
+it runs the row-range kernel too (3-4 tokens on 512-1024 groups: raw lanes load
+whole blocks and transpose them into the same A fragments), else within 1e-6;
+repeatable bit for bit;
 and with a zero workspace need reported by the C ABI.  Cases cover 1 to 4
 groups per workgroup, one to four K phases (single and double buffered), N not
 a multiple of 16 (a partial last group), an odd number of block pairs, fp32 and bf16
@@ -18,7 +21,7 @@ import numpy as np
 import pytest
 
 from helpers import (assert_bitexact, empty_f32, note, rel_l2, rows_decode, rows_decode_multi,
-                     rows_decode_swiglu,
+                     rows_decode_raw, rows_decode_swiglu,
                      to_dev, to_host)
 from llmengine_amd import capi
 from llmengine_amd import synthetic as S
@@ -68,7 +71,7 @@ def test_rows_decode_matches_oracle_and_split_k(dev, orc, M, N, K, bias):
     b32 = S.activations(N + 2, (N,), tag=S.TAG_BIAS) if bias else None
     dx, dw = to_dev(x, dev), to_dev(raw, dev)
     dt = tiled_dev(dw, N, K, dev)
-    y_t, y_t2, y_raw = (empty_f32((M, N), dev) for _ in range(3))
+    y_t, y_t2, y_raw, y_sk = (empty_f32((M, N), dev) for _ in range(4))
     if bias == "bf16":
         b16 = torch.from_numpy(b32).to(dev).to(torch.bfloat16)
         b32 = b16.float().cpu().numpy()  # the widened bias the oracle adds
@@ -80,10 +83,17 @@ def test_rows_decode_matches_oracle_and_split_k(dev, orc, M, N, K, bias):
         capi.linear_tiled(dx, dt, db, y_t, M, N, K)
         capi.linear_tiled(dx, dt, db, y_t2, M, N, K)
         capi.linear(dx, dw, db, y_raw, M, N, K)
+    # the split-K kernel on raw weights (forced launch shape), widened bias
+    capi.linear_ex(dx, dw, to_dev(b32, dev) if bias else None, y_sk, M, N, K, path=3,
+                   mt=4 if M <= 4 else 8, waves=8, kslice=16)
     torch.cuda.synchronize()
     assert torch.equal(y_t, y_t2)  # deterministic
     got = to_host(y_t)
-    close_to_raw(got, to_host(y_raw), "rows vs split-K")
+    close_to_raw(got, to_host(y_sk), "rows vs split-K")
+    if rows_decode_raw(M, N, K):
+        assert_bitexact(got, to_host(y_raw), "tiled vs raw row-range")
+    else:
+        close_to_raw(got, to_host(y_raw), "tiled rows vs raw")
     rows = np.array(sorted({0, 1, N // 2, N - 17, N - 1}))
     w_rows = np.ascontiguousarray(raw.reshape(N, -1)[rows]).reshape(-1)
     want = orc.linear(x, w_rows, b32[rows] if bias else None, M, rows.size, K)
@@ -120,6 +130,35 @@ def test_rows_decode_special_values(dev):
     close_to_raw(got, want, "special values")
 
 
+def test_rows_decode_raw_special_values(dev):
+    """Raw weights at 4 tokens on 512 groups (the raw entry point's row-range
+    decode): Inf, NaN and large activations give the tiled launch's bits, including
+    the non-finite entries, and the split-K kernel's within 1e-6."""
+    import torch
+    M, N, K = 4, 8192, 2048
+    assert rows_decode_raw(M, N, K)
+    raw = weight(93, N, K)
+    x = S.activations(94, (M, K))
+    x[0, 3] = 1.0e30
+    x[1, 5] = np.inf
+    x[2, 100] = -np.inf
+    x[3, 7] = np.nan
+    note("raw rows decode special values")
+    dx, dw = to_dev(x, dev), to_dev(raw, dev)
+    dt = tiled_dev(dw, N, K, dev)
+    y_raw, y_t, y_sk = (empty_f32((M, N), dev) for _ in range(3))
+    capi.linear(dx, dw, None, y_raw, M, N, K)
+    capi.linear_tiled(dx, dt, None, y_t, M, N, K)
+    capi.linear_ex(dx, dw, None, y_sk, M, N, K, path=3, mt=4, waves=8, kslice=16)
+    torch.cuda.synchronize()
+    got = to_host(y_raw)
+    assert np.isnan(got[3]).all()
+    assert not np.isfinite(got[[1, 2]]).any()
+    assert_bitexact(got, to_host(y_t), "raw vs tiled row-range")
+    close_to_raw(got, to_host(y_sk), "raw row-range vs split-K")
+    assert capi.workspace_size(capi.OP_LINEAR, M, [N], K, False) == (0, 0)
+
+
 @pytest.mark.parametrize("M,Ns,K", [(4, (4096, 4096, 4096), 4096), (8, (4096, 4096, 4096), 4096),
                                     (3, (4000, 4000, 4100), 2048), (7, (8192, 192), 3072),
                                     (4, (3000, 900), 2112)])
@@ -128,7 +167,9 @@ def test_rows_decode_multi_output(dev, orc, M, Ns, K):
     inside workgroups (250 + 250 + 257 groups over 3-group workgroups), two outputs,
     and 240 groups in one-group workgroups.  Each output against the oracle (sampled
     rows on the larger shapes), against the single tiled Linear within 1e-6, with
-    its own bias; repeatable bit for bit; no workspace."""
+    its own bias; repeatable bit for bit; no workspace; the raw multi-output launch
+    gives the same bits where it takes the row-range kernel too (3-4 tokens), else
+    within 1e-6."""
     import torch
     assert rows_decode_multi(M, Ns, K)
     note(f"rows decode multi M={M} Ns={Ns} K={K}")
@@ -143,10 +184,17 @@ def test_rows_decode_multi_output(dev, orc, M, Ns, K):
     ys2 = [empty_f32((M, n), dev) for n in Ns]
     capi.linear_multi_tiled(dx, dts, dbs, ys, Ns, M, K)
     capi.linear_multi_tiled(dx, dts, dbs, ys2, Ns, M, K)
+    yr = [empty_f32((M, n), dev) for n in Ns]
+    capi.linear_multi(dx, [to_dev(w, dev) for w in raws], dbs, yr, Ns, M, K)
     torch.cuda.synchronize()
+    raw_rows = rows_decode_raw(M, 16 * sum((n + 15) // 16 for n in Ns), K)
     for i, n in enumerate(Ns):
         assert torch.equal(ys[i], ys2[i]), i
         got = to_host(ys[i])
+        if raw_rows:
+            assert_bitexact(got, to_host(yr[i]), f"multi {i} tiled vs raw")
+        else:
+            close_to_raw(got, to_host(yr[i]), f"multi {i} tiled vs raw")
         single = empty_f32((M, n), dev)
         capi.linear_tiled(dx, dts[i], dbs[i], single, M, n, K)
         close_to_raw(got, to_host(single), f"multi {i} vs single")
