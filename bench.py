@@ -116,14 +116,15 @@ def decode_kernel_name(M, layout="raw", N=4096, K=4096):
         if K > 4096:
             return "gemv_rawk_kernel (FP32 GEMV, 4 rows per workgroup, lanes along K)"
         return "gemv_q8_0_kernel (FP32 GEMV)"
+    lay = "tiled weights" if layout == "tiled" else "raw weights"
     if layout == "tiled" and tiled_gemv_wins(M, N, K):
         return "gemv_tiled_kernel (FP32 GEMV, tiled weights)"
-    if layout == "tiled" and rows_decode_wins(M, N, K):
+    if rows_decode_wins(M, N, K) and (layout == "tiled" or (M in (3, 4) and (N + 15) // 16 >= 512)):
         return ("gemv_mfma_rows_kernel (MFMA decode without split K, exact bf16 activation "
-                "split, tiled weights)")
-    if layout == "tiled" and hybrid_decode_wins(M, N, K):
+                f"split, {lay})")
+    if hybrid_decode_wins(M, N, K):
         return ("gemv_mfma_hyb_kernel (hybrid MFMA decode: 4 row groups x 44-block K splits "
-                "per workgroup, exact bf16 activation split, tiled weights)")
+                f"per workgroup, exact bf16 activation split, {lay})")
     if M < 64:
         return ("gemv_q8_0_mfma_kernel (MFMA decode, exact bf16 activation split"
                 + (", tiled weights)" if layout == "tiled" else ")"))

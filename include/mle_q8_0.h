@@ -377,8 +377,8 @@ size_t mle_q8_0_bytes(int64_t numel);
  *             workgroup in {2,4,8} (16 rows each), t2 = K blocks per
  *             workgroup in {16, 32} (32 only for a token tile <= 8), t3 = 0,
  *             or t3 in 1..4 = a launch shape of the hybrid kernel (row groups x
- *             a short K split; tiled weights, token tile 4 or 8, t1 and t2
- *             then unused but valid).
+ *             a short K split; token tile 4 or 8, t1 and t2 then unused but
+ *             valid).
  * mle_q8_0_linear_tiled_ex: the same hook on kTiled weights (path 0 or 3).
  */
 int mle_q8_0_f16_decode(const uint16_t* bits, float* out, int64_t n,

@@ -179,7 +179,7 @@ def linear_ex(x, w, bias, y, M, N, K, path=0, mt=0, lpr=0, rw=0, waves=0, kslice
     path 1 (FP32 GEMV) takes mt, lpr, rw, or mt and rpw (the row-span kernel on
     raw weights, rpw rows per workgroup); path 2 (MFMA GEMM) takes splits, bm, bn;
     path 3 (MFMA decode) takes mt, waves, kslice and hyb (a hybrid-kernel launch
-    shape, tiled weights); zero = automatic.  tiled: W in 16-row tiles (path 0 or 3)."""
+    shape); zero = automatic.  tiled: W in 16-row tiles (path 0 or 3)."""
     if path == 3:
         t = (mt, waves or (4 if hyb else 0), kslice or (16 if hyb else 0), hyb)
     elif path == 2:

@@ -564,10 +564,10 @@ int linear_ex(const float* x, const uint8_t* w_q8_0, const float* bias, float* y
     } else if (path == 3) {
       tune.dec = mle::DecodeMfmaConfig{t0, t1, t2};
       tune.dec.hyb = t3;
-      if (t3 != 0 && (layout != mle::WeightLayout::kTiled || (t0 != 4 && t0 != 8)))
+      if (t3 != 0 && t0 != 4 && t0 != 8)
         return fail(MLE_INVALID_ARGUMENT,
-                    "hip sgemm_nt_q8_0_weight: a hybrid MFMA decode shape needs tiled weights "
-                    "and a token tile of 4 or 8");
+                    "hip sgemm_nt_q8_0_weight: a hybrid MFMA decode shape needs a token tile "
+                    "of 4 or 8");
       if (t3 < 0 || t3 > 4 || !mle::decode_mfma_config_valid(tune.dec))
         return fail(MLE_INVALID_ARGUMENT,
                     "hip sgemm_nt_q8_0_weight: invalid MFMA decode shape (mt " +

@@ -1103,7 +1103,13 @@ hipError_t launch_rows(const float* x, const LinearSegs& s, int M, int K, hipStr
 // by the last workgroup in split order: deterministic).  Wave (group lg, index
 // qw) multiplies pairs [qw WPP, (qw + 1) WPP) of the split for its group; the
 // WG waves of a group add their sums in LDS in wave order.
-template <int MT, int NG, int WG, int SPB, int RING>
+//
+// Raw weights (LAYOUT kRaw): lane (g, r16) loads blocks 4 u + g (u = 0, 1) of each
+// 8-block chunk of row r16 of its group as whole 34-byte blocks and transposes
+// them in registers into the same A fragments (the row-range kernel's raw path);
+// blocks meet the same accumulators in the same order, so raw and tiled launches
+// give the same bits.
+template <int MT, int NG, int WG, int SPB, int RING, int LAYOUT>
 __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_hyb_kernel(
     const float* __restrict__ x, const RowsArgs args, int M, int K,
     float* __restrict__ partials, uint32_t* __restrict__ counters) {
@@ -1177,31 +1183,63 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_hyb_kernel(
   //    blocks of a pair) and scale dwords (lane l: pair l/16 of the chunk, row
   //    l % 16) of this wave's group; pairs past the wave's share, the split or K,
   //    and groups past N, read zeros.
+  constexpr bool kTiled = LAYOUT == int(WeightLayout::kTiled);
   const uint8_t* qb = w + rg * KP * kTilePieceBytes;
   const uint8_t* sb = w + G * KP * kTilePieceBytes + rg * KP * kTileScaleBytes;
   const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qb, live_g ? (uint32_t)KP * kTilePieceBytes : 0u);
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, live_g ? (uint32_t)KP * kTileScaleBytes : 0u);
-  u32x4 tq[NCK][4];
-  uint32_t ts[NCK];
+  // Raw: one buffer over the group's rows (rows past N read as zero); a chunk's
+  // blocks start 8-block (272-byte) steps apart, so each lane's 4-byte alignment
+  // phase is fixed.
+  const uint32_t row_bytes = (uint32_t)KB * kBlockBytes;
+  const uint8_t* gbase = w + rg * kTileRows * (int64_t)row_bytes;
+  const int64_t grows = live_g ? min((int64_t)kTileRows, (int64_t)N - rg * kTileRows) : 0;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(gbase, (uint32_t)(grows * row_bytes));
+  const uint32_t lane_off =
+      (uint32_t)r16 * row_bytes + (uint32_t)(kb0 + 2 * qw * WPP + g) * kBlockBytes;
+  const uint32_t mis = (uint32_t)(((uintptr_t)gbase + lane_off) & 2u);
+  const uint32_t voff = lane_off + mis;
+  const uint32_t uoff = lane_off + (mis ? 0u : 32u);
+  u32x4 tq[kTiled ? NCK : 1][4];
+  uint32_t ts[kTiled ? NCK : 1];
+  RawBlock wr[kTiled ? 1 : NCK][2];
   auto pair_live = [&](int j) {  // pair j of this wave's share
     return j < WPP && qw * WPP + j < SPP && pp0 + qw * WPP + j < KP;
   };
   auto load_chunk = [&](int ck) {
+    if constexpr (kTiled) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int j = 4 * ck + u;
-      uint32_t off = pair_live(j)
-                         ? (uint32_t)(pp0 + qw * WPP + j) * kTilePieceBytes + (uint32_t)lane * 16
-                         : 0x80000000u;
-      asm volatile("" : "+v"(off));
-      tq[ck][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, kNonTemporal);
+      for (int u = 0; u < 4; ++u) {
+        const int j = 4 * ck + u;
+        uint32_t off = pair_live(j)
+                           ? (uint32_t)(pp0 + qw * WPP + j) * kTilePieceBytes + (uint32_t)lane * 16
+                           : 0x80000000u;
+        asm volatile("" : "+v"(off));
+        tq[ck][u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, kNonTemporal);
+      }
+      const int j = 4 * ck + g;
+      uint32_t soff = pair_live(j)
+                          ? (uint32_t)(pp0 + qw * WPP + j) * kTileScaleBytes + (uint32_t)r16 * 4
+                          : 0x80000000u;
+      asm volatile("" : "+v"(soff));
+      ts[ck] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff, 0, 0);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int jb = 8 * ck + 4 * u + g;  // block of this wave's share
+        const bool live = jb < 2 * WPP && 2 * qw * WPP + jb < SPB && kb0 + 2 * qw * WPP + jb < KB;
+        const uint32_t soff = (uint32_t)(8 * ck + 4 * u) * kBlockBytes;  // multiple of 4
+        uint32_t v8 = live ? voff + soff : 0x80000000u;
+        uint32_t v2 = live ? uoff + soff : 0x80000000u;
+        asm volatile("" : "+v"(v8), "+v"(v2));
+        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8, 0, 0);
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrs, v8 + 16, 0, 0);
+        wr[ck][u].v0 = u32x4_a4{v0.x, v0.y, v0.z, v0.w};
+        wr[ck][u].v1 = u32x4_a4{v1.x, v1.y, v1.z, v1.w};
+        wr[ck][u].u = __builtin_amdgcn_raw_buffer_load_b16(wrs, v2, 0, 0);
+        wr[ck][u].mis = mis;
+      }
     }
-    const int j = 4 * ck + g;
-    uint32_t soff = pair_live(j)
-                        ? (uint32_t)(pp0 + qw * WPP + j) * kTileScaleBytes + (uint32_t)r16 * 4
-                        : 0x80000000u;
-    asm volatile("" : "+v"(soff));
-    ts[ck] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff, 0, 0);
   };
 #pragma unroll
   for (int ck = 0; ck < RG; ++ck) load_chunk(ck);
@@ -1266,14 +1304,39 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_hyb_kernel(
 #pragma unroll
   for (int ck = 0; ck < NCK; ++ck) {
     const int kbw = 2 * (qw * WPP + 4 * ck);  // first B-area block of the chunk
-    scl[wave][2 * g][r16] = scale_to_f32_fast(ts[ck] & 0xffffu);
-    scl[wave][2 * g + 1][r16] = scale_to_f32_fast(ts[ck] >> 16);
+    if constexpr (kTiled) {
+      scl[wave][2 * g][r16] = scale_to_f32_fast(ts[ck] & 0xffffu);
+      scl[wave][2 * g + 1][r16] = scale_to_f32_fast(ts[ck] >> 16);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (4 * ck + u >= WPP) break;  // past the wave's share: nothing to add
-      const u32x4 q = tq[ck][u];
-      block_mma(2 * u, kbw + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
-      block_mma(2 * u + 1, kbw + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
+      for (int u = 0; u < 4; ++u) {
+        if (4 * ck + u >= WPP) break;  // past the wave's share: nothing to add
+        const u32x4 q = tq[ck][u];
+        block_mma(2 * u, kbw + 2 * u, quants_to_bf16(q.x, q.y), accs[0]);
+        block_mma(2 * u + 1, kbw + 2 * u + 1, quants_to_bf16(q.z, q.w), accs[1]);
+      }
+    } else {
+      // Realign, scales to (wave-private) LDS, in-register transpose into A
+      // fragments; blocks in K order into the even / odd accumulators.
+      Block blk[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        blk[u] = finish_block(wr[ck][u]);
+        scl[wave][4 * u + g][r16] = scale_to_f32_fast(blk[u].scale_bits);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = blk[u].q[i];
+        transpose_chunks(q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // past the wave's share: nothing to add (those B blocks are other waves')
+          if (8 * ck + 4 * u + j >= 2 * WPP) break;
+          block_mma(4 * u + j, kbw + 4 * u + j, quants_to_bf16(q[2 * j], q[2 * j + 1]),
+                    accs[j & 1]);
+        }
+      }
     }
     if (ck + RG < NCK) load_chunk(ck + RG);
   }
@@ -1407,15 +1470,19 @@ constexpr HybShape kHybShapes[] = {
 constexpr int kHybCount = sizeof(kHybShapes) / sizeof(kHybShapes[0]);
 
 template <int MT, int NG, int WG, int SPB, int RING>
-hipError_t launch_hyb_k(const float* x, const RowsArgs& a, int M, int K,
+hipError_t launch_hyb_k(const float* x, const RowsArgs& a, WeightLayout layout, int M, int K,
                         const SplitKWorkspace& ws, hipStream_t stream) {
   const unsigned groups = a.grp_end[a.count - 1];
   const int KB = K / kBlockElems;
   const dim3 grid((groups + NG - 1) / NG, (unsigned)((KB + SPB - 1) / SPB)), block(64 * WG * NG);
   if (grid.y > 1 && (ws.partials == nullptr || ws.counters == nullptr))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemv_mfma_hyb_kernel<MT, NG, WG, SPB, RING>), grid, block, 0, stream, x, a,
-                     M, K, ws.partials, ws.counters);
+  if (layout == WeightLayout::kTiled)
+    hipLaunchKernelGGL((gemv_mfma_hyb_kernel<MT, NG, WG, SPB, RING, int(WeightLayout::kTiled)>),
+                       grid, block, 0, stream, x, a, M, K, ws.partials, ws.counters);
+  else
+    hipLaunchKernelGGL((gemv_mfma_hyb_kernel<MT, NG, WG, SPB, RING, int(WeightLayout::kRaw)>),
+                       grid, block, 0, stream, x, a, M, K, ws.partials, ws.counters);
   return hipGetLastError();
 }
 
@@ -1424,10 +1491,10 @@ hipError_t launch_hyb(int hyb, const float* x, const LinearSegs& s, int M, int K
                       const SplitKWorkspace& ws, hipStream_t stream) {
   const RowsArgs a = rows_args(s);
   switch (hyb) {
-    case 1: return launch_hyb_k<MT, 4, 2, 44, 2>(x, a, M, K, ws, stream);
-    case 2: return launch_hyb_k<MT, 8, 1, 44, 3>(x, a, M, K, ws, stream);
-    case 3: return launch_hyb_k<MT, 16, 1, 22, 2>(x, a, M, K, ws, stream);
-    case 4: return launch_hyb_k<MT, 4, 4, 32, 1>(x, a, M, K, ws, stream);
+    case 1: return launch_hyb_k<MT, 4, 2, 44, 2>(x, a, s.layout, M, K, ws, stream);
+    case 2: return launch_hyb_k<MT, 8, 1, 44, 3>(x, a, s.layout, M, K, ws, stream);
+    case 3: return launch_hyb_k<MT, 16, 1, 22, 2>(x, a, s.layout, M, K, ws, stream);
+    case 4: return launch_hyb_k<MT, 4, 4, 32, 1>(x, a, s.layout, M, K, ws, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -1565,6 +1632,9 @@ DecodeMfmaConfig decode_mfma_pick(int M, int N, int K, WeightLayout layout) {
   // at 8 tokens (1.00-1.01x) or on 256 groups (o_proj at 4 tokens: 1.01x).
   const int64_t G = ((int64_t)N + kTileRows - 1) / kTileRows;
   if (K % 64 == 0 && K >= 2048 && K <= 4096 && c.mt == 4 && G >= 512 && G <= 1024) c.rows = 1;
+  // and the hybrid kernel where it runs on tiled weights (raw down 4096 x 11008,
+  // three interleaved runs: 0.96x at 4 tokens, 0.94x at 8; the tiled launch's bits).
+  if ((c.mt == 4 || c.mt == 8) && K >= 8192 && KB <= 8 * 44 && G <= 256) c.hyb = 1;
   return c;
 }
 
@@ -1603,11 +1673,12 @@ static bool rows_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
   return (G >= 512 && G <= 1024) || (c.mt == 4 && G >= 240 && G <= 256);
 }
 
-// The launches the hybrid kernel takes: 1-3 plain outputs on tiled weights, 4 or
-// 8 tokens.
+// The launches the hybrid kernel takes: 1-3 plain outputs on tiled or raw
+// weights, 4 or 8 tokens.
 static bool hyb_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
   return c.hyb > 0 && c.hyb < kHybCount && (c.mt == 4 || c.mt == 8) && s.count >= 1 &&
-         s.count <= 3 && s.mode == Epilogue::kPlain && s.layout == WeightLayout::kTiled;
+         s.count <= 3 && s.mode == Epilogue::kPlain &&
+         (s.layout == WeightLayout::kTiled || s.layout == WeightLayout::kRaw);
 }
 
 SplitKNeed decode_mfma_workspace_segs(const DecodeMfmaConfig& c, const LinearSegs& s, int K) {

@@ -45,7 +45,10 @@ def test_kernel_names_follow_the_path_choice():
     assert "mfma" in bench.decode_kernel_name(2, "tiled", 151936, 896)
     assert "gemv_mfma_hyb_kernel" in bench.decode_kernel_name(8, "tiled", 4096, 11008)
     assert "gemv_mfma_hyb_kernel" in bench.decode_kernel_name(4, "tiled", 4096, 11008)
-    assert "gemv_q8_0_mfma_kernel" in bench.decode_kernel_name(8, "raw", 4096, 11008)
+    assert "gemv_mfma_hyb_kernel" in bench.decode_kernel_name(8, "raw", 4096, 11008)
+    assert "gemv_mfma_rows_kernel" in bench.decode_kernel_name(4, "raw", 12288, 4096)
+    assert "gemv_q8_0_mfma_kernel" in bench.decode_kernel_name(8, "raw", 12288, 4096)
+    assert "gemv_q8_0_mfma_kernel" in bench.decode_kernel_name(4, "raw", 4096, 4096)
     assert "gemv_q8_0_mfma_kernel" in bench.decode_kernel_name(8, "tiled", 4096, 4096)
     assert "gemv_mfma_rows_kernel" in bench.decode_kernel_name(8, "tiled", 12288, 4096)
     assert "gemv_mfma_rows_kernel" in bench.decode_kernel_name(4, "tiled", 11008, 4096)

@@ -206,8 +206,8 @@ def test_linear_ex_rejects_bad_launch_shape():
     for t in [(3, 4, 16, 0), (4, 6, 16, 0), (4, 4, 8, 0), (16, 4, 32, 0)]:
         rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 3, *t, None)
         assert rc == 1 and "MFMA decode shape" in capi.last_error(), t
-    # hybrid MFMA decode shapes (t3 = 1..4): tiled weights and a 4- or 8-token tile only
-    for t in [(4, 4, 16, 1), (8, 4, 16, 4)]:
+    # hybrid MFMA decode shapes (t3 = 1..4): a 4- or 8-token tile only
+    for t in [(2, 4, 16, 1), (16, 4, 16, 4)]:
         rc = lib.mle_q8_0_linear_ex(FAKE, FAKE, None, FAKE, 1, 64, 64, 3, *t, None)
         assert rc == 1 and "hybrid MFMA decode shape" in capi.last_error(), t
     fake16 = FAKE + 64 - FAKE % 64  # 16-byte aligned, never dereferenced

@@ -1,11 +1,14 @@
-"""GPU parity of the hybrid MFMA decode: tiled weights, 3-8 tokens, each workgroup
-owning a few 16-row groups and one short split of K (mle::decode_mfma_pick takes it
-for rows of 8192+ elements over at most 256 groups, the Llama down projection).
+"""GPU parity of the hybrid MFMA decode: tiled and raw weights, 3-8 tokens, each
+workgroup owning a few 16-row groups and one short split of K (mle::decode_mfma_pick
+takes it for rows of 8192+ elements over at most 256 groups, the Llama down
+projection).
 
 Checked against the CPU oracle (reference cpu_kernels.cpp:208-218) at the decode
 bar, relative L2 <= 1e-5; against the split-K MFMA decode on the raw bytes within
 relative L2 1e-6 with equal non-finite entries (both sum the same exact block
-products, grouped differently over K); repeatable bit for bit.  Every launch shape
+products, grouped differently over K); the same launch shape on the raw bytes bit
+for bit (raw lanes load whole blocks and transpose them into the same A fragments);
+repeatable bit for bit.  Every launch shape
 of the kernel (mle_q8_0_linear_tiled_ex, t3 = 1..4: 4 / 8 / 16 groups per
 workgroup, 1-4 waves per group, 22-44-block splits, 1-3 load chunks in flight) runs
 on ragged shapes: N not a multiple of 16 and fewer groups than a workgroup holds,
@@ -91,11 +94,14 @@ def test_hybrid_matches_oracle_and_split_k(dev, orc, hyb, M, N, K, bias):
         db = to_dev(b32, dev) if bias else None
     capi.linear_ex(dx, dt, db, y, M, N, K, path=3, mt=mt, hyb=hyb, tiled=True)
     capi.linear_ex(dx, dt, db, y2, M, N, K, path=3, mt=mt, hyb=hyb, tiled=True)
-    capi.linear(dx, dw, db, y_raw, M, N, K)
+    capi.linear_ex(dx, dw, db, y_raw, M, N, K, path=3, mt=mt, waves=4, kslice=16)
+    y_rh = empty_f32((M, N), dev)
+    capi.linear_ex(dx, dw, db, y_rh, M, N, K, path=3, mt=mt, hyb=hyb)
     torch.cuda.synchronize()
     assert torch.equal(y, y2)  # deterministic
     got = to_host(y)
     close_to_raw(got, to_host(y_raw), "hybrid vs split-K")
+    assert_bitexact(to_host(y_rh), got, "raw vs tiled hybrid")
     check_against_oracle(orc, x, raw, b32, got, M, N, K)
 
 
@@ -104,9 +110,10 @@ def test_hybrid_matches_oracle_and_split_k(dev, orc, hyb, M, N, K, bias):
 def test_hybrid_picked_by_tiled_linear(dev, orc, M, N, K, bias):
     """mle_q8_0_linear_tiled (and the bf16-bias entry point) on the shapes the
     picker gives the hybrid kernel: equal to the forced launch shape 1 bit for bit,
-    within 1e-6 of the split-K raw launch, at the decode bar against the oracle, and
-    with its split-K workspace (partials and one counter per workgroup column)
-    reported by the C ABI."""
+    and so is the raw entry point (the same kernel on the raw bytes); within 1e-6 of
+    the split-K raw launch, at the decode bar against the oracle, and with its split-K
+    workspace (partials and one counter per workgroup column) reported by the C ABI
+    for either layout."""
     import torch
     assert hybrid_decode(M, N, K)
     note(f"hybrid picked M={M} N={N} K={K} bias={bias}")
@@ -126,19 +133,24 @@ def test_hybrid_picked_by_tiled_linear(dev, orc, M, N, K, bias):
         capi.linear_tiled(dx, dt, db, y, M, N, K)
     capi.linear_ex(dx, dt, db, y_forced, M, N, K, path=3, mt=4 if M <= 4 else 8, hyb=1,
                    tiled=True)
-    capi.linear(dx, dw, db, y_raw, M, N, K)
+    capi.linear_ex(dx, dw, db, y_raw, M, N, K, path=3, mt=4 if M <= 4 else 8, waves=4,
+                   kslice=16)
+    y_auto_raw = empty_f32((M, N), dev)
+    capi.linear(dx, dw, db, y_auto_raw, M, N, K)
     torch.cuda.synchronize()
     got = to_host(y)
     assert_bitexact(got, to_host(y_forced), "picked vs forced shape 1")
+    assert_bitexact(to_host(y_auto_raw), got, "raw entry point vs tiled")
     close_to_raw(got, to_host(y_raw), "hybrid vs split-K")
     check_against_oracle(orc, x, raw, b32, got, M, N, K)
     G = (N + 15) // 16
     tiles, splits, mt = (G + 3) // 4, (K // 32 + 43) // 44, 4 if M <= 4 else 8
-    b, c = capi.workspace_size(capi.OP_LINEAR, M, [N], K, True)
-    if splits > 1:
-        assert b >= tiles * splits * 4 * 16 * mt * 4 and c >= tiles * 32
-    else:
-        assert (b, c) == (0, 0)
+    for tiled in (True, False):
+        b, c = capi.workspace_size(capi.OP_LINEAR, M, [N], K, tiled)
+        if splits > 1:
+            assert b >= tiles * splits * 4 * 16 * mt * 4 and c >= tiles * 32
+        else:
+            assert (b, c) == (0, 0)
 
 
 @pytest.mark.parametrize("hyb", SHAPES)
@@ -158,14 +170,16 @@ def test_hybrid_special_values(dev, hyb):
     note(f"hybrid special values shape {hyb}")
     dx, dw = to_dev(x, dev), to_dev(raw, dev)
     dt = tiled_dev(dw, N, K, dev)
-    y_raw, y = empty_f32((M, N), dev), empty_f32((M, N), dev)
-    capi.linear(dx, dw, None, y_raw, M, N, K)
+    y_raw, y, y_rh = (empty_f32((M, N), dev) for _ in range(3))
+    capi.linear_ex(dx, dw, None, y_raw, M, N, K, path=3, mt=8, waves=4, kslice=16)
     capi.linear_ex(dx, dt, None, y, M, N, K, path=3, mt=8, hyb=hyb, tiled=True)
+    capi.linear_ex(dx, dw, None, y_rh, M, N, K, path=3, mt=8, hyb=hyb)
     got, want = to_host(y), to_host(y_raw)
     assert np.isnan(got[3]).all()
     assert (got[4] == 0).all()
     assert not np.isfinite(got[[1, 2, 6]]).any()
     close_to_raw(got, want, "special values")
+    assert_bitexact(to_host(y_rh), got, "raw vs tiled hybrid, special values")
 
 
 @pytest.mark.parametrize("M,Ns,K", [(8, (2000, 2096), 11008), (4, (1000, 24, 3056), 8192)])
