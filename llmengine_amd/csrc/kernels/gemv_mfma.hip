@@ -654,7 +654,8 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_0_mfma_kernel(
 // GPU's 256 CUs.
 int rows_groups_per_workgroup(int64_t G) { return (int)((G + 255) / 256); }
 
-// Row-range MFMA decode on tiled weights, without split K (3-8 tokens).  The
+// Row-range MFMA decode without split K (3-8 tokens; tiled weights, and raw
+// weights at 3-4 tokens and in the SwiGLU launches).  The
 // split-K kernel above needs a hand-off between the workgroups of a row tile
 // (partial stores, their completion, a counter, the read-back), about 3 us at
 // the end of every launch.  Here a workgroup owns whole rows instead: NG 16-row
@@ -1088,8 +1089,8 @@ hipError_t launch_rows(const float* x, const LinearSegs& s, int M, int K, hipStr
   return hipErrorInvalidValue;
 }
 
-// Row groups with a short K split ("hybrid" decode, tiled weights, 4 or 8
-// tokens, plain outputs).  The split-K kernel above gives a workgroup 16 W rows
+// Row groups with a short K split ("hybrid" decode, tiled or raw weights, 4 or
+// 8 tokens, plain outputs).  The split-K kernel above gives a workgroup 16 W rows
 // x 16 blocks, so every output row's activations are read and split once per
 // row tile (64 times for down's 4096 rows) and 22 partial sums meet per output;
 // the row-range kernel reads and splits all of K once per workgroup.  Here a
@@ -1656,7 +1657,8 @@ SplitKNeed decode_mfma_workspace(const DecodeMfmaConfig& c, int N, int K) {
   return decode_mfma_workspace_segs(c, single(nullptr, nullptr, nullptr, N), K);
 }
 
-// The launches the row-range kernel takes: 1-3 plain outputs on tiled weights.
+// The launches the row-range kernel takes: 1-3 plain outputs (tiled weights; raw
+// weights at 4 tokens on 512-1024 groups) and the gate/up SwiGLU pair.
 static bool rows_takes(const DecodeMfmaConfig& c, const LinearSegs& s) {
   if (c.rows != 1 || s.count < 1 || s.count > 3) return false;
   if (s.mode == Epilogue::kSwiGLU) {  // tiled or raw weights
