@@ -767,7 +767,7 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_rows_kernel(
   // Tiled: quant slots (lane l: rows l % 16, quants 8 (l/16) .. +7 of both
   // blocks of a pair) and scale dwords (lane l: pair l/16 of the chunk, row
   // l % 16) of this wave's group; a group past N reads zeros (empty buffer).
-  // Raw (SwiGLU launches): a chunk's 8 blocks as two load sets of whole 34-byte
+  // Raw (SwiGLU launches; plain ones at 4 tokens): a chunk's 8 blocks as two load sets of whole 34-byte
   // blocks, lane (g, r16) taking block 4u + g of the chunk in row r16 of the
   // group, as the split-K kernel's raw path (rows past N and blocks past K read
   // as zeros).  A wave's chunks start 8-block (272-byte) steps apart, so each
