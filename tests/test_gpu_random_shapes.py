@@ -153,3 +153,35 @@ def test_random_fused_shapes(dev, orc, i, M, Ns, K):
     assert rel_l2(got_r[:, rows], want) <= bar, "swiglu raw"
     assert rel_l2(got_t[:, rows], want) <= bar, "swiglu tiled"
     assert rel_l2(got_t, got_r) <= (1e-2 if M >= 64 else 1e-6), "swiglu tiled vs raw"
+
+
+def _matmul_cases(n=14, seed=1203):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        M = int(rng.choice([1, 2, 5, 8, 9, 17, 40, 63, 64, 90, 200]))
+        N = 32 * int(rng.choice([int(rng.integers(1, 20)), int(rng.integers(20, 200))]))
+        K = 32 * int(rng.choice([int(rng.integers(1, 10)), int(rng.integers(10, 160))]))
+        out.append((i, M, N, K))  # K and N multiples of 32, as the reference requires
+    return out
+
+
+@pytest.mark.parametrize("i,M,N,K", _matmul_cases())
+def test_random_matmul_shapes(dev, orc, i, M, N, K):
+    """MatMul C = A . B (B [K, N] in blocks along N) over its three kernels (up to 8
+    rows of A, 9-63, the bf16 GEMM from 64) on random shapes against the oracle's
+    cpu::sgemm restatement (cpu_kernels.cpp:116-130): relative L2 1e-5 below 64 rows,
+    1e-2 on the GEMM; repeatable bit for bit."""
+    import torch
+    note(f"random matmul #{i}: M={M} N={N} K={K}")
+    b = S.q8_0_weight(1300 + i, K, N)[0]
+    a = S.activations(1400 + i, (M, K))
+    da, db = to_dev(a, dev), to_dev(b, dev)
+    c1, c2 = empty_f32((M, N), dev), empty_f32((M, N), dev)
+    capi.matmul(da, db, c1, M, N, K)
+    capi.matmul(da, db, c2, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2)
+    got = to_host(c1)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, orc.sgemm(a, b, M, N, K)) <= (1e-2 if M >= 64 else 1e-5)
