@@ -1456,7 +1456,9 @@ __global__ __launch_bounds__(64 * WG * NG) void gemv_mfma_hyb_kernel(
 //   4: 4 groups x 4 waves, 32-block splits, 1 chunk: 64 x 11 workgroups.
 // Other measured shapes (kept out): 9-10 splits (288-320 workgroups, more than
 // fit at once) 15.8-16.7 / 20-20.7; 2 groups per workgroup (1024 workgroups)
-// 14.4 / 18.7; 16 waves over 4 groups 12.5 / 17.0.  On K = 4096 (o_proj, gate,
+// 14.4 / 18.7; 16 waves over 4 groups 12.5 / 17.0; 16 waves over 4 groups with
+// 88-block splits (4 splits, 256 workgroups, 157 KB of LDS at 8 tokens) 12.8 /
+// 14.1 with 2 chunks in flight, 14.0 / 15.6 with 3.  On K = 4096 (o_proj, gate,
 // qkv) every shape tried was slower than the kernels above.
 struct HybShape {
   int ng, wg, spb, ring;
