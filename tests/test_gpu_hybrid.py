@@ -187,7 +187,8 @@ def test_hybrid_multi_output(dev, orc, M, Ns, K):
     """A multi-output Linear on the hybrid decode: 125 + 131 groups (the segment
     boundary inside a 4-group workgroup) and three outputs of 63 + 2 + 191 groups.
     Each output against the oracle on sampled rows, against its single tiled Linear
-    within 1e-6, with its own bias; repeatable bit for bit."""
+    within 1e-6, with its own bias; repeatable bit for bit; the raw multi-output launch
+    (the same kernel on the raw bytes) gives the same bits."""
     import torch
     G = sum((n + 15) // 16 for n in Ns)
     assert hybrid_decode(M, 16 * G, K)
@@ -203,9 +204,12 @@ def test_hybrid_multi_output(dev, orc, M, Ns, K):
     ys2 = [empty_f32((M, n), dev) for n in Ns]
     capi.linear_multi_tiled(dx, dts, dbs, ys, Ns, M, K)
     capi.linear_multi_tiled(dx, dts, dbs, ys2, Ns, M, K)
+    yr = [empty_f32((M, n), dev) for n in Ns]
+    capi.linear_multi(dx, [to_dev(w, dev) for w in raws], dbs, yr, Ns, M, K)
     torch.cuda.synchronize()
     for i, n in enumerate(Ns):
         assert torch.equal(ys[i], ys2[i]), i
+        assert torch.equal(ys[i], yr[i]), ("raw vs tiled", i)
         got = to_host(ys[i])
         single = empty_f32((M, n), dev)
         capi.linear_tiled(dx, dts[i], dbs[i], single, M, n, K)
