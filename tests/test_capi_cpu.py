@@ -371,15 +371,16 @@ def test_workspace_size_matches_launch_plan():
     ws = capi.workspace_size
     assert ws(capi.OP_LINEAR, 1, [4096], 4096) == (0, 0)              # FP32 GEMV
     assert ws(capi.OP_LINEAR, 1, [4096], 4096, tiled=True) == (0, 0)  # tiled GEMV
-    b, c = ws(capi.OP_LINEAR, 8, [4096], 11008)                       # MFMA decode, 22 splits
-    # every row x 22 K slices x 8 tokens of partial floats; 32 counters per row tile
+    b, c = ws(capi.OP_LINEAR, 16, [4096], 11008)                      # MFMA decode, 22 splits
+    # every row x 22 K slices x 16 tokens of partial floats; 32 counters per row tile
     # (4-wave tiles of 64 rows; o_proj's 4096-element rows take 8-wave tiles of 128
     # rows when tiled)
-    assert b == 4096 * 22 * 8 * 4 and c == (4096 // 64) * 32
-    # tiled, the hybrid decode: every row x 8 splits of 44 blocks x 8 tokens, one
-    # counter line per 4-group (64-row) workgroup column
-    assert ws(capi.OP_LINEAR, 8, [4096], 11008, tiled=True) == (4096 * 8 * 8 * 4,
-                                                                (4096 // 64) * 32)
+    assert b == 4096 * 22 * 16 * 4 and c == (4096 // 64) * 32
+    # 6-8 tokens, raw or tiled, the hybrid decode: every row x 8 splits of 44 blocks x
+    # 8 tokens, one counter line per 4-group (64-row) workgroup column
+    for tiled in (False, True):
+        assert ws(capi.OP_LINEAR, 8, [4096], 11008, tiled=tiled) == (4096 * 8 * 8 * 4,
+                                                                     (4096 // 64) * 32)
     bo, co = ws(capi.OP_LINEAR, 8, [4096], 4096, tiled=True)         # o_proj: 8 splits
     assert bo == 4096 * 8 * 8 * 4 and co == (4096 // 128) * 32
     bg, cg = ws(capi.OP_LINEAR, 512, [11008], 4096)                   # prefill GEMM
