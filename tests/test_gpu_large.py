@@ -9,6 +9,14 @@ the bf16 MFMA GEMM.  Outputs start as NaN and every element must be written.  Sa
 rows, including the last ones, are checked against the CPU oracle (reference
 cpu_kernels.cpp:208-218) at the path's bar: relative L2 1e-5 below 64 tokens, 1e-2 on
 the GEMM.  The tiled launch is checked against the raw one over all outputs.  The
+first 1 000 000 rows of the same bytes, read as a MatMul B [K = 1 000 000, N = 4096]
+(blocks along N), are multiplied at 1, 8 and 64 rows of A and checked on two whole
+column blocks (the first and the last).  Over a million-term K sum the reference's own
+sequential fp32 chain (cpu_kernels.cpp:116-130) strays from the exact sum by ~1e-5
+relative L2 (its error grows as the square root of K), so the bar is taken against the
+exact product instead: float64 sums of the reference's element values d * q (the
+oracle's dequantisation), relative L2 1e-5, with the oracle's restatement held to 1e-4
+of the same exact product (B past 2 GiB keeps the FP32 MatMul kernel at every M).  The
 Embedding gathers the first and last rows and out-of-range ids, from both layouts, bit
 for bit against the oracle (cpu_kernels.cpp:286-295; ids outside the table give zero
 rows, as the reference device kernel does, cuda_kernels.cu:399-427).
@@ -115,3 +123,30 @@ def test_embedding_table_past_4gib(dev, orc, big_weight):
     capi.embedding_tiled(t, dids, out, n, N_BIG, K_BIG)
     torch.cuda.synchronize()
     assert_bitexact(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("M", [1, 8, 64])
+def test_matmul_b_past_4gib(dev, orc, big_weight, M):
+    import torch
+    w, _ = big_weight
+    K, N = 1_000_000, K_BIG
+    b = w[:K * ROW_BYTES]  # B [K, N] row-major, blocks along N: the weight's first K rows
+    note(f"large weight MatMul: M={M} N={N} K={K}")
+    a = S.activations(4300 + M, (M, K))
+    da = torch.from_numpy(a).to(dev)
+    c = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    capi.matmul(da, b, c, M, N, K)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(c).all())
+    blocks = torch.tensor([0, N // 32 - 1], device=dev)
+    b_sub = b.view(K, N // 32, 34).index_select(1, blocks).cpu().numpy().reshape(-1)
+    exact = a.astype(np.float64) @ orc.dequantize_q8_0(b_sub, K * 64).reshape(K, 64).astype(
+        np.float64)
+    got = torch.cat([c[:, :32], c[:, N - 32:]], dim=1).cpu().numpy().astype(np.float64)
+    err = np.linalg.norm(got - exact) / np.linalg.norm(exact)
+    assert err <= 1e-5, err
+    ref = orc.sgemm(a, b_sub, M, 64, K).astype(np.float64)
+    ref_err = np.linalg.norm(ref - exact) / np.linalg.norm(exact)
+    note(f"large MatMul M={M}: relative L2 to the exact product {err:.2e} (reference chain "
+         f"{ref_err:.2e})")
+    assert ref_err <= 1e-4, ref_err
