@@ -643,13 +643,9 @@ void launch_tile(const GemmGrid& g, Epilogue mode, WeightLayout layout, const u3
                  hipStream_t stream) {
   if (layout == WeightLayout::kTiled)
     launch_tile_l<MI, NJ, int(WeightLayout::kTiled)>(g, mode, xf, xf_bytes, M, K, ws, stream);
-  else if (layout == WeightLayout::kKN) {
-    // MatMul tiles are 128 rows high: its producer ring (two raw blocks per
-    // item and step) does not fit the register budget of the 12-wave 256-row
-    // tiles without spilling.
-    if constexpr (MI == 1)
-      launch_tile_l<MI, NJ, int(WeightLayout::kKN)>(g, mode, xf, xf_bytes, M, K, ws, stream);
-  } else
+  else if (layout == WeightLayout::kKN)
+    launch_tile_l<MI, NJ, int(WeightLayout::kKN)>(g, mode, xf, xf_bytes, M, K, ws, stream);
+  else
     launch_tile_l<MI, NJ, int(WeightLayout::kRaw)>(g, mode, xf, xf_bytes, M, K, ws, stream);
 }
 
@@ -686,7 +682,7 @@ GemmConfig gemm_mfma_pick_segs(int M, const LinearSegs& s, int K) {
   GemmConfig best{128, 64, 1};
   double best_us = 1e300;
   for (const Shape& sh : shapes) {
-    if (sh.bm == 256 && (M <= 128 || s.layout == WeightLayout::kKN)) continue;
+    if (sh.bm == 256 && (M <= 128 || s.layout == WeightLayout::kKN)) continue;  // KN: below
     const int cols = swi ? sh.bn / 2 : sh.bn;
     int64_t col_tiles = 0, out_cols = 0;
     for (int i = 0; i < count; ++i) {
@@ -706,6 +702,24 @@ GemmConfig gemm_mfma_pick_segs(int M, const LinearSegs& s, int K) {
         best = GemmConfig{sh.bm, sh.bn, splits};
       }
     }
+  }
+  // MatMul (B [K, N]): in the 12-wave 256-row tiles the producer ring (two raw
+  // blocks per item and step) spills ~20 registers, and a K step costs about
+  // twice a 128-row tile's, so those tiles pay only where they put the whole
+  // grid in one round of workgroups and no 128-row tile does (512 rows of A with
+  // 8192 < N <= 12288).  Measured on MI355X, rotated B copies, three
+  // interleaved runs: 512 x 11008 x 4096 77-78 us vs 116 us on 128 x 96 tiles;
+  // where 128-row tiles fit one round or neither fits, the 128-row pick stays
+  // faster (512 x 4096 x 4096: 46-47 vs 49-50 us on 256 x 64 tiles with two K
+  // splits; 2048 x 4096 x 4096: 127-128 vs 142-143 on 256 x 96).
+  if (s.layout == WeightLayout::kKN && M > 256) {
+    const int64_t N = s.seg[0].N;
+    auto one_round = [&](int bm, int bn) {
+      return (N + bn - 1) / bn * ((M + bm - 1) / bm) <= 256;
+    };
+    if (!one_round(128, 128) && !one_round(128, 96) && !one_round(128, 64) &&
+        one_round(256, 96))
+      return GemmConfig{256, 96, 1};
   }
   return best;
 }
@@ -760,7 +774,7 @@ hipError_t launch_gemm_mfma_segs(const GemmConfig& c, const float* x, const Line
     return hipErrorInvalidValue;
   for (int i = 0; i < s.count; ++i)
     if (s.seg[i].N <= 0 || s.seg[i].w == nullptr) return hipErrorInvalidValue;
-  if (s.layout == WeightLayout::kKN && (c.bm != 128 || !gemm_mfma_kn_fits(s, K)))
+  if (s.layout == WeightLayout::kKN && !gemm_mfma_kn_fits(s, K))
     return hipErrorInvalidValue;
   const GemmGrid g = gemm_grid(c, M, s, K);
   if (g.splits > 1 && (ws.partials == nullptr || ws.counters == nullptr))

@@ -737,8 +737,11 @@ def test_matmul_b_at_two_byte_offset(dev, M, N, K):
 
 # (M, N, K) of the MatMul on the bf16 MFMA GEMM (M >= 64): the configs[2]-sized square
 # shape, ragged M / N tiles with an odd number of K blocks (the last K step half empty),
-# the smallest GEMM shape, and a long K with split-K partials.
-MATMUL_GEMM_CASES = [(512, 4096, 4096), (77, 1056, 1312), (64, 32, 32), (130, 384, 11008)]
+# the smallest GEMM shape, a long K with split-K partials, and two shapes on 256-row
+# tiles (taken where they fit the grid in one round and 128-row tiles do not), one with
+# a ragged second row tile and an odd number of K blocks.
+MATMUL_GEMM_CASES = [(512, 4096, 4096), (77, 1056, 1312), (64, 32, 32), (130, 384, 11008),
+                     (512, 11008, 512), (300, 11264, 352)]
 
 
 @pytest.mark.parametrize("M,N,K", MATMUL_GEMM_CASES)
