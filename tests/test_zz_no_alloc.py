@@ -33,7 +33,7 @@ def _operands(dev, seed, M, N, K, bias):
 
 
 @pytest.mark.parametrize("first,second", [
-    ((8, 4096, 11008, False), (4, 1024, 4096, True)),      # split-K decode: 22 then 8 splits
+    ((8, 4096, 11008, False), (4, 1024, 4096, True)),      # hybrid, then split-K: 8 splits each
     ((512, 4096, 11008, False), (96, 512, 2048, True)),    # prefill GEMM: 28 MB of scratch
     ((16, 2048, 8192, True), (5, 1024, 4096, False)),      # split-K decode, other tile/splits
 ])
@@ -71,9 +71,10 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(dev):
 
 
 def test_noalloc_back_to_back_split_k(dev):
-    """Three split-K decode calls of different shapes (22, 8 and 16 splits; different tile
-    counts) enqueued on one stream with no synchronisation between them: each resets
-    the counters it used before the next starts, and each matches mle_q8_0_linear."""
+    """Three MFMA decode calls with K splits, of different shapes (the hybrid decode's 8
+    splits of 44 blocks, then split-K with 8 and 16 splits; different tile counts),
+    enqueued on one stream with no synchronisation between them: each resets the
+    counters it used before the next starts, and each matches mle_q8_0_linear."""
     import torch
     shapes = [(8, 4096, 11008, False), (4, 1024, 4096, True), (16, 2048, 8192, False)]
     stream = torch.cuda.Stream()
