@@ -15,8 +15,8 @@ def dev_tensor(a):
 
 def main():
     dev = "cuda:0"
-    M, N, K = 8, 4096, 11008            # split-K decode (22 splits)
-    Mo, No, Ko = 4, 1024, 4096          # another split-K shape for the eager calls
+    M, N, K = 8, 4096, 11008            # hybrid decode (8 K splits through the scratch)
+    Mo, No, Ko = 4, 1024, 4096          # a split-K shape for the eager calls
     x = dev_tensor(S.activations(401, (M, K)))
     w = dev_tensor(S.q8_0_weight(402, N, K)[0])
     xo = dev_tensor(S.activations(403, (Mo, Ko)))
@@ -49,7 +49,7 @@ def main():
     torch.cuda.synchronize()
     assert torch.equal(y, want)
 
-    print("[child] capture a split-K no-allocation call", flush=True)
+    print("[child] capture a no-allocation call with K splits", flush=True)
     yg = torch.full((M, N), float("nan"), device=dev)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):

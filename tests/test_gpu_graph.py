@@ -5,7 +5,7 @@ with eager launches of other shapes after it, on the default stream while eager 
 of another shape run on the capturing stream at the same time (captured calls use the
 stream's graph workspace, which no eager call shares), and after a later eager call has
 outgrown the reservation -- gives the eager results bit for bit.  Shapes:
-the split-K MFMA decode (M = 8, 22 splits), the tiled FP32 GEMV (M = 1), the bf16 GEMM
+the split-K MFMA decode (M = 16, 22 splits), the tiled FP32 GEMV (M = 1), the bf16 GEMM
 with its X pre-pass (M = 96), the row-range MFMA decode (M = 4 on 512 tiled row
 groups, no workspace) and the hybrid MFMA decode (M = 8 on tiled rows of 11008
 elements, 8 splits through the workspace).  The kernels
@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 def test_linear_graph_replays_match_eager(dev, orc):
     import torch
-    shapes = [(8, 1024, 11008, False), (1, 512, 4096, True), (96, 384, 1024, False),
+    shapes = [(16, 1024, 11008, False), (1, 512, 4096, True), (96, 384, 1024, False),
               (4, 8192, 4096, True), (8, 1024, 11008, True)]
     assert rows_decode(4, 8192, 4096)  # the fourth shape takes the row-range kernel
     assert hybrid_decode(8, 1024, 11008)  # the last one the hybrid kernel

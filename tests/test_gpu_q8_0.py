@@ -11,8 +11,8 @@ import functools
 import numpy as np
 import pytest
 
-from helpers import (assert_bitexact, bits, empty_f32, note, rel_l2, sha, to_dev,
-                     to_host)
+from helpers import (assert_bitexact, bits, empty_f32, hybrid_decode, note, rel_l2, sha,
+                     to_dev, to_host)
 from llmengine_amd import capi
 from llmengine_amd import synthetic as S
 
@@ -533,18 +533,21 @@ def test_linear_decode_mfma_two_streams_concurrently(dev, orc):
 
 def test_linear_decode_mfma_split_k_after_poisoned_workspace(dev, orc):
     """The split-K hand-off reads only partials written by its own launch: before each
-    split-K launch, a launch of another shape on the same stream fills the same
-    workspace lines with NaN partials (NaN activations, 22 splits).  Every result of
-    the split-K shapes (8, 16 and 22 splits; raw and tiled weights) stays finite and
-    within 1e-5 relative L2 of the oracle."""
+    launch with K splits, a launch of another shape on the same stream fills the same
+    workspace lines with NaN partials (NaN activations, 16 tokens, 22 splits of the
+    split-K kernel: 5.8 MB of partials).  Every result of the split-K kernel (8 and 22
+    splits) and of the hybrid decode (8 splits of 44 blocks at 4 tokens, 6 at 8 tokens;
+    raw and tiled weights) stays finite and within 1e-5 relative L2 of the oracle."""
     import torch
-    Mp, Np, Kp = 8, 4096, 11008
+    Mp, Np, Kp = 16, 4096, 11008
     xp = np.full((Mp, Kp), np.nan, dtype=np.float32)
     dwp, dxp = to_dev(weight(130, Np, Kp), dev), to_dev(xp, dev)
     yp = empty_f32((Mp, Np), dev)
-    cases = [(8, 4096, 4096, False), (4, 4096, 11008, False), (8, 4096, 8192, True)]
+    cases = [(8, 4096, 4096, False), (16, 4096, 11008, False), (4, 4096, 11008, False),
+             (8, 4096, 8192, True)]
+    assert hybrid_decode(4, 4096, 11008) and hybrid_decode(8, 4096, 8192)
     for M, N, K, tiled in cases:
-        note(f"split-K after poisoned workspace M={M} N={N} K={K} tiled={tiled}")
+        note(f"K splits after poisoned workspace M={M} N={N} K={K} tiled={tiled}")
         w, x = weight(131 + K, N, K), acts(132 + M, M, K)
         want = orc.sgemm_nt(x, w, M, N, K)
         dw, dx = to_dev(w, dev), to_dev(x, dev)
@@ -566,14 +569,16 @@ def test_linear_decode_mfma_split_k_after_poisoned_workspace(dev, orc):
 
 def test_linear_threads_share_one_stream_while_workspace_grows(dev, orc):
     """Host threads launching on one (new) stream while its workspace grows: each
-    thread runs shapes of increasing workspace need (8 -> 22 splits, then the
-    prefill GEMM with its bf16 copy of X), so some calls free and reallocate the
-    buffers other threads just took.  The workspace table stays locked until a
-    launch is enqueued, so every result equals the oracle's (decode 1e-5, GEMM
-    1e-2) and the workspace ends at the largest need."""
+    thread runs shapes of increasing workspace need (split-K decode with 8 splits,
+    0.26 MB; with 22 splits at 16 tokens, 5.8 MB; the prefill GEMM with its bf16 copy
+    of X, 19.7 MB), starting from the 4 MB first allocation, so calls replace the
+    buffers other threads have just taken (the replaced ones stay allocated for the
+    launches already enqueued).  The workspace table stays locked until a launch is
+    enqueued, so every result equals the oracle's (decode 1e-5, GEMM 1e-2) and the
+    workspace ends at the largest need, after at least one replacement."""
     import threading
     import torch
-    shapes = [(8, 1024, 4096), (4, 1024, 11008), (96, 256, 2048)]
+    shapes = [(8, 1024, 4096), (16, 4096, 11008), (512, 1024, 11008)]
     data = []
     for i, (M, N, K) in enumerate(shapes):
         w, x = weight(140 + i, N, K), acts(141 + i, M, K)
@@ -593,6 +598,11 @@ def test_linear_threads_share_one_stream_while_workspace_grows(dev, orc):
             errors.append(e)
 
     torch.cuda.synchronize()  # inputs and outputs are in place before any launch
+    M0, N0, K0, dw0, dx0, _ = data[0]
+    capi.linear(dx0, dw0, None, empty_f32((M0, N0), dev), M0, N0, K0, stream=stream)
+    stream.synchronize()
+    gen0 = capi.workspace_info(stream)[2]  # the first (4 MB) allocation
+    assert gen0 >= 1
     note("threads share one stream while its workspace grows")
     threads = [threading.Thread(target=work, args=(t,)) for t in range(T)]
     for th in threads:
@@ -607,8 +617,9 @@ def test_linear_threads_share_one_stream_while_workspace_grows(dev, orc):
                 bar = MFMA_TOL if M >= 64 else GEMV_TOL
                 assert rel_l2(to_host(outs[t][r][i]), want) <= bar, (t, r, i)
     need = [capi.workspace_size(capi.OP_LINEAR, M, [N], K) for (M, N, K, *_r) in data]
-    b, c, _g = capi.workspace_info(stream)
+    b, c, g = capi.workspace_info(stream)
     assert b >= max(n[0] for n in need) and c >= max(n[1] for n in need)
+    assert g > gen0  # the larger shapes replaced the first buffer
 
 
 # ----------------------------------------------------------------------------- linear MFMA

@@ -5,10 +5,11 @@ library's static device array instead of the per-stream workspace.  Bar: the sam
 kernels run on the same operands, so outputs are bit-identical to mle_q8_0_linear (the
 Linear paths themselves are held to the oracle by the other GPU tests).  Each pair of
 calls runs twice in a row on the shared array, the second call with a smaller input, so
-stale partials or counters left by the first call would show; a chain of split-K calls of
+stale partials or counters left by the first call would show; a chain of calls with K splits of
 different shapes is also enqueued back to back with a single synchronisation at the end
 (calls ordered on one stream share the array safely).  A child process checks the
-array's first use under graph capture (refused) and a captured split-K call replayed
+array's first use under graph capture (refused) and a captured call with K splits (the
+hybrid decode) replayed
 between eager calls.
 """
 import os
@@ -83,7 +84,7 @@ def test_noalloc_back_to_back_split_k(dev):
         ops.append(_operands(dev, 300 + 10 * i, M, N, K, bias))
         outs.append(empty_f32((M, N), dev))
     torch.cuda.synchronize()
-    note("linear_noalloc: three split-K calls back to back on one stream")
+    note("linear_noalloc: three calls with K splits back to back on one stream")
     with torch.cuda.stream(stream):
         for (M, N, K, _b), (dx, dw, db), y in zip(shapes, ops, outs):
             capi.linear_noalloc(dx, dw, db, y, M, N, K, stream=stream)
@@ -99,7 +100,8 @@ def test_noalloc_back_to_back_split_k(dev):
 def test_noalloc_under_graph_capture_fresh_process():
     """In a fresh process (the library's per-device scratch not yet set up): the first
     no-allocation call, made under graph capture, is refused; after one eager call a
-    captured split-K call replays bit-identical to the eager result, with eager
+    captured call with K splits (the hybrid decode) replays bit-identical to the eager
+    result, with eager
     no-allocation calls of another shape on the same stream between the replays."""
     child = os.path.join(os.path.dirname(__file__), "noalloc_capture_child.py")
     note("linear_noalloc under graph capture (child process)")
