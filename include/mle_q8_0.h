@@ -18,7 +18,8 @@
  *     on its hot path reserves both beforehand (mle_q8_0_workspace_size +
  *     mle_workspace_reserve), and capture requires it; otherwise the eager one
  *     is allocated with hipMalloc on first need.  It only grows: a buffer too
- *     small for a call is replaced by one of max(need, 2 x capacity) bytes and
+ *     small for a call is replaced by one of max(need, 2 x capacity, 4 MiB) bytes
+ *     (counters: at least 4096) and
  *     the old one is kept (launches already enqueued, or captured in a HIP
  *     graph, still use it), so growth never synchronises; everything lives
  *     until process exit.  Nothing else is allocated.  Entry points are
